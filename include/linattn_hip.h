@@ -1,0 +1,309 @@
+/*
+ * linattn_hip.h -- C ABI of the MI355X (gfx950) sparse-attention hot path.
+ *
+ * This is the drop-in boundary that replaces the lazily imported Triton
+ * backend of tongxin/linattn (src/linattn/kernels/triton/) and the ctypes C
+ * decode (src/linattn/kernels/c_attention.py).  Every entry point:
+ *   - takes plain device pointers, element strides and sizes (no torch types),
+ *   - enqueues work on the given HIP stream and returns without a host sync,
+ *   - never allocates: scratch memory comes in through `workspace`, whose size
+ *     the matching *_workspace() call reports,
+ *   - returns 0 on success or a la_status code; la_last_error() then holds a
+ *     message for the calling thread.
+ * Inputs are never written.  Shapes are validated here as well as in the
+ * Python wrapper.
+ *
+ * Citations are path:line in the reference repository.
+ */
+#ifndef LINATTN_HIP_H
+#define LINATTN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LA_ABI_VERSION 1
+
+/* element types */
+enum {
+  LA_F32 = 0,
+  LA_BF16 = 1,
+  LA_F16 = 2,
+  LA_FP8_E4M3 = 3, /* OCP e4m3fn, bit-identical to torch.float8_e4m3fn */
+  LA_F64 = 4
+};
+
+/* status codes */
+enum {
+  LA_OK = 0,
+  LA_ERR_INVALID = 1,     /* bad shape / argument (Python raises ValueError) */
+  LA_ERR_UNSUPPORTED = 2, /* shape the kernels are not instantiated for */
+  LA_ERR_HIP = 3,         /* HIP runtime error (launch, attribute) */
+  LA_ERR_WORKSPACE = 4    /* workspace smaller than *_workspace() */
+};
+
+/* ABI version of the loaded library (LA_ABI_VERSION). */
+int la_abi_version(void);
+
+/* Message describing the last non-zero status returned on this thread. */
+const char *la_last_error(void);
+
+/*
+ * A view of a KV cache.  Two layouts:
+ *  - contiguous: k/v are (B, Hkv, T, D) with element strides k_sb/k_sh/k_st
+ *    (unit stride over D), as in the reference (block_sparse.py:40-57);
+ *  - paged: page_table != NULL.  k/v are pools of physical pages laid out
+ *    [phys_page][Hkv][page_size][D]; logical token t of sequence b lives in
+ *    physical page page_table[b * pt_stride + t / page_size] at row
+ *    t % page_size.  The reference has no page table; this layout is new.
+ * fp8 caches carry one fp32 scale per token and KV head (kv/quant.py:90-93
+ * with group_size == head_dim): contiguous scales are (B, Hkv, T) with
+ * strides s_sb/s_sh/s_st; paged scales are [phys_page][Hkv][page_size].
+ * kv_len (optional, int32 [B]) limits the valid tokens of each sequence.
+ */
+typedef struct {
+  const void *k;
+  const void *v;
+  const float *k_scale;
+  const float *v_scale;
+  const int32_t *page_table;
+  const int32_t *kv_len;
+  int64_t T;
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t s_sb, s_sh, s_st;
+  int64_t pt_stride;
+  int64_t page_size;
+  int32_t dtype; /* LA_F32, LA_BF16 or LA_FP8_E4M3 */
+  int32_t reserved;
+} la_kv;
+
+/*
+ * Exact attention over listed KV units (blocks, pages or tokens).
+ * Replaces block_sparse_attention / _block_sparse_fwd_kernel
+ * (kernels/triton/block_sparse.py:131-163, torch semantics :40-75) and the
+ * C paged decode (kernels/c/decode_attn.c:39-133, c_attention.py:76-111).
+ *
+ * ids: int32 [B][ids_heads][rows][N] with element strides id_sb/id_sh/id_st
+ *   (id_st = 0 broadcasts one list over all Tq queries, the reference's
+ *   (B, Hkv, N) form).  ids_heads == Hkv shares a list across a GQA group;
+ *   ids_heads == Hq gives every query head its own list.  Entry u selects
+ *   tokens [u*unit, (u+1)*unit); -1 entries are skipped.  A unit listed twice
+ *   is attended twice, as the reference's gather does (block_sparse.py:62-68).
+ * counts (optional, int32 [B][ids_heads][rows] contiguous) bounds the entries
+ *   read per list.
+ * Tokens >= kv length are masked (block_sparse.py:66-71); with causal != 0
+ *   token j is also masked for query t when j > offset + t.
+ * Scores use `scale` (the reference uses 1/sqrt(D)); softmax is fp32 online
+ * softmax; an empty row yields zeros (the reference divides by max(l,1e-12)).
+ * out: (B, Hq, Tq, D) with strides o_sb/o_sh/o_st in out_dtype (F32/BF16).
+ * Work is split over the list ("split-K"); num_splits = 0 picks a split count.
+ */
+typedef struct {
+  const void *q;
+  void *out;
+  const int32_t *ids;
+  const int32_t *counts;
+  void *workspace;
+  int64_t ws_bytes;
+  int64_t B, Hq, Hkv, Tq, D;
+  int64_t q_sb, q_sh, q_st;
+  int64_t o_sb, o_sh, o_st;
+  int64_t ids_heads, ids_rows, N;
+  int64_t id_sb, id_sh, id_st;
+  int64_t unit;
+  int64_t offset;
+  int64_t num_splits;
+  float scale;
+  int32_t q_dtype;
+  int32_t out_dtype;
+  int32_t causal;
+} la_sparse_attn_args;
+
+size_t la_sparse_attention_workspace(const la_sparse_attn_args *a, const la_kv *kv);
+int la_sparse_attention(const la_sparse_attn_args *a, const la_kv *kv, void *stream);
+
+/*
+ * Quest page metadata: channel-wise min / max of the keys of every page.
+ * Replaces page_bounds_torch / page_update_triton
+ * (kernels/triton/quest_pages.py:38-48, 84-100, 134-142) and
+ * QuestAttention._refresh_pages (variants/selection.py:181-201).
+ * Page p covers logical tokens [p*page_size, min(len,(p+1)*page_size)); pages
+ * with no valid token get min = +inf, max = -inf (quest_pages.py:44-46).
+ * page_min / page_max: [B][Hkv][n_pages][D] addressed by element strides
+ * m_sb/m_sh/m_sp/m_sd (any order; page-minor m_sp == 1 is what
+ * la_quest_scores reads fastest), stored in meta_dtype (the key dtype).
+ * Pages [first_page, n_pages) are written; first_page > 0 gives the
+ * incremental refresh after an append (selection.py:186-190).
+ */
+int la_quest_page_bounds(const la_kv *kv, int64_t B, int64_t Hkv, int64_t D, int64_t page_size,
+                         int64_t first_page, int64_t n_pages, void *page_min, void *page_max,
+                         int64_t m_sb, int64_t m_sh, int64_t m_sp, int64_t m_sd, int32_t meta_dtype,
+                         void *stream);
+
+/*
+ * Quest upper-bound page scores sum_d max(q_d*m_d, q_d*M_d)
+ * (quest_pages.py:51-55, selection.py:203-212), one score per query head:
+ * scores[((b*Hq + h)*Tq + t)*n_pages + p], fp64.  Products of fp32 or bf16
+ * values are exact in fp64 and are summed over d = 0..D-1 in order, so the
+ * score is a fixed function of the inputs and selection is reproducible.
+ * Masking (visibility, own page) is applied by la_topk_rows.
+ */
+int la_quest_scores(const void *q, int32_t q_dtype, int64_t B, int64_t Hq, int64_t Tq, int64_t D,
+                    int64_t q_sb, int64_t q_sh, int64_t q_st, const void *page_min,
+                    const void *page_max, int32_t meta_dtype, int64_t Hkv, int64_t n_pages,
+                    int64_t m_sb, int64_t m_sh, int64_t m_sp, int64_t m_sd, double *scores,
+                    void *stream);
+
+/*
+ * Row-wise top-k with ties broken by lowest index.
+ * Replaces topk_blocks (variants/selection.py:51-59), the torch.topk calls of
+ * page_select_torch / page_select_triton (quest_pages.py:76-77, 159-160),
+ * QuestAttention.page_selection (selection.py:214-237) and the selection of
+ * MInferenceAttention._block_sparse (selection.py:339-353).
+ *
+ * scores: fp64 rows (b, h, t) at scores[((b*H + h)*Tq + t)*row_stride + i],
+ *   i < n.  Row (b, h, t) considers i < n_valid[t] (all n when NULL).
+ * pos_unit > 0 derives both tables from positions instead: with
+ *   pos = pos_offset + t, n_valid = min(n, pos/pos_unit + 1) (units whose
+ *   start is <= pos: the Quest visibility rule, selection.py:219-223) and
+ *   own = min(pos/pos_unit, n-1) (selection.py:224); explicit tables win.
+ * force_own: unit own[t] ranks above everything, inside the k budget (the
+ *   Quest own-page rule, selection.py:224-231).
+ * k: per row, min(k, valid) entries are kept (entries the reference would
+ *   take from masked -inf scores are never read, selection.py:96-98).
+ * group G > 1: the G consecutive heads h = g*G..g*G+G-1 are unioned (Quest
+ *   gqa_union, selection.py:232-235).
+ * sink_units / window_units (C3 composition): units [0, sink_units) and
+ *   [own[t]-window_units+1, own[t]] are OR'd in after the top-k.
+ * Output per group (b, g, t): out_idx[((b*(H/G)+g)*Tq+t)*width + j],
+ *   -1 padded; order 0 sorts by (score desc, index asc) -- only for G == 1
+ *   and no sink/window -- order 1 sorts by ascending index.  out_val
+ *   (optional, order 0 only) gets the fp32 scores, -inf for padding;
+ *   out_count (optional) the number of valid entries.
+ */
+typedef struct {
+  const double *scores;
+  int32_t *out_idx;
+  float *out_val;
+  int32_t *out_count;
+  const int32_t *n_valid;
+  const int32_t *own;
+  void *workspace;
+  int64_t ws_bytes;
+  int64_t B, H, Tq, n, row_stride;
+  int64_t group, k, width;
+  int64_t sink_units, window_units;
+  int64_t pos_offset, pos_unit;
+  int32_t force_own;
+  int32_t order;
+} la_topk_args;
+
+size_t la_topk_rows_workspace(const la_topk_args *a);
+int la_topk_rows(const la_topk_args *a, void *stream);
+
+/*
+ * Lightning-indexer top-k (DSA): I[b,t,s] = sum_h w[b,t,h] * ReLU(q[b,t,h].k[b,s,h])
+ * and the k highest-scoring keys per query, ties to the lowest index.
+ * Replaces indexer_topk / indexer_topk_triton / indexer_topk_torch
+ * (kernels/triton/fused_indexer.py:52-73, 153-206).
+ * q_idx: (B, Tq, HI, d), k_idx: (B, Tk, HI, d) in F32 or BF16 with element
+ * strides (unit stride over d); w: fp32 (B, Tq, HI) with strides.
+ * Scores are computed in fp64: each q.k product is exact, summed over d in
+ * order, then ReLU, then sum over heads h = 0..HI-1 of fl(w_h * relu_h).
+ * causal != 0 keeps keys s <= offset + t only (an addition; the reference
+ * scores every key, fused_indexer.py:63-73).
+ * out_idx int32 (B, Tq, k) sorted by (score desc, index asc), -1 padded;
+ * out_val fp32 (B, Tq, k), -inf padded (optional).
+ * q_chunk bounds the queries scored per pass (workspace = q_chunk*Tk*8 bytes
+ * plus the top-k scratch); 0 picks one.
+ */
+typedef struct {
+  const void *q;
+  const void *kk;
+  const float *w;
+  int32_t *out_idx;
+  float *out_val;
+  void *workspace;
+  int64_t ws_bytes;
+  int64_t B, Tq, Tk, HI, d, k;
+  int64_t q_sb, q_st, q_sh;
+  int64_t k_sb, k_st, k_sh;
+  int64_t w_sb, w_st, w_sh;
+  int64_t offset;
+  int64_t q_chunk;
+  int32_t in_dtype;
+  int32_t causal;
+} la_indexer_args;
+
+size_t la_indexer_topk_workspace(const la_indexer_args *a);
+int la_indexer_topk(const la_indexer_args *a, void *stream);
+
+/*
+ * Block selection for block-sparse prefill (config C3 composition of
+ * MInferenceAttention._block_sparse, variants/selection.py:339-353, with
+ * block_reduce mean pooling, core.py:102-120): per (b, h, query block qb)
+ *   score(qb, kb) = mean_pool(q)[qb] . mean_pool(k)[kb]   (fp64, in order)
+ * over kb <= qb, top `topk` by (score desc, kb asc), OR the sink blocks
+ * [0, sink_blocks) and the window [qb-window_blocks+1, qb].
+ * q: (B, Hq, T, D), k: (B, Hkv, T, D), F32 or BF16, strides as above.
+ * Output out_idx (B, Hq, nqb, width) ascending, -1 padded; out_count (B,Hq,nqb).
+ * The positive 1/sqrt(D) factor of the reference does not change the ranking
+ * and is not applied.
+ */
+typedef struct {
+  const void *q;
+  const void *k;
+  int32_t *out_idx;
+  int32_t *out_count;
+  void *workspace;
+  int64_t ws_bytes;
+  int64_t B, Hq, Hkv, T, D;
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  int64_t block, topk, sink_blocks, window_blocks, width;
+  int32_t in_dtype;
+  int32_t reserved;
+} la_block_select_args;
+
+size_t la_block_select_workspace(const la_block_select_args *a);
+int la_block_select(const la_block_select_args *a, void *stream);
+
+/*
+ * Block-sparse causal prefill on the matrix cores (MFMA bf16, fp32 accumulate).
+ * The executor of block_sparse_attention (block_sparse.py:80-163) for lists
+ * shared by a whole query block: query block qb of head h attends the key
+ * blocks ids[b][h][qb][0..count) of block_size 64 tokens, with the causal mask
+ * j <= i applied in-kernel (the reference's selector applies it through the
+ * token mask, selection.py:86-108).  q (B,Hq,T,128), k/v (B,Hkv,T,128) bf16;
+ * out (B,Hq,T,128) in out_dtype (F32 or BF16).
+ */
+typedef struct {
+  const void *q;
+  const void *k;
+  const void *v;
+  void *out;
+  const int32_t *ids;
+  const int32_t *counts;
+  int64_t B, Hq, Hkv, T, D;
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  int64_t block, width;
+  float scale;
+  int32_t causal;
+  int32_t out_dtype;
+  int32_t reserved;
+} la_prefill_args;
+
+int la_block_sparse_prefill(const la_prefill_args *a, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LINATTN_HIP_H */

@@ -1,0 +1,127 @@
+// Shared device/host helpers for the gfx950 sparse-attention kernels.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "linattn_hip.h"
+
+namespace la {
+
+// ---------------------------------------------------------------- errors ----
+void set_error(const char *fmt, ...);
+int fail(int code, const char *fmt, ...);
+
+#define LA_REQUIRE(cond, ...)                               \
+  do {                                                      \
+    if (!(cond)) return ::la::fail(LA_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define LA_HIP(expr)                                                               \
+  do {                                                                             \
+    hipError_t _e = (expr);                                                        \
+    if (_e != hipSuccess)                                                          \
+      return ::la::fail(LA_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e)); \
+  } while (0)
+
+// Check the launch that was just enqueued.
+#define LA_LAUNCHED()                                                                \
+  do {                                                                               \
+    hipError_t _e = hipGetLastError();                                               \
+    if (_e != hipSuccess)                                                            \
+      return ::la::fail(LA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(_e)); \
+  } while (0)
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+inline int ilog2(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+
+// --------------------------------------------------------- element loads ----
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 bits (finite inputs; NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// OCP e4m3fn byte pair -> two fp32 (gfx950 v_cvt_pk_f32_fp8 decodes OCP e4m3).
+// HI selects bytes 2..3 of the word, otherwise bytes 0..1.
+template <bool HI>
+__device__ __forceinline__ float2 fp8x2_to_f32(uint32_t word) {
+  auto r = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, HI);
+  return make_float2(r[0], r[1]);
+}
+
+// Scalar load of one element of dtype `dt` as double (exact for f32/bf16/f16).
+__device__ __forceinline__ double load_as_f64(const void *base, int64_t idx, int dt) {
+  switch (dt) {
+    case LA_F32:
+      return (double)((const float *)base)[idx];
+    case LA_BF16:
+      return (double)bf16_bits_to_f32(((const uint16_t *)base)[idx]);
+    case LA_F16:
+      return (double)__half2float(((const __half *)base)[idx]);
+    case LA_F64:
+      return ((const double *)base)[idx];
+    default:
+      return 0.0;
+  }
+}
+__device__ __forceinline__ float load_as_f32(const void *base, int64_t idx, int dt) {
+  switch (dt) {
+    case LA_F32:
+      return ((const float *)base)[idx];
+    case LA_BF16:
+      return bf16_bits_to_f32(((const uint16_t *)base)[idx]);
+    case LA_F16:
+      return __half2float(((const __half *)base)[idx]);
+    case LA_F64:
+      return (float)((const double *)base)[idx];
+    default:
+      return 0.0f;
+  }
+}
+__device__ __forceinline__ void store_from_f32(void *base, int64_t idx, int dt, float x) {
+  if (dt == LA_BF16)
+    ((uint16_t *)base)[idx] = f32_to_bf16_bits(x);
+  else if (dt == LA_F16)
+    ((__half *)base)[idx] = __float2half(x);
+  else
+    ((float *)base)[idx] = x;
+}
+
+// -------------------------------------------------------- ordering keys ----
+// Monotone map fp64 -> uint64: a > b (as reals) <=> key(a) > key(b).  -0 and +0
+// map to the same key so that equal scores tie exactly.
+__device__ __forceinline__ uint64_t ord_key(double x) {
+  if (x == 0.0) x = 0.0;
+  uint64_t u = (uint64_t)__double_as_longlong(x);
+  return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
+__device__ __forceinline__ double key_to_double(uint64_t u) {
+  uint64_t b = (u >> 63) ? (u & 0x7fffffffffffffffull) : ~u;
+  return __longlong_as_double((long long)b);
+}
+constexpr uint64_t KEY_FORCED = 0xffffffffffffffffull;  // above every finite score
+
+// ------------------------------------------------------------ wave utils ----
+__device__ __forceinline__ float wave_xor_f32(float x, int m) { return __shfl_xor(x, m, 64); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace la

@@ -1,0 +1,381 @@
+// Row-wise top-k on gfx950: one workgroup (4 wave64) per row group.
+//
+// Selection is a radix select over a 64-bit order-preserving image of the fp64
+// scores (8 passes of 8 bits, MSB first, stopping as soon as the threshold
+// bucket is taken whole), followed by an index-ordered compaction in which
+// threshold ties are taken lowest index first.  The k survivors are then
+// either bitonic-sorted by (score desc, index asc) in LDS or OR'd into a
+// bitmap (GQA union, sink, window) and emitted in ascending index order.
+//
+// Replaces the torch.topk selections of topk_blocks (variants/selection.py:51-59),
+// QuestAttention.page_selection (selection.py:214-237), page_select_torch
+// (kernels/triton/quest_pages.py:58-78) and indexer_topk_torch
+// (kernels/triton/fused_indexer.py:63-73).  torch.topk leaves tie order
+// unspecified; here ties go to the lowest index.
+#include "topk.h"
+
+namespace la {
+
+constexpr int TK_NT = 256;
+constexpr int TK_NW = TK_NT / 64;
+
+struct TkShared {
+  uint32_t hist[256];
+  uint32_t wtmp[2][TK_NW];
+  uint32_t sel_bin, above, bin_cnt;
+};
+
+__device__ __forceinline__ uint64_t lanemask_lt(int lane) {
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Inclusive scan of one value per thread across the workgroup.
+__device__ __forceinline__ uint32_t tk_block_incl_scan(uint32_t v, uint32_t *wtmp, uint32_t &total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(v, off, 64);
+    if (lane >= off) v += y;
+  }
+  if (lane == 63) wtmp[w] = v;
+  __syncthreads();
+  uint32_t base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < TK_NW; ++i) {
+    const uint32_t x = wtmp[i];
+    base += (i < w) ? x : 0u;
+    tot += x;
+  }
+  __syncthreads();
+  total = tot;
+  return v + base;
+}
+
+struct RowKeys {
+  const double *row;
+  const uint64_t *lds;
+  int64_t own;
+  bool force;
+  __device__ __forceinline__ uint64_t operator()(int64_t i) const {
+    if (lds) return lds[i];
+    if (force && i == own) return KEY_FORCED;
+    return ord_key(row[i]);
+  }
+  // "x precedes y": higher key first, lower index on equal keys; -1 is last.
+  __device__ __forceinline__ bool before(int32_t x, int32_t y) const {
+    if (x < 0) return false;
+    if (y < 0) return true;
+    const uint64_t kx = (*this)(x), ky = (*this)(y);
+    return kx > ky || (kx == ky && x < y);
+  }
+};
+
+// Selects the top K of keys [0, n_v) and calls emit(index, position) for each,
+// positions 0..K-1 in increasing index order.  Collective over the workgroup.
+template <class Emit>
+__device__ void tk_select(const RowKeys &key, int64_t n_v, int64_t K, TkShared &sh, Emit emit) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (K <= 0) return;
+  uint64_t prefix = 0, mask = 0;
+  uint32_t need = (uint32_t)K;
+  bool all_in = true;
+  if (K < n_v) {
+    all_in = false;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+      sh.hist[tid] = 0;
+      __syncthreads();
+      for (int64_t i = tid; i < n_v; i += TK_NT) {
+        const uint64_t u = key(i);
+        if ((u & mask) == prefix) atomicAdd(&sh.hist[(u >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      const uint32_t c = sh.hist[255 - tid];
+      uint32_t tot;
+      const uint32_t incl = tk_block_incl_scan(c, sh.wtmp[0], tot);
+      if (incl >= need && incl - c < need) {
+        sh.sel_bin = 255 - tid;
+        sh.above = incl - c;
+        sh.bin_cnt = c;
+      }
+      __syncthreads();
+      need -= sh.above;
+      prefix |= (uint64_t)sh.sel_bin << shift;
+      mask |= 0xffull << shift;
+      const bool done = (sh.bin_cnt == need);
+      __syncthreads();
+      if (done) {
+        all_in = true;
+        break;
+      }
+    }
+  }
+  // Index-ordered compaction; wave w owns a contiguous index range.
+  const int64_t per = ((n_v + TK_NW - 1) / TK_NW + 63) / 64 * 64;
+  const int64_t beg = (int64_t)w * per;
+  const int64_t end = min(n_v, beg + per);
+  uint32_t c_gt = 0, c_eq = 0;
+  for (int64_t i = beg + lane; i < end; i += 64) {
+    const uint64_t um = key(i) & mask;
+    c_gt += um > prefix;
+    c_eq += um == prefix;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    c_gt += __shfl_xor(c_gt, off, 64);
+    c_eq += __shfl_xor(c_eq, off, 64);
+  }
+  if (lane == 0) {
+    sh.wtmp[0][w] = c_eq;
+    sh.wtmp[1][w] = c_gt;
+  }
+  __syncthreads();
+  uint32_t eq_acc = 0, eq_before = 0, sel_before = 0;
+#pragma unroll
+  for (int x = 0; x < TK_NW; ++x) {
+    const uint32_t e = sh.wtmp[0][x], g = sh.wtmp[1][x];
+    const uint32_t take_e = all_in ? e : min(e, need > eq_acc ? need - eq_acc : 0u);
+    if (x < w) sel_before += g + take_e;
+    if (x == w) eq_before = eq_acc;
+    eq_acc += e;
+  }
+  __syncthreads();
+  const uint64_t lt = lanemask_lt(lane);
+  uint32_t eq_seen = eq_before, pos = sel_before;
+  for (int64_t base = beg; base < end; base += 64) {
+    const int64_t i = base + lane;
+    const bool valid = i < end;
+    const uint64_t um = valid ? (key(i) & mask) : 0ull;
+    const bool is_gt = valid && um > prefix;
+    const bool is_eq = valid && um == prefix;
+    const uint64_t em = __ballot(is_eq);
+    const uint32_t rank = eq_seen + (uint32_t)__popcll(em & lt);
+    const bool take = is_gt || (is_eq && (all_in || rank < need));
+    const uint64_t tm = __ballot(take);
+    if (take) emit(i, pos + (uint32_t)__popcll(tm & lt));
+    eq_seen += (uint32_t)__popcll(em);
+    pos += (uint32_t)__popcll(tm);
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ TkShared sh;
+  const int64_t gi = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t tl = gi % p.Tq;
+  const int64_t t = tl + p.t_base;
+  const int64_t orow = (gi / p.Tq) * p.out_tq + t;
+  int64_t n_v = p.n;
+  int64_t own = -1;
+  if (p.pos_unit > 0) {
+    const int64_t pos = p.pos_off + t;
+    const int64_t u = pos >= 0 ? pos / p.pos_unit : -1;
+    n_v = min(p.n, u + 1);
+    own = min(u, p.n - 1);
+  }
+  if (p.n_valid_tab) n_v = min(p.n, (int64_t)p.n_valid_tab[t]);
+  if (p.own_tab) own = (int64_t)p.own_tab[t];
+  n_v = max(n_v, (int64_t)0);
+  const bool force = p.force_own && own >= 0 && own < n_v;
+  const int64_t K = min(p.k, n_v);
+
+  unsigned char *ptr = dyn;
+  uint64_t *lkeys = nullptr;
+  if (p.lds_keys) {
+    lkeys = (uint64_t *)ptr;
+    ptr += ((p.n * 8 + 15) / 16) * 16;
+  }
+  int32_t *sel = nullptr;
+  uint32_t *bm = nullptr;
+  if (p.use_bitmap) {
+    bm = (uint32_t *)ptr;
+    for (int64_t i = tid; i < p.bitmap_words; i += TK_NT) bm[i] = 0u;
+  } else {
+    sel = (int32_t *)ptr;
+  }
+  __syncthreads();
+
+  for (int64_t j = 0; j < p.G; ++j) {
+    const int64_t row = ((gi / p.Tq) * p.G + j) * p.Tq + tl;
+    const double *rp = p.scores + row * p.row_stride;
+    if (lkeys) {
+      for (int64_t i = tid; i < n_v; i += TK_NT)
+        lkeys[i] = (force && i == own) ? KEY_FORCED : ord_key(rp[i]);
+      __syncthreads();
+    }
+    const RowKeys key{rp, lkeys, own, force};
+    if (bm) {
+      tk_select(key, n_v, K, sh, [&](int64_t i, uint32_t) {
+        atomicOr(&bm[i >> 5], 1u << (i & 31));
+      });
+    } else {
+      tk_select(key, n_v, K, sh, [&](int64_t i, uint32_t pos) { sel[pos] = (int32_t)i; });
+      // bitonic sort of sel[0, p2k) by (key desc, index asc); padding is -1.
+      for (int64_t i = K + tid; i < p.p2k; i += TK_NT) sel[i] = -1;
+      __syncthreads();
+      for (int64_t size = 2; size <= p.p2k; size <<= 1) {
+        for (int64_t stride = size >> 1; stride > 0; stride >>= 1) {
+          for (int64_t i = tid; i < p.p2k; i += TK_NT) {
+            const int64_t l = i ^ stride;
+            if (l > i) {
+              const int32_t a = sel[i], b = sel[l];
+              const bool up = (i & size) == 0;
+              if (up ? key.before(b, a) : key.before(a, b)) {
+                sel[i] = b;
+                sel[l] = a;
+              }
+            }
+          }
+          __syncthreads();
+        }
+      }
+      int32_t *oi = p.out_idx + orow * p.width;
+      for (int64_t jj = tid; jj < p.width; jj += TK_NT) {
+        const int32_t s = jj < K ? sel[jj] : -1;
+        oi[jj] = s;
+        if (p.out_val) {
+          float v = __int_as_float(0xff800000);
+          if (s >= 0) v = (force && s == own) ? __int_as_float(0x7f800000) : (float)rp[s];
+          p.out_val[orow * p.width + jj] = v;
+        }
+      }
+      if (p.out_count && tid == 0) p.out_count[orow] = (int32_t)K;
+      __syncthreads();
+    }
+  }
+  if (!bm) return;
+
+  // Sink and window units, OR'd after the top-k.
+  if (n_v > 0) {
+    const int64_t s_end = min(p.sink, n_v);
+    for (int64_t i = tid; i < s_end; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    if (p.window > 0 && own >= 0) {
+      const int64_t w0 = max((int64_t)0, own - p.window + 1);
+      const int64_t w1 = min(own, n_v - 1);
+      for (int64_t i = w0 + tid; i <= w1; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    }
+  }
+  __syncthreads();
+  // Ascending emission: each thread owns a run of bitmap words.
+  const int64_t words = (n_v + 31) / 32;
+  const int64_t wpt = (words + TK_NT - 1) / TK_NT;
+  const int64_t w_beg = min(words, (int64_t)tid * wpt), w_end = min(words, w_beg + wpt);
+  uint32_t cnt = 0;
+  for (int64_t x = w_beg; x < w_end; ++x) cnt += __popc(bm[x]);
+  uint32_t total;
+  const uint32_t incl = tk_block_incl_scan(cnt, sh.wtmp[1], total);
+  uint32_t pos = incl - cnt;
+  int32_t *oi = p.out_idx + orow * p.width;
+  for (int64_t x = w_beg; x < w_end; ++x) {
+    uint32_t bits = bm[x];
+    while (bits) {
+      const int b = __ffs(bits) - 1;
+      if (pos < (uint32_t)p.width) oi[pos] = (int32_t)(x * 32 + b);
+      ++pos;
+      bits &= bits - 1;
+    }
+  }
+  for (int64_t jj = (int64_t)total + tid; jj < p.width; jj += TK_NT) oi[jj] = -1;
+  if (p.out_count && tid == 0) p.out_count[orow] = (int32_t)min((int64_t)total, p.width);
+}
+
+static int64_t align16(int64_t x) { return (x + 15) / 16 * 16; }
+
+int64_t topk_lds_bytes(const TopkKParams &p) {
+  int64_t b = 0;
+  if (p.lds_keys) b += align16(p.n * 8);
+  if (p.use_bitmap)
+    b += align16(p.bitmap_words * 4);
+  else
+    b += align16(p.p2k * 4);
+  return b;
+}
+
+static int max_dynamic_lds() {
+  static int cached = -1;
+  if (cached < 0) {
+    int dev = 0, v = 65536;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess) {
+      cached = v;
+    } else {
+      cached = 65536;
+    }
+  }
+  return cached;
+}
+
+int topk_launch(TopkKParams p, hipStream_t st) {
+  if (p.NG <= 0) return LA_OK;
+  p.use_bitmap = (p.G > 1 || p.sink > 0 || p.window > 0 || p.order == 1) ? 1 : 0;
+  p.bitmap_words = (p.n + 31) / 32;
+  int64_t p2 = 1;
+  while (p2 < p.k) p2 <<= 1;
+  p.p2k = p2;
+  const int64_t limit = (int64_t)max_dynamic_lds() - (int64_t)sizeof(TkShared) - 256;
+  p.lds_keys = 1;
+  int64_t bytes = topk_lds_bytes(p);
+  if (bytes > limit) {
+    p.lds_keys = 0;
+    bytes = topk_lds_bytes(p);
+  }
+  if (bytes > limit)
+    return fail(LA_ERR_UNSUPPORTED, "topk: k=%lld / n=%lld needs %lld B of LDS (limit %lld)",
+                (long long)p.k, (long long)p.n, (long long)bytes, (long long)limit);
+  if (bytes > 65536) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      LA_HIP(hipFuncSetAttribute((const void *)topk_rows_kernel,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)limit));
+      attr_set = true;
+    }
+  }
+  topk_rows_kernel<<<dim3((unsigned)p.NG), TK_NT, (size_t)bytes, st>>>(p);
+  LA_LAUNCHED();
+  return LA_OK;
+}
+
+}  // namespace la
+
+using namespace la;
+
+extern "C" size_t la_topk_rows_workspace(const la_topk_args *) { return 0; }
+
+extern "C" int la_topk_rows(const la_topk_args *a, void *stream) {
+  LA_REQUIRE(a && a->scores && a->out_idx, "la_topk_rows: null pointer");
+  LA_REQUIRE(a->B > 0 && a->H > 0 && a->Tq > 0 && a->n > 0, "la_topk_rows: bad shape");
+  LA_REQUIRE(a->row_stride >= a->n, "la_topk_rows: row_stride < n");
+  LA_REQUIRE(a->group >= 1 && a->H % a->group == 0, "la_topk_rows: H must be a multiple of group");
+  LA_REQUIRE(a->k >= 1 && a->width >= 1, "la_topk_rows: k and width must be >= 1");
+  LA_REQUIRE(a->order == 0 || a->order == 1, "la_topk_rows: order must be 0 or 1");
+  const bool bitmap = a->group > 1 || a->sink_units > 0 || a->window_units > 0 || a->order == 1;
+  LA_REQUIRE(!(bitmap && a->out_val), "la_topk_rows: values are only produced for order 0");
+  LA_REQUIRE(!(a->order == 0 && bitmap), "la_topk_rows: union/sink/window need order 1");
+  if (a->order == 0) LA_REQUIRE(a->width >= a->k, "la_topk_rows: width < k");
+  if (a->window_units > 0 || a->force_own)
+    LA_REQUIRE(a->own != nullptr || a->pos_unit > 0, "la_topk_rows: window/force_own need own[]");
+  TopkKParams p{};
+  p.scores = a->scores;
+  p.row_stride = a->row_stride;
+  p.G = a->group;
+  p.Tq = a->Tq;
+  p.NG = a->B * (a->H / a->group) * a->Tq;
+  p.t_base = 0;
+  p.out_tq = a->Tq;
+  p.n = a->n;
+  p.k = a->k;
+  p.width = a->width;
+  p.n_valid_tab = a->n_valid;
+  p.own_tab = a->own;
+  p.pos_off = a->pos_offset;
+  p.pos_unit = a->pos_unit;
+  p.sink = a->sink_units;
+  p.window = a->window_units;
+  p.force_own = a->force_own;
+  p.order = a->order;
+  p.out_idx = a->out_idx;
+  p.out_val = a->out_val;
+  p.out_count = a->out_count;
+  return topk_launch(p, (hipStream_t)stream);
+}

@@ -1,0 +1,186 @@
+"""Quest page metadata, page scores and page selection on gfx950.
+
+Mirrors kernels/triton/quest_pages.py:38-161 (``page_update_triton``,
+``page_select_triton``) and the selection of QuestAttention
+(variants/selection.py:139-248).  Differences by design:
+
+* scores are fp64 and a fixed function of the inputs (products exact, summed
+  over d in order), so page ids are reproducible bit for bit;
+* ties go to the lowest page index (torch.topk leaves the order unspecified);
+* the own page is forced per query row (selection.py:224-231), not with the
+  (T_q, T_q) block write of quest_pages.py:75 / :159 (defect for T_q > 1);
+* every KV head has its own metadata (the Triton kernels ignore the head
+  index, quest_pages.py:94-100, 124-130);
+* metadata is stored page-minor ([B][Hkv][D][P]) and returned as a
+  (B, Hkv, P, D) view, so the scoring kernel reads 4 pages per 8-byte load.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from linattn_amd import _native as N
+
+__all__ = [
+    "page_update_hip",
+    "page_scores_hip",
+    "page_select_hip",
+    "quest_select_hip",
+    "page_update_triton",
+    "page_select_triton",
+    "alloc_page_meta",
+]
+
+
+def alloc_page_meta(B: int, Hkv: int, n_pages: int, D: int, dtype: torch.dtype,
+                    device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Empty (mins, maxs) with page-minor storage, viewed as (B, Hkv, P, D)."""
+    p4 = (n_pages + 3) // 4 * 4
+    store = torch.empty(2, B, Hkv, D, p4, dtype=dtype, device=device)
+    return store[0, ..., :n_pages].transpose(-1, -2), store[1, ..., :n_pages].transpose(-1, -2)
+
+
+def page_update_hip(k: torch.Tensor, page_size: int, n_pages: Optional[int] = None, *,
+                    page_table: Optional[torch.Tensor] = None, pool_page_size: Optional[int] = None,
+                    kv_len: Optional[torch.Tensor] = None,
+                    out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+                    first_page: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Channel-wise key min/max per page (quest_pages.py:38-48, 134-142).
+
+    k: (B, Hkv, T, D) fp32/bf16, or a paged pool (n_phys, Hkv, pool_page, D)
+    with ``page_table`` (B, pages) int32.  Returns (mins, maxs), each
+    (B, Hkv, n_pages, D) in k's dtype; pages with no valid token hold +inf / -inf.
+    ``out`` + ``first_page`` refreshes pages [first_page, n_pages) in place (the
+    incremental update of selection.py:181-201)."""
+    dev = N.require_gpu(k, page_table, kv_len, what="page_update_hip")
+    from linattn_amd.kernels.block_sparse import _kv_struct
+
+    if page_table is not None:
+        B, Hkv, D = page_table.shape[0], k.shape[1], k.shape[3]
+        pps = int(pool_page_size or k.shape[2])
+        T = page_table.shape[1] * pps
+        kv = _kv_struct(k, k, page_table=page_table, page_size=pps, kv_len=kv_len, k_scale=None,
+                        v_scale=None, T=T, D=D, Hkv=Hkv)
+    else:
+        B, Hkv, T, D = k.shape
+        kv = _kv_struct(k, k, page_table=None, page_size=None, kv_len=kv_len, k_scale=None,
+                        v_scale=None, T=T, D=D, Hkv=Hkv)
+    if n_pages is None:
+        n_pages = (T + page_size - 1) // page_size
+    if out is None:
+        mins, maxs = alloc_page_meta(B, Hkv, n_pages, D, k.dtype, dev)
+    else:
+        mins, maxs = out
+        if mins.shape != (B, Hkv, n_pages, D) or maxs.shape != mins.shape:
+            raise ValueError("out must be two (B, Hkv, n_pages, D) tensors")
+        if mins.stride() != maxs.stride():
+            raise ValueError("mins and maxs must share strides")
+    sb, sh, sp, sd = mins.stride()
+    N.check(N.load().la_quest_page_bounds(ctypes.byref(kv), B, Hkv, D, page_size, first_page,
+                                          n_pages, mins.data_ptr(), maxs.data_ptr(), sb, sh, sp,
+                                          sd, N.dtype_code(mins.dtype), N.stream_handle(dev)),
+            "page_update_hip")
+    return mins, maxs
+
+
+def page_scores_hip(q: torch.Tensor, mins: torch.Tensor, maxs: torch.Tensor,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Upper-bound scores sum_d max(q_d m_d, q_d M_d), fp64 (B, Hq, Tq, P)
+    (quest_pages.py:51-55); query head h reads KV head h // (Hq/Hkv)."""
+    dev = N.require_gpu(q, mins, maxs, what="page_scores_hip")
+    B, Hq, Tq, D = q.shape
+    Hkv, P = mins.shape[1], mins.shape[2]
+    if mins.shape != (B, Hkv, P, D) or maxs.shape != mins.shape or mins.stride() != maxs.stride():
+        raise ValueError("mins/maxs must be (B, Hkv, P, D) with equal strides")
+    if mins.dtype != maxs.dtype:
+        raise ValueError("mins/maxs dtype mismatch")
+    if out is None:
+        out = torch.empty(B, Hq, Tq, P, dtype=torch.float64, device=dev)
+    elif out.shape != (B, Hq, Tq, P) or out.dtype != torch.float64 or not out.is_contiguous():
+        raise ValueError("out must be contiguous fp64 (B, Hq, Tq, P)")
+    qs = q.stride()
+    ms = mins.stride()
+    N.check(N.load().la_quest_scores(q.data_ptr(), N.dtype_code(q.dtype), B, Hq, Tq, D, qs[0], qs[1],
+                                     qs[2], mins.data_ptr(), maxs.data_ptr(),
+                                     N.dtype_code(mins.dtype), Hkv, P, ms[0], ms[1], ms[2], ms[3],
+                                     out.data_ptr(), N.stream_handle(dev)),
+            "page_scores_hip")
+    return out
+
+
+def _topk(scores: torch.Tensor, *, k: int, width: int, group: int, order: int,
+          pos_offset: int, pos_unit: int, force_own: bool, with_values: bool = False,
+          sink: int = 0, window: int = 0):
+    B, H, Tq, n = scores.shape
+    dev = scores.device
+    ids = torch.empty(B, H // group, Tq, width, dtype=torch.int32, device=dev)
+    counts = torch.empty(B, H // group, Tq, dtype=torch.int32, device=dev)
+    vals = torch.empty(B, H, Tq, width, dtype=torch.float32, device=dev) if with_values else None
+    a = N.LaTopkArgs()
+    a.scores, a.out_idx, a.out_count = scores.data_ptr(), ids.data_ptr(), counts.data_ptr()
+    a.out_val = N.ptr(vals)
+    a.B, a.H, a.Tq, a.n, a.row_stride = B, H, Tq, n, scores.stride(2)
+    a.group, a.k, a.width = group, k, width
+    a.sink_units, a.window_units = sink, window
+    a.pos_offset, a.pos_unit = pos_offset, pos_unit
+    a.force_own, a.order = int(force_own), order
+    N.check(N.load().la_topk_rows(ctypes.byref(a), N.stream_handle(dev)), "top-k")
+    return ids, counts, vals
+
+
+def quest_select_hip(q: torch.Tensor, mins: torch.Tensor, maxs: torch.Tensor, *, page_size: int,
+                     topk: int, offset: int = 0, gqa_union: bool = True
+                     ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """QuestAttention.page_selection (selection.py:214-237) as page lists.
+
+    Visible pages (start <= offset + t) are ranked; the query's own page is
+    forced inside the budget; k = max(1, min(topk, n_pages)).  With
+    ``gqa_union`` (the reference default) the G query heads of a KV head read
+    the union of their pages: ids (B, Hkv, Tq, G*k) ascending, -1 padded.
+    Otherwise each query head keeps its own list: ids (B, Hq, Tq, k) by
+    (score desc, index asc).  Also returns counts (valid entries per list)."""
+    scores = page_scores_hip(q, mins, maxs)
+    B, Hq, Tq, P = scores.shape
+    Hkv = mins.shape[1]
+    G = Hq // Hkv
+    k = max(1, min(int(topk), P))
+    if gqa_union and G > 1:
+        ids, counts, _ = _topk(scores, k=k, width=G * k, group=G, order=1, pos_offset=offset,
+                               pos_unit=page_size, force_own=True)
+    else:
+        ids, counts, _ = _topk(scores, k=k, width=k, group=1, order=0, pos_offset=offset,
+                               pos_unit=page_size, force_own=True)
+    return ids, counts
+
+
+def page_select_hip(q: torch.Tensor, mins: torch.Tensor, maxim: torch.Tensor, page_size: int,
+                    topk: int, *, offset: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Top-k page ids per query plus the page scores (quest_pages.py:58-78, 145-161).
+
+    Returns ids int32 (B, H, Tq, k) ordered by (score desc, index asc), -1 where
+    fewer than k pages are visible, and fp32 scores (B, H, Tq, P) with
+    invisible pages -inf and the own page +inf, as the reference does."""
+    scores = page_scores_hip(q, mins, maxim)
+    B, H, Tq, P = scores.shape
+    k = max(1, min(int(topk), P))
+    ids, _, _ = _topk(scores, k=k, width=k, group=1, order=0, pos_offset=offset,
+                      pos_unit=page_size, force_own=True)
+    pos = torch.arange(Tq, device=q.device) + offset
+    visible = (torch.arange(P, device=q.device) * page_size).unsqueeze(0) <= pos.unsqueeze(1)
+    out = scores.to(torch.float32).masked_fill(~visible, float("-inf"))
+    own = torch.clamp(pos // page_size, max=P - 1)
+    out.scatter_(-1, own.view(1, 1, Tq, 1).expand(B, H, Tq, 1), float("inf"))
+    return ids, out
+
+
+def page_update_triton(k: torch.Tensor, page_size: int, n_pages: int):
+    """Drop-in alias for kernels/triton/quest_pages.py:134 (runs the HIP kernel)."""
+    return page_update_hip(k, page_size, n_pages)
+
+
+def page_select_triton(q, mins, maxim, page_size: int, topk: int, *, offset: int = 0):
+    """Drop-in alias for kernels/triton/quest_pages.py:145 (runs the HIP kernels)."""
+    return page_select_hip(q, mins, maxim, page_size, topk, offset=offset)
