@@ -1,0 +1,238 @@
+"""Benchmark of the MI355X sparse-attention hot path (one GPU).
+
+Headline workload: paged Quest sparse decode, bf16 KV,
+batch 64, context 65536 per sequence in 64-token pages behind a randomly
+permuted page table, 32 query / 8 KV heads, head_dim 128, a 2048-token budget
+(32 pages per query head, the last page forced), GQA union of the group's
+pages (the reference default, variants/selection.py:232-235).
+
+A step = one decode step for all 64 sequences: Quest page scores, top-k page
+selection, split-K attention over the selected pages.  Inputs (query, KV pool,
+page table, page metadata) are resident in HBM before timing starts.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Prints one JSON line (see the driver contract in the repository docs).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
+
+C4 = dict(B=64, Hq=32, Hkv=8, T=65536, D=128, page=64, topk=32, seed=0)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=16, help="sequences timed on the CPU")
+    ap.add_argument("--shared", action="store_true",
+                    help="per-query-head page lists instead of the GQA union")
+    return ap.parse_args()
+
+
+def setup_c4(dev, cfg):
+    import torch
+
+    from linattn_amd.kernels.quest_pages import page_update_hip
+
+    B, Hq, Hkv, T, D, ps = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["T"], cfg["D"], cfg["page"]
+    P = T // ps
+    g = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    q = torch.randn(B, Hq, 1, D, generator=g, device=dev).to(torch.bfloat16)
+    pool_k = torch.empty(B * P, Hkv, ps, D, dtype=torch.bfloat16, device=dev)
+    pool_v = torch.empty_like(pool_k)
+    chunk = 4096
+    for i in range(0, B * P, chunk):  # bounded fp32 temporaries
+        pool_k[i:i + chunk] = torch.randn(min(chunk, B * P - i), Hkv, ps, D, generator=g, device=dev)
+    for i in range(0, B * P, chunk):
+        pool_v[i:i + chunk] = torch.randn(min(chunk, B * P - i), Hkv, ps, D, generator=g, device=dev)
+    pt = torch.randperm(B * P, generator=g, device=dev).view(B, P).to(torch.int32)
+    mins, maxs = page_update_hip(pool_k, ps, page_table=pt)
+    torch.cuda.synchronize()
+    return q, pool_k, pool_v, pt, mins, maxs
+
+
+def cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg, n_seq, union):
+    """Time the CPU oracle (oracle/, C + numpy, one thread) on the first n_seq
+    sequences of the same inputs: page scores, top-k, attention."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    B, Hkv, T, D, ps = cfg["B"], cfg["Hkv"], cfg["T"], cfg["D"], cfg["page"]
+    seqs = []
+    for b in range(n_seq):
+        kb = pool_k[pt[b].long()].permute(1, 0, 2, 3).reshape(1, Hkv, T, D).cpu()
+        vb = pool_v[pt[b].long()].permute(1, 0, 2, 3).reshape(1, Hkv, T, D).cpu()
+        seqs.append((q[b:b + 1].cpu(), kb, vb, mins[b:b + 1].cpu(), maxs[b:b + 1].cpu()))
+    oracle.lib()
+    t0 = time.perf_counter()
+    for qb, kb, vb, mb, xb in seqs:
+        ids = oracle.quest_select(qb, mb, xb, page_size=ps, topk=cfg["topk"], offset=T - 1,
+                                  gqa_union=union)
+        oracle.attend_lists(qb, kb, vb, ids, unit=ps, causal=True, offset=T - 1)
+    dt = time.perf_counter() - t0
+    return {"value": n_seq / dt, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{n_seq} of {B} sequences of config 4 (full step: page scores, top-k, "
+                      f"attention), {dt:.1f} s, CPU oracle (C, single thread)"}
+
+
+FP64_VALU_PEAK_TFLOPS = 78.6  # MI355X fp64 vector, AMD public spec
+
+
+def time_cuda(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def bench_c2(dev, steps, warmup):
+    """Config 2: fused indexer + causal top-2048, bf16, B=1, T=8192, 4x64 heads."""
+    import torch
+
+    from linattn_amd.kernels.fused_indexer import indexer_topk
+
+    T, HI, d, kk = 8192, 4, 64, 2048
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(1, T, HI, d, generator=g, device=dev).bfloat16()
+    k = torch.randn(1, T, HI, d, generator=g, device=dev).bfloat16()
+    w = torch.rand(1, T, HI, generator=g, device=dev)
+    ms = time_cuda(lambda: indexer_topk(q, k, w, kk, causal=True), steps, warmup)
+    pairs = T * (T + 1) // 2
+    flops = pairs * HI * d * 2  # exact fp64 q.k products
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "C2 indexer top-2048, causal, T=8192, 4x64 heads, bf16",
+            "queries_per_s": round(T / (ms * 1e-3), 1), "ms": round(ms, 4),
+            "score_tflops_fp64": round(tflops, 2),
+            "frac_fp64_valu_peak": round(tflops / FP64_VALU_PEAK_TFLOPS, 4)}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
+        return 2
+    import torch
+
+    from linattn_amd.kernels.block_sparse import sparse_attention
+    from linattn_amd.kernels.quest_pages import quest_select_hip
+
+    dev = torch.device("cuda:0")
+    cfg = dict(C4)
+    union = not args.shared
+    q, pool_k, pool_v, pt, mins, maxs = setup_c4(dev, cfg)
+    B, Hq, Hkv, T, D, ps = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["T"], cfg["D"], cfg["page"]
+    pos = T - 1
+    stream = torch.cuda.current_stream(dev)
+
+    def select():
+        return quest_select_hip(q, mins, maxs, page_size=ps, topk=cfg["topk"], offset=pos,
+                                gqa_union=union)
+
+    def attend(ids, counts):
+        return sparse_attention(q, pool_k, pool_v, ids, unit=ps, counts=counts, causal=True,
+                                offset=pos, page_table=pt, page_size=ps)
+
+    for _ in range(args.warmup):
+        ids, counts = select()
+        attend(ids, counts)
+    torch.cuda.synchronize()
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t_all0 = torch.cuda.Event(enable_timing=True)
+    t_all1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_all0.record(stream)
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        ids, counts = select()
+        ev[i][1].record(stream)
+        attend(ids, counts)
+        ev[i][2].record(stream)
+    t_all1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t_all0.elapsed_time(t_all1) / args.steps
+    ms_sel = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    ms_att = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+
+    # algorithmic bytes, from the actual selection
+    n_pages_read = int(counts.sum())  # distinct (b, list head, page) triples
+    lists_heads = ids.shape[1]
+    kv_row_bytes = D * 2 * 2  # K and V, bf16
+    att_bytes = n_pages_read * ps * kv_row_bytes
+    if lists_heads == Hq:  # per-query-head lists share KV heads; count distinct pages
+        sel = torch.zeros(B, Hkv, T // ps, dtype=torch.bool, device=dev)
+        g = Hq // Hkv
+        idl = ids.view(B, Hkv, g, -1).clamp(min=0).long().reshape(B, Hkv, -1)
+        sel.scatter_(-1, idl, True)
+        att_bytes = int(sel.sum()) * ps * kv_row_bytes
+    att_bytes += q.numel() * 2 + B * Hq * D * 2 + ids.numel() * 4
+    meta_bytes = 2 * mins.numel() * 2 + B * Hq * (T // ps) * 8 * 2  # min+max, scores w+r
+    step_bytes = att_bytes + meta_bytes
+    tok_s = B / (ms_step * 1e-3)
+    att_gbs = att_bytes / (ms_att * 1e-3) / 1e9
+    step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
+
+    result = {
+        "metric": "sparse decode tok/s (paged Quest, 64K ctx, batch 64)",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1), seeded; random page table",
+        "config": {"workload": "C4 paged Quest sparse decode", "batch": B, "context": T,
+                   "page_size": ps, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
+                   "budget_tokens": cfg["topk"] * ps, "gqa": "union" if union else "per-head"},
+        "roofline": {"bound": "hbm", "kernel": "sparse_attn_kernel (+ split combine)",
+                     "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": att_bytes, "ms_per_launch": round(ms_att, 4)},
+        "step": {"ms_select": round(ms_sel, 4), "ms_attend": round(ms_att, 4),
+                 "bytes": step_bytes, "GBps": round(step_gbs, 1),
+                 "frac_hbm": round(step_gbs / HBM_PEAK_GBS, 4),
+                 "pages_read_per_kv_list": round(n_pages_read / (B * lists_heads), 2)},
+    }
+    result["indexer"] = bench_c2(dev, max(3, args.steps // 4), 2)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg,
+                                              args.cpu_sample, union)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -122,6 +122,26 @@ constexpr uint64_t KEY_FORCED = 0xffffffffffffffffull;  // above every finite sc
 // ------------------------------------------------------------ wave utils ----
 __device__ __forceinline__ float wave_xor_f32(float x, int m) { return __shfl_xor(x, m, 64); }
 
+// DPP lane permutation within rows of 16 lanes (no LDS traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over aligned groups of N lanes; every lane of a group gets the same sum
+// (each step adds a value to its partner's, and fp addition is commutative).
+// quad_perm [1,0,3,2] and [2,3,0,1], then row_half_mirror and row_mirror.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_f32<0xB1>(x);
+  if constexpr (N >= 4) x += dpp_f32<0x4E>(x);
+  if constexpr (N >= 8) x += dpp_f32<0x141>(x);
+  if constexpr (N >= 16) x += dpp_f32<0x140>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace la

@@ -64,37 +64,51 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
 #pragma unroll
     for (int i = 0; i < PPT; ++i) acc[g][i] = 0.0;
   const int64_t mbase = b * m_sb + kvh * m_sh;
-  const bool full = (p0 + PPT <= n_pages);
-  for (int64_t d = 0; d < D; ++d) {
-    double lo[PPT], hi[PPT];
-    const int64_t o = mbase + d * m_sd + p0 * m_sp;
-    if (VEC && full) {
-      if (MT == LA_BF16) {
-        static_assert(PPT == 4, "vector path loads 4 pages");
-        const uint2 a = *(const uint2 *)((const uint16_t *)mn + o);
-        const uint2 c = *(const uint2 *)((const uint16_t *)mx + o);
-        lo[0] = bf16lo(a.x); lo[1] = bf16hi(a.x); lo[2] = bf16lo(a.y); lo[3] = bf16hi(a.y);
-        hi[0] = bf16lo(c.x); hi[1] = bf16hi(c.x); hi[2] = bf16lo(c.y); hi[3] = bf16hi(c.y);
-      } else {
-        const float4 a = *(const float4 *)((const float *)mn + o);
-        const float4 c = *(const float4 *)((const float *)mx + o);
-        lo[0] = a.x; lo[1] = a.y; lo[2] = a.z; lo[3] = a.w;
-        hi[0] = c.x; hi[1] = c.y; hi[2] = c.z; hi[3] = c.w;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < PPT; ++i) {
-        const bool ok = p0 + i < n_pages;
-        lo[i] = ok ? load_as_f64(mn, o + i * m_sp, MT) : 0.0;
-        hi[i] = ok ? load_as_f64(mx, o + i * m_sp, MT) : 0.0;
-      }
-    }
+  auto accumulate = [&](int64_t d, const double (&lo)[PPT], const double (&hi)[PPT]) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const double qv = qd[g * D + d];
       const bool pos = qv >= 0.0;
 #pragma unroll
       for (int i = 0; i < PPT; ++i) acc[g][i] = __builtin_fma(qv, pos ? hi[i] : lo[i], acc[g][i]);
+    }
+  };
+  if (VEC && p0 + PPT <= n_pages) {
+    static_assert(PPT == 4, "vector path loads 4 pages");
+    if constexpr (MT == LA_BF16) {
+      const uint16_t *pl = (const uint16_t *)mn + mbase + p0;
+      const uint16_t *ph = (const uint16_t *)mx + mbase + p0;
+#pragma unroll 2
+      for (int64_t d = 0; d < D; ++d) {
+        const uint2 a = *(const uint2 *)(pl + d * m_sd);
+        const uint2 c = *(const uint2 *)(ph + d * m_sd);
+        const double lo[PPT] = {bf16lo(a.x), bf16hi(a.x), bf16lo(a.y), bf16hi(a.y)};
+        const double hi[PPT] = {bf16lo(c.x), bf16hi(c.x), bf16lo(c.y), bf16hi(c.y)};
+        accumulate(d, lo, hi);
+      }
+    } else {
+      const float *pl = (const float *)mn + mbase + p0;
+      const float *ph = (const float *)mx + mbase + p0;
+#pragma unroll 2
+      for (int64_t d = 0; d < D; ++d) {
+        const float4 a = *(const float4 *)(pl + d * m_sd);
+        const float4 c = *(const float4 *)(ph + d * m_sd);
+        const double lo[PPT] = {a.x, a.y, a.z, a.w};
+        const double hi[PPT] = {c.x, c.y, c.z, c.w};
+        accumulate(d, lo, hi);
+      }
+    }
+  } else {
+    for (int64_t d = 0; d < D; ++d) {
+      double lo[PPT], hi[PPT];
+      const int64_t o = mbase + d * m_sd + p0 * m_sp;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const bool ok = p0 + i < n_pages;
+        lo[i] = ok ? load_as_f64(mn, o + i * m_sp, MT) : 0.0;
+        hi[i] = ok ? load_as_f64(mx, o + i * m_sp, MT) : 0.0;
+      }
+      accumulate(d, lo, hi);
     }
   }
 #pragma unroll

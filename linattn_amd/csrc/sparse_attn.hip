@@ -117,7 +117,8 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
   const int64_t qpos = p.causal ? (p.offset + t) : (int64_t)0x7fffffffffffffffLL;
   const int64_t lim = min(len - 1, qpos);  // last attendable token
 
-  // Stage the split's entries.
+  // Stage the split's entries: logical first token (for masking) and, for a
+  // paged cache, the pool row of that token (so a token costs no page lookup).
   for (int64_t e = tid; e < ne; e += SA_NT) {
     const int32_t id = list[e0 + e];
     const int64_t tok0 = (int64_t)id * p.unit;
@@ -126,10 +127,15 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
     if constexpr (PAGED) {
       if (p.staged && ok) {
         const int64_t ps = p.kv.page_size;
-        s_phys[e] = p.kv.page_table[b * p.kv.pt_stride + tok0 / ps];
+        const int64_t phys = p.kv.page_table[b * p.kv.pt_stride + tok0 / ps];
+        s_phys[e] = (int32_t)((phys * p.Hkv + kvh) * ps + tok0 % ps);
       }
     }
   }
+  const int64_t k_bh = b * p.kv.k_sb + kvh * p.kv.k_sh;  // contiguous-layout bases
+  const int64_t v_bh = b * p.kv.v_sb + kvh * p.kv.v_sh;
+  const int64_t s_bh = b * p.kv.s_sb + kvh * p.kv.s_sh;
+  const int32_t lim32 = (int32_t)min(lim, (int64_t)0x7fffffff);
 
   // q chunk of this lane for the G heads, pre-scaled into the log2 domain.
   float qf[G][EPL];
@@ -153,24 +159,35 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
   const char *kbase = (const char *)p.kv.k;
   const char *vbase = (const char *)p.kv.v;
   constexpr int64_t WAVE_SPAN = (int64_t)RPI * UNR;
-  for (int64_t base = 0; base < F; base += SA_NW * WAVE_SPAN) {
+  constexpr int64_t STEP = SA_NW * WAVE_SPAN;
+  struct Batch {
     Vec kr[UNR], vr[UNR];
     float ksc[UNR], vsc[UNR];
     bool ok[UNR];
+  };
+  // Issue the loads of the batch starting at flat token `base`.
+  auto load = [&](int64_t base, Batch &bt) {
+    Vec(&kr)[UNR] = bt.kr;
+    Vec(&vr)[UNR] = bt.vr;
+    float(&ksc)[UNR] = bt.ksc;
+    float(&vsc)[UNR] = bt.vsc;
+    bool(&ok)[UNR] = bt.ok;
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
-      const int64_t f = base + w * WAVE_SPAN + u * RPI + slot;
-      int64_t e, j;
+      // flat token indices stay below 2^31 (checked on the host)
+      const int32_t f = (int32_t)base + w * (int32_t)WAVE_SPAN + u * RPI + slot;
+      int32_t e, j;
       if (p.unit_shift >= 0) {
         e = f >> p.unit_shift;
-        j = f & ((1ll << p.unit_shift) - 1);
+        j = f & ((1 << p.unit_shift) - 1);
       } else {
-        e = (int64_t)((uint32_t)f / (uint32_t)p.unit);
-        j = f - e * p.unit;
+        e = (int32_t)((uint32_t)f / (uint32_t)p.unit);
+        j = f - e * (int32_t)p.unit;
       }
-      const int32_t tok0 = (f < F) ? s_tok0[min(e, (int64_t)SA_MAX_EPS - 1)] : -1;
-      const int64_t tok = (int64_t)tok0 + j;
-      ok[u] = tok0 >= 0 && tok <= lim;
+      const int32_t es = min(e, SA_MAX_EPS - 1);
+      const int32_t tok0 = (f < (int32_t)F) ? s_tok0[es] : -1;
+      const int32_t tok = tok0 + j;
+      ok[u] = tok0 >= 0 && tok <= lim32;
       kr[u] = Vec{};
       vr[u] = Vec{};
       ksc[u] = 1.f;
@@ -178,15 +195,20 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
       if (ok[u]) {
         int64_t ko, vo, so = 0;
         if constexpr (PAGED) {
-          const int64_t ps = p.kv.page_size;
-          const int64_t phys = p.staged ? (int64_t)s_phys[e] : (int64_t)p.kv.page_table[b * p.kv.pt_stride + tok / ps];
-          const int64_t prow = (phys * p.Hkv + kvh) * ps + tok % ps;
+          int64_t prow;
+          if (p.staged) {
+            prow = (int64_t)((uint32_t)s_phys[es] + (uint32_t)j);  // pool rows < 2^32
+          } else {
+            const int64_t ps = p.kv.page_size;
+            const int64_t phys = p.kv.page_table[b * p.kv.pt_stride + tok / ps];
+            prow = (phys * p.Hkv + kvh) * ps + tok % ps;
+          }
           ko = vo = prow * D;
           so = prow;
         } else {
-          ko = b * p.kv.k_sb + kvh * p.kv.k_sh + tok * p.kv.k_st;
-          vo = b * p.kv.v_sb + kvh * p.kv.v_sh + tok * p.kv.v_st;
-          so = b * p.kv.s_sb + kvh * p.kv.s_sh + tok * p.kv.s_st;
+          ko = k_bh + (int64_t)tok * p.kv.k_st;
+          vo = v_bh + (int64_t)tok * p.kv.v_st;
+          so = s_bh + (int64_t)tok * p.kv.s_st;
         }
         kr[u] = *(const Vec *)(kbase + (ko + c * EPL) * Tr::ESZ);
         vr[u] = *(const Vec *)(vbase + (vo + c * EPL) * Tr::ESZ);
@@ -196,6 +218,14 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
         }
       }
     }
+  };
+  // Online-softmax update with one loaded batch.
+  auto process = [&](Batch &bt) {
+    Vec(&kr)[UNR] = bt.kr;
+    Vec(&vr)[UNR] = bt.vr;
+    float(&ksc)[UNR] = bt.ksc;
+    float(&vsc)[UNR] = bt.vsc;
+    bool(&ok)[UNR] = bt.ok;
     float s[G][UNR];
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
@@ -210,11 +240,9 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
       }
     }
 #pragma unroll
-    for (int off = 1; off < LPR; off <<= 1)
+    for (int u = 0; u < UNR; ++u)
 #pragma unroll
-      for (int u = 0; u < UNR; ++u)
-#pragma unroll
-        for (int g = 0; g < G; ++g) s[g][u] += __shfl_xor(s[g][u], off, 64);
+      for (int g = 0; g < G; ++g) s[g][u] = group_sum<LPR>(s[g][u]);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float mb = __int_as_float(0xff800000);
@@ -246,6 +274,16 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(s[g][u], vf[e], acc[g][e]);
     }
+  };
+  // Double-buffered: the next batch's loads are in flight while one is processed.
+  Batch b0, b1;
+  if (F > 0) load(0, b0);
+  for (int64_t base = 0; base < F; base += 2 * STEP) {
+    if (base + STEP < F) load(base + STEP, b1);
+    process(b0);
+    if (base + STEP >= F) break;
+    if (base + 2 * STEP < F) load(base + 2 * STEP, b0);
+    process(b1);
   }
 
   // Merge the row slots of the wave (lanes that own the same chunk c).
@@ -332,9 +370,10 @@ __global__ __launch_bounds__(256) void sparse_attn_combine(AttnKP p, int64_t G, 
   }
 }
 
+// Tokens per row slot per batch; two batches are in flight per wave.
 template <int KT>
 constexpr int unroll_for(int D) {
-  return 8;
+  return 4;
 }
 
 template <int KT, int D, int G, bool PAGED>

@@ -42,6 +42,8 @@ def _kv_struct(k: torch.Tensor, v: torch.Tensor, *, page_table: Optional[torch.T
             raise ValueError("page_size must equal the pool's page dimension")
         if page_table.dtype != torch.int32 or page_table.dim() != 2 or page_table.stride(1) != 1:
             raise ValueError("page_table must be int32 (B, pages) with unit last stride")
+        if k.shape[0] * k.shape[1] * k.shape[2] >= 2 ** 32:
+            raise ValueError("paged pool holds >= 2^32 token rows")
         kv.page_table = page_table.data_ptr()
         kv.pt_stride = page_table.stride(0)
         kv.page_size = page_size
