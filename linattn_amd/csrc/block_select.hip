@@ -1,7 +1,172 @@
-// Block selection for block-sparse prefill.
-#include "common.h"
+// Block selection for block-sparse prefill (config C3), gfx950.
+//
+// The block-sparse estimator of MInferenceAttention._block_sparse
+// (variants/selection.py:339-353): mean-pool q and k over 64-token blocks
+// (block_reduce, core.py:102-120; the tail block repeats the last row), score
+// every causal block pair with the pooled dot product, keep the top-k key
+// blocks per (b, h, query block), then OR the sink blocks and the local window
+// (which contains the diagonal block, selection.py:351).
+//
+// Arithmetic is fp64 and a fixed function of the inputs: pooled sums add rows
+// in order and divide by the block size; block scores add fl(qbar_d*kbar_d)
+// over d in order (never fused).  The positive 1/sqrt(D) factor of the
+// reference does not change the ranking and is not applied.
+#include <algorithm>
 
-extern "C" size_t la_block_select_workspace(const la_block_select_args *) { return 0; }
-extern "C" int la_block_select(const la_block_select_args *, void *) {
-  return la::fail(LA_ERR_UNSUPPORTED, "la_block_select: not built yet");
+#include "common.h"
+#include "topk.h"
+
+namespace la {
+
+// qbar/kbar[b][h][blk][d] = (sum_{i<bs} x[b][h][min(blk*bs+i, T-1)][d]) / bs
+__global__ __launch_bounds__(128) void mean_pool_kernel(const void *x, int dt, int64_t T, int64_t D,
+                                                        int64_t sb, int64_t sh, int64_t st,
+                                                        int64_t bs, int64_t H, int64_t nb,
+                                                        double *out) {
+  const int64_t blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t base = b * sb + h * sh;
+  for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
+    double acc = 0.0;
+    for (int64_t i = 0; i < bs; ++i) {
+      const int64_t row = min(blk * bs + i, T - 1);
+      acc = acc + load_as_f64(x, base + row * st + d, dt);
+    }
+    out[((b * H + h) * nb + blk) * D + d] = acc / (double)bs;
+  }
+}
+
+constexpr int BS_TQ = 64, BS_TK = 64, BS_DC = 32, BS_NT = 256;
+
+// scores[(b*Hq+h)*nqb + i][j] = sum_d fl(qbar[b,h,i,d] * kbar[b,h/G,j,d]) for
+// the 64x64 tile (i, j), j <= i (tiles above the diagonal are skipped).
+__global__ __launch_bounds__(BS_NT) void block_score_kernel(const double *qbar, const double *kbar,
+                                                            int64_t Hq, int64_t Hkv, int64_t nqb,
+                                                            int64_t nkb, int64_t D, double *scores) {
+  __shared__ double sq[BS_DC][BS_TQ + 2];
+  __shared__ double sk[BS_DC][BS_TK + 2];
+  const int tid = threadIdx.x;
+  const int tq = tid >> 4, tk = tid & 15;  // rows 4*tq.., cols 4*tk..
+  const int64_t i0 = (int64_t)blockIdx.y * BS_TQ, j0 = (int64_t)blockIdx.x * BS_TK;
+  const int64_t bh = blockIdx.z;
+  const int64_t b = bh / Hq, h = bh % Hq;
+  if (j0 > min(i0 + BS_TQ - 1, nqb - 1)) return;  // entirely above the diagonal
+  const double *qb = qbar + bh * nqb * D;
+  const double *kb = kbar + (b * Hkv + h / (Hq / Hkv)) * nkb * D;
+  double acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[a][c] = 0.0;
+  for (int64_t d0 = 0; d0 < D; d0 += BS_DC) {
+    const int dn = (int)min((int64_t)BS_DC, D - d0);
+    __syncthreads();
+    for (int x = tid; x < BS_TQ * BS_DC; x += BS_NT) {
+      const int r = x / BS_DC, dd = x % BS_DC;
+      sq[dd][r] = (dd < dn && i0 + r < nqb) ? qb[(i0 + r) * D + d0 + dd] : 0.0;
+      sk[dd][r] = (dd < dn && j0 + r < nkb) ? kb[(j0 + r) * D + d0 + dd] : 0.0;
+    }
+    __syncthreads();
+    for (int dd = 0; dd < dn; ++dd) {
+      double qv[4], kv[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        qv[a] = sq[dd][4 * tq + a];
+        kv[a] = sk[dd][4 * tk + a];
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[a][c] = add_product(acc[a][c], qv[a], kv[c]);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int64_t i = i0 + 4 * tq + a;
+    if (i >= nqb) continue;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t j = j0 + 4 * tk + c;
+      if (j < nkb) scores[(bh * nqb + i) * nkb + j] = acc[a][c];
+    }
+  }
+}
+
+struct BsLayout {
+  int64_t nqb, nkb, qbar_off, kbar_off, sc_off, bytes;
+};
+
+static BsLayout layout(const la_block_select_args *a) {
+  BsLayout L{};
+  L.nqb = ceil_div(a->T, a->block);
+  L.nkb = L.nqb;
+  L.qbar_off = 0;
+  L.kbar_off = L.qbar_off + a->B * a->Hq * L.nqb * a->D * 8;
+  L.sc_off = L.kbar_off + a->B * a->Hkv * L.nkb * a->D * 8;
+  L.bytes = L.sc_off + a->B * a->Hq * L.nqb * L.nkb * 8;
+  return L;
+}
+
+static int validate(const la_block_select_args *a) {
+  LA_REQUIRE(a && a->q && a->k && a->out_idx, "la_block_select: null pointer");
+  LA_REQUIRE(a->B > 0 && a->Hq > 0 && a->Hkv > 0 && a->T > 0 && a->D > 0 && a->block > 0,
+             "la_block_select: bad shape");
+  LA_REQUIRE(a->Hq % a->Hkv == 0, "n_heads must be a multiple of n_kv_heads");
+  LA_REQUIRE(a->topk >= 1 && a->sink_blocks >= 0 && a->window_blocks >= 0, "la_block_select: budget");
+  LA_REQUIRE(a->width >= a->topk + a->sink_blocks + a->window_blocks,
+             "la_block_select: width < topk + sink + window");
+  LA_REQUIRE(a->in_dtype == LA_F32 || a->in_dtype == LA_BF16 || a->in_dtype == LA_F16,
+             "la_block_select: q/k dtype");
+  return LA_OK;
+}
+
+}  // namespace la
+
+using namespace la;
+
+extern "C" size_t la_block_select_workspace(const la_block_select_args *a) {
+  if (validate(a) != LA_OK) return 0;
+  return (size_t)layout(a).bytes;
+}
+
+extern "C" int la_block_select(const la_block_select_args *a, void *stream) {
+  int rc = validate(a);
+  if (rc != LA_OK) return rc;
+  const BsLayout L = layout(a);
+  if (!a->workspace || a->ws_bytes < L.bytes)
+    return fail(LA_ERR_WORKSPACE, "la_block_select: workspace %lld < %lld bytes",
+                (long long)a->ws_bytes, (long long)L.bytes);
+  hipStream_t st = (hipStream_t)stream;
+  char *ws = (char *)a->workspace;
+  double *qbar = (double *)(ws + L.qbar_off);
+  double *kbar = (double *)(ws + L.kbar_off);
+  double *sc = (double *)(ws + L.sc_off);
+  mean_pool_kernel<<<dim3((unsigned)L.nqb, (unsigned)a->Hq, (unsigned)a->B), 128, 0, st>>>(
+      a->q, a->in_dtype, a->T, a->D, a->q_sb, a->q_sh, a->q_st, a->block, a->Hq, L.nqb, qbar);
+  LA_LAUNCHED();
+  mean_pool_kernel<<<dim3((unsigned)L.nkb, (unsigned)a->Hkv, (unsigned)a->B), 128, 0, st>>>(
+      a->k, a->in_dtype, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block, a->Hkv, L.nkb, kbar);
+  LA_LAUNCHED();
+  block_score_kernel<<<dim3((unsigned)ceil_div(L.nkb, BS_TK), (unsigned)ceil_div(L.nqb, BS_TQ),
+                            (unsigned)(a->B * a->Hq)),
+                       BS_NT, 0, st>>>(qbar, kbar, a->Hq, a->Hkv, L.nqb, L.nkb, a->D, sc);
+  LA_LAUNCHED();
+  TopkKParams tp{};
+  tp.scores = sc;
+  tp.row_stride = L.nkb;
+  tp.G = 1;
+  tp.Tq = L.nqb;
+  tp.NG = a->B * a->Hq * L.nqb;
+  tp.t_base = 0;
+  tp.out_tq = L.nqb;
+  tp.n = L.nkb;
+  tp.k = a->topk;
+  tp.width = a->width;
+  tp.pos_off = 0;  // query block qb: key blocks kb <= qb, own block qb
+  tp.pos_unit = 1;
+  tp.sink = a->sink_blocks;
+  tp.window = a->window_blocks;
+  tp.order = 1;
+  tp.out_idx = a->out_idx;
+  tp.out_count = a->out_count;
+  return topk_launch(tp, st);
 }

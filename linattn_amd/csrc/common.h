@@ -119,6 +119,12 @@ __device__ __forceinline__ double key_to_double(uint64_t u) {
 }
 constexpr uint64_t KEY_FORCED = 0xffffffffffffffffull;  // above every finite score
 
+// fl(acc + fl(a * b)): two roundings, never fused into an fma.
+__device__ __forceinline__ double add_product(double acc, double a, double b) {
+#pragma clang fp contract(off)
+  return acc + a * b;
+}
+
 // ------------------------------------------------------------ wave utils ----
 __device__ __forceinline__ float wave_xor_f32(float x, int m) { return __shfl_xor(x, m, 64); }
 

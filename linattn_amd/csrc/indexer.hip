@@ -37,11 +37,6 @@ struct IdxKP {
   int32_t dt, causal;
 };
 
-__device__ __forceinline__ double add_product(double acc, double a, double b) {
-#pragma clang fp contract(off)
-  return acc + a * b;
-}
-
 constexpr int IT_Q = 64, IT_K = 128, IT_D = 64;  // tile, d slice
 constexpr int IT_NT = 256;
 

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
     if constexpr (MT == LA_BF16) {
       const uint16_t *pl = (const uint16_t *)mn + mbase + p0;
       const uint16_t *ph = (const uint16_t *)mx + mbase + p0;
-#pragma unroll 2
+#pragma unroll 8
       for (int64_t d = 0; d < D; ++d) {
         const uint2 a = *(const uint2 *)(pl + d * m_sd);
         const uint2 c = *(const uint2 *)(ph + d * m_sd);
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
     } else {
       const float *pl = (const float *)mn + mbase + p0;
       const float *ph = (const float *)mx + mbase + p0;
-#pragma unroll 2
+#pragma unroll 8
       for (int64_t d = 0; d < D; ++d) {
         const float4 a = *(const float4 *)(pl + d * m_sd);
         const float4 c = *(const float4 *)(ph + d * m_sd);

@@ -187,12 +187,14 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
     ptr += ((p.n * 8 + 15) / 16) * 16;
   }
   int32_t *sel = nullptr;
+  uint64_t *skey = nullptr;  // keys of sel[], kept beside them for the sort
   uint32_t *bm = nullptr;
   if (p.use_bitmap) {
     bm = (uint32_t *)ptr;
     for (int64_t i = tid; i < p.bitmap_words; i += TK_NT) bm[i] = 0u;
   } else {
-    sel = (int32_t *)ptr;
+    skey = (uint64_t *)ptr;
+    sel = (int32_t *)(ptr + p.p2k * 8);
   }
   __syncthreads();
 
@@ -210,21 +212,34 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
         atomicOr(&bm[i >> 5], 1u << (i & 31));
       });
     } else {
-      tk_select(key, n_v, K, sh, [&](int64_t i, uint32_t pos) { sel[pos] = (int32_t)i; });
-      // bitonic sort of sel[0, p2k) by (key desc, index asc); padding is -1.
-      for (int64_t i = K + tid; i < p.p2k; i += TK_NT) sel[i] = -1;
+      tk_select(key, n_v, K, sh, [&](int64_t i, uint32_t pos) {
+        sel[pos] = (int32_t)i;
+        skey[pos] = key(i);
+      });
+      // Bitonic sort of (skey, sel)[0, p2k) by (key desc, index asc); padding
+      // entries (index -1) sort last.  Each thread handles whole pairs.
+      for (int64_t i = K + tid; i < p.p2k; i += TK_NT) {
+        sel[i] = -1;
+        skey[i] = 0;
+      }
       __syncthreads();
-      for (int64_t size = 2; size <= p.p2k; size <<= 1) {
-        for (int64_t stride = size >> 1; stride > 0; stride >>= 1) {
-          for (int64_t i = tid; i < p.p2k; i += TK_NT) {
-            const int64_t l = i ^ stride;
-            if (l > i) {
-              const int32_t a = sel[i], b = sel[l];
-              const bool up = (i & size) == 0;
-              if (up ? key.before(b, a) : key.before(a, b)) {
-                sel[i] = b;
-                sel[l] = a;
-              }
+      const uint32_t half = (uint32_t)(p.p2k >> 1);
+      for (uint32_t size = 2; size <= (uint32_t)p.p2k; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+          for (uint32_t jp = tid; jp < half; jp += TK_NT) {
+            const uint32_t i = ((jp & ~(stride - 1)) << 1) | (jp & (stride - 1));
+            const uint32_t l = i + stride;
+            const int32_t a = sel[i], b = sel[l];
+            const uint64_t ka = skey[i], kb = skey[l];
+            // x precedes y: valid before padding, higher key, then lower index
+            const bool b_first = b >= 0 && (a < 0 || kb > ka || (kb == ka && b < a));
+            const bool a_first = a >= 0 && (b < 0 || ka > kb || (ka == kb && a < b));
+            const bool up = (i & size) == 0;
+            if (up ? b_first : a_first) {
+              sel[i] = b;
+              sel[l] = a;
+              skey[i] = kb;
+              skey[l] = ka;
             }
           }
           __syncthreads();
@@ -288,7 +303,7 @@ int64_t topk_lds_bytes(const TopkKParams &p) {
   if (p.use_bitmap)
     b += align16(p.bitmap_words * 4);
   else
-    b += align16(p.p2k * 4);
+    b += align16(p.p2k * 12);
   return b;
 }
 
