@@ -133,6 +133,40 @@ def bench_c2(dev, steps, warmup):
             "frac_fp64_valu_peak": round(tflops / FP64_VALU_PEAK_TFLOPS, 4)}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, AMD public spec
+
+
+def bench_c3(dev, steps, warmup):
+    """Config 3: block-sparse causal prefill, bf16, B=2, T=32768, 32/8 heads,
+    D=128, 64x64 blocks, sink + 4-block window + top-16 by pooled scores."""
+    import torch
+
+    from linattn_amd.kernels.prefill import block_select_hip, block_sparse_prefill
+
+    B, Hq, Hkv, T, D, bs = 2, 32, 8, 32768, 128, 64
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, Hq, T, D, generator=g, device=dev)
+    k = torch.randn(B, Hkv, T, D, generator=g, device=dev)
+    v = torch.randn(B, Hkv, T, D, generator=g, device=dev)
+    for b in range(B):
+        for h in range(Hkv):
+            rows = torch.randperm(T, generator=g, device=dev)[:T // 100]
+            k[b, h, rows] *= 8.0
+    q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    ids, counts = block_select_hip(q, k, block=bs, topk=16, sink_blocks=1, window_blocks=4)
+    ms_sel = time_cuda(lambda: block_select_hip(q, k, block=bs, topk=16, sink_blocks=1,
+                                                window_blocks=4), steps, warmup)
+    ms = time_cuda(lambda: block_sparse_prefill(q, k, v, ids, counts, block_size=bs), steps, warmup)
+    pairs = int(counts.sum())
+    flops = pairs * bs * bs * D * 2 * 2  # QK^T and PV, diagonal blocks counted whole
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "C3 block-sparse causal prefill, B=2, T=32768, 32/8 heads, D=128, bf16",
+            "selected_block_pairs": pairs, "ms_prefill": round(ms, 4),
+            "ms_block_select": round(ms_sel, 4), "TFLOPs": round(tflops, 1),
+            "frac_mfma_bf16_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "note": "useful FLOPs; the PV product issues two bf16 MFMAs (P split hi+lo)"}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -227,6 +261,7 @@ def main() -> int:
                  "pages_read_per_kv_list": round(n_pages_read / (B * lists_heads), 2)},
     }
     result["indexer"] = bench_c2(dev, max(3, args.steps // 4), 2)
+    result["prefill"] = bench_c3(dev, max(3, args.steps // 4), 2)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg,
                                               args.cpu_sample, union)

@@ -168,7 +168,11 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     l *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-    bf16x8 pb[2];
+    // P = P_hi + P_lo in bf16 (P_lo = bf16(P - P_hi)): the product keeps ~16
+    // mantissa bits of each weight, so bf16 rounding of P costs ~2^-17
+    // relative instead of 2^-9 (which alone exceeds 2e-3 on rows whose mass
+    // sits on a few keys).
+    bf16x8 ph[2], pl[2];
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       float pv[8];
@@ -181,9 +185,13 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       for (int e = 0; e < 8; ++e) l += pv[e];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        const bf16x2 t2 = __builtin_convertvector((f32x2{pv[e], pv[e + 1]}), bf16x2);
-        pb[s2][e] = t2[0];
-        pb[s2][e + 1] = t2[1];
+        const bf16x2 h2 = __builtin_convertvector((f32x2{pv[e], pv[e + 1]}), bf16x2);
+        const f32x2 hf = __builtin_convertvector(h2, f32x2);
+        const bf16x2 l2 = __builtin_convertvector((f32x2{pv[e] - hf[0], pv[e + 1] - hf[1]}), bf16x2);
+        ph[s2][e] = h2[0];
+        ph[s2][e + 1] = h2[1];
+        pl[s2][e] = l2[0];
+        pl[s2][e + 1] = l2[1];
       }
     }
     // O^T += V^T P^T
@@ -195,8 +203,9 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
         const uint2 lo = *(const uint2 *)vrow;
         const uint2 hi = *(const uint2 *)(vrow + 16);
         const uint4 av = {lo.x, lo.y, hi.x, hi.y};
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)&av, pb[s2], acc[dt],
-                                                          0, 0, 0);
+        const bf16x8 a = *(const bf16x8 *)&av;
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[s2], acc[dt], 0, 0, 0);
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[s2], acc[dt], 0, 0, 0);
       }
     }
     if (j + 1 < n) lstore(buf ^ 1);
