@@ -167,6 +167,49 @@ def bench_c3(dev, steps, warmup):
             "note": "useful FLOPs; the PV product issues two bf16 MFMAs (P split hi+lo)"}
 
 
+def bench_c5(dev, steps, warmup):
+    """Config 5: fp8 e4m3 KV (per-token fp32 scales) sparse decode, batch 16,
+    context 131072 in 64-token pages, 32/8 heads, D=128; the indexer (4 x 64,
+    bf16) picks 4096 tokens per sequence."""
+    import torch
+
+    from linattn_amd.kernels.paged_decode import indexer_decode_step, quantize_fp8_per_token
+
+    B, Hq, Hkv, T, D, ps, HI, d, topk = 16, 32, 8, 131072, 128, 64, 4, 64, 4096
+    P = T // ps
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, Hq, 1, D, generator=g, device=dev).bfloat16()
+    kc = torch.empty(B * P, Hkv, ps, D, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.empty(B * P, Hkv, ps, dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    chunk = 4096
+    for dst, sdst in ((kc, ks), (vc, vs)):
+        for i in range(0, B * P, chunk):
+            n = min(chunk, B * P - i)
+            c, s = quantize_fp8_per_token(torch.randn(n, Hkv, ps, D, generator=g, device=dev))
+            dst[i:i + n], sdst[i:i + n] = c, s
+    pt = torch.randperm(B * P, generator=g, device=dev).view(B, P).to(torch.int32)
+    q_idx = torch.randn(B, 1, HI, d, generator=g, device=dev).bfloat16()
+    k_idx = torch.randn(B, T, HI, d, generator=g, device=dev).bfloat16()
+    w = torch.rand(B, 1, HI, generator=g, device=dev)
+
+    def step():
+        return indexer_decode_step(q, kc, vc, pt, q_idx, k_idx, w, topk=topk, pos=T - 1,
+                                   page_size=ps, k_scale=ks, v_scale=vs)
+
+    ms = time_cuda(step, steps, warmup)
+    bytes_step = (B * T * HI * d * 2            # indexer keys
+                  + B * Hkv * topk * D * 2       # fp8 K and V of the kept tokens
+                  + B * Hkv * topk * 2 * 4       # their scales
+                  + B * T * 8 * 2)               # fp64 scores written and read
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    return {"workload": "C5 fp8-KV indexer sparse decode, B=16, T=131072, top-4096",
+            "tok_per_s": round(B / (ms * 1e-3), 1), "ms": round(ms, 4),
+            "bytes_per_step": bytes_step, "GBps": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -262,6 +305,7 @@ def main() -> int:
     }
     result["indexer"] = bench_c2(dev, max(3, args.steps // 4), 2)
     result["prefill"] = bench_c3(dev, max(3, args.steps // 4), 2)
+    result["fp8_decode"] = bench_c5(dev, max(3, args.steps // 4), 2)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg,
                                               args.cpu_sample, union)

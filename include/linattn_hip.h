@@ -215,7 +215,9 @@ int la_topk_rows(const la_topk_args *a, void *stream);
  * Scores are computed in fp64: each q.k product is exact, summed over d in
  * order, then ReLU, then sum over heads h = 0..HI-1 of fl(w_h * relu_h).
  * causal != 0 keeps keys s <= offset + t only (an addition; the reference
- * scores every key, fused_indexer.py:63-73).
+ * scores every key, fused_indexer.py:63-73).  With causal_unit = m > 1 the
+ * keys are pooled groups of m tokens and group s is kept when s*m <= offset+t
+ * (the compressed-indexing mask of selection.py:739-747); 0 or 1 = tokens.
  * out_idx int32 (B, Tq, k) sorted by (score desc, index asc), -1 padded;
  * out_val fp32 (B, Tq, k), -inf padded (optional).
  * q_chunk bounds the queries scored per pass (workspace = q_chunk*Tk*8 bytes
@@ -235,6 +237,7 @@ typedef struct {
   int64_t w_sb, w_st, w_sh;
   int64_t offset;
   int64_t q_chunk;
+  int64_t causal_unit;
   int32_t in_dtype;
   int32_t causal;
 } la_indexer_args;

@@ -75,7 +75,7 @@ class LaIndexerArgs(ctypes.Structure):
                 ("HI", _i64), ("d", _i64), ("k", _i64), ("q_sb", _i64), ("q_st", _i64),
                 ("q_sh", _i64), ("k_sb", _i64), ("k_st", _i64), ("k_sh", _i64), ("w_sb", _i64),
                 ("w_st", _i64), ("w_sh", _i64), ("offset", _i64), ("q_chunk", _i64),
-                ("in_dtype", _i32), ("causal", _i32)]
+                ("causal_unit", _i64), ("in_dtype", _i32), ("causal", _i32)]
 
 
 class LaBlockSelectArgs(ctypes.Structure):

@@ -34,6 +34,7 @@ struct IdxKP {
   int64_t q_sb, q_st, q_sh, k_sb, k_st, k_sh, w_sb, w_st, w_sh;
   int64_t t0, tn;  // query chunk [t0, t0 + tn)
   int64_t offset;
+  int64_t unit;  // tokens per key (pooled groups); key s starts at token s*unit
   int32_t dt, causal;
 };
 
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(IT_NT) void indexer_tile_kernel(IdxKP p) {
   // causal: skip tiles whose first key is after the tile's last query
   if (p.causal) {
     const int64_t last_q = p.offset + p.t0 + min(q0 + IT_Q, p.tn) - 1;
-    if (k0 > last_q) return;
+    if (k0 * p.unit > last_q) return;
   }
   double score[8][4];
 #pragma unroll
@@ -242,6 +243,7 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     p.offset = a->offset;
     p.dt = a->in_dtype;
     p.causal = a->causal;
+    p.unit = std::max<int64_t>(1, a->causal_unit);
     if (decode) {
       indexer_decode_kernel<<<dim3((unsigned)ceil_div(a->Tk, ID_KEYS), (unsigned)a->B), 256, 0,
                               st>>>(p);
@@ -263,7 +265,7 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     tp.k = a->k;
     tp.width = a->k;
     tp.pos_off = a->causal ? a->offset : 0;
-    tp.pos_unit = a->causal ? 1 : 0;
+    tp.pos_unit = a->causal ? std::max<int64_t>(1, a->causal_unit) : 0;
     tp.order = 0;
     tp.out_idx = a->out_idx;
     tp.out_val = a->out_val;

@@ -26,11 +26,13 @@ __all__ = ["indexer_topk", "indexer_topk_hip", "indexer_topk_triton"]
 
 def indexer_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, head_weights: torch.Tensor, k: int, *,
                  backend: str = "auto", causal: bool = False, offset: int = 0,
-                 q_chunk: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+                 causal_unit: int = 1, q_chunk: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
     """Top-k indexer scores: ``(values fp32 (B,Tq,k), indices int32 (B,Tq,k))``.
 
     q_idx: (B, Tq, H_I, d), k_idx: (B, Tk, H_I, d) in fp32/bf16/fp16;
-    head_weights: (B, Tq, H_I).  ``k`` is clipped to Tk as in the reference."""
+    head_weights: (B, Tq, H_I).  ``k`` is clipped to Tk as in the reference.
+    With ``causal_unit`` = m > 1 the keys are pooled groups of m tokens and
+    group s is visible to query t when s*m <= offset + t."""
     if backend not in ("auto", "hip", "triton"):
         raise ValueError(f"backend {backend!r} is not provided by linattn_amd (only 'hip')")
     dev = N.require_gpu(q_idx, k_idx, head_weights, what="indexer_topk")
@@ -61,6 +63,7 @@ def indexer_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, head_weights: torch.T
     a.w_sb, a.w_st, a.w_sh = w.stride(0), w.stride(1), w.stride(2)
     a.offset = int(offset)
     a.q_chunk = int(q_chunk)
+    a.causal_unit = int(causal_unit)
     a.in_dtype = N.dtype_code(q_idx.dtype)
     a.causal = 1 if causal else 0
     L = N.load()

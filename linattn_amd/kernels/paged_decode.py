@@ -16,9 +16,40 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from linattn_amd.kernels.block_sparse import sparse_attention
+from linattn_amd.kernels.fused_indexer import indexer_topk
 from linattn_amd.kernels.quest_pages import quest_select_hip
 
-__all__ = ["paged_decode", "quest_decode_step"]
+__all__ = ["paged_decode", "quest_decode_step", "indexer_decode_step", "quantize_fp8_per_token"]
+
+
+def quantize_fp8_per_token(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """fp8 e4m3 codec of kv/quant.py:76-93 with group = head_dim: scale =
+    max|x| / 448 per row (clamped to 1e-8), codes = (x / scale) cast to
+    float8_e4m3fn.  Returns (codes, fp32 scales without the last dim)."""
+    xf = x.to(torch.float32)
+    scale = xf.abs().amax(-1, keepdim=True).clamp_min(1e-8) / 448.0
+    return (xf / scale).to(torch.float8_e4m3fn), scale.squeeze(-1)
+
+
+def indexer_decode_step(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                        page_table: torch.Tensor, q_idx: torch.Tensor, k_idx: torch.Tensor,
+                        head_weights: torch.Tensor, *, topk: int, pos: int, page_size: int,
+                        k_scale: Optional[torch.Tensor] = None,
+                        v_scale: Optional[torch.Tensor] = None,
+                        out_dtype: Optional[torch.dtype] = None
+                        ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One DSA-style decode step (config C5): the lightning indexer picks
+    ``topk`` tokens per sequence (causal, one list shared by every head,
+    fused_indexer.py:52-73), then every query head attends those tokens of the
+    paged (optionally fp8) cache.  q (B, Hq, 1, D); q_idx (B, 1, H_I, d);
+    k_idx (B, T, H_I, d); head_weights (B, 1, H_I).  Returns (out, token ids)."""
+    B, Hkv = q.shape[0], k_pool.shape[1]
+    _, idx = indexer_topk(q_idx, k_idx, head_weights, topk, causal=True, offset=pos)
+    ids = idx.view(B, 1, 1, -1).expand(B, Hkv, 1, idx.shape[-1])
+    out = sparse_attention(q, k_pool, v_pool, ids, unit=1, causal=True, offset=pos,
+                           page_table=page_table, page_size=page_size, k_scale=k_scale,
+                           v_scale=v_scale, out_dtype=out_dtype)
+    return out, idx
 
 
 def paged_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, page_ids: torch.Tensor, *,

@@ -428,12 +428,16 @@ def indexer_scores(q_idx, k_idx, w, *, causal: bool = False, offset: int = 0) ->
     return out
 
 
-def indexer_topk(q_idx, k_idx, w, k: int, *, causal: bool = False, offset: int = 0):
+def indexer_topk(q_idx, k_idx, w, k: int, *, causal: bool = False, offset: int = 0,
+                 causal_unit: int = 1):
     """indexer_topk_torch (fused_indexer.py:63-73): top-k by (score desc, index
-    asc), int32 indices, -1 / -inf padding when fewer than k keys are valid."""
-    sc = indexer_scores(q_idx, k_idx, w, causal=causal, offset=offset)
+    asc), int32 indices, -1 / -inf padding when fewer than k keys are valid.
+    With ``causal_unit`` = m keys are groups of m tokens and group s is visible
+    when s*m <= offset + t (selection.py:739-747)."""
+    sc = indexer_scores(q_idx, k_idx, w, causal=False)
     B, Tq, Tk = sc.shape
-    nv = np.minimum(Tk, np.arange(Tq) + offset + 1) if causal else np.full(Tq, Tk)
+    m = max(1, causal_unit)
+    nv = np.minimum(Tk, (np.arange(Tq) + offset) // m + 1) if causal else np.full(Tq, Tk)
     idx, val = topk_rows(np.where(np.isfinite(sc), sc, 0.0), k, n_valid=nv)
     return val, idx
 

@@ -1,0 +1,136 @@
+"""The ``hip_*`` variants behind the reference's variant API, against the CPU
+oracle (the backend-parity pattern of the reference's tests/test_mlx.py:40-57:
+same outputs and the same reads_per_query, to within 1)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from linattn_amd.core import AttnConfig
+from linattn_amd.registry import build
+
+pytestmark = pytest.mark.gpu
+
+
+def inputs(b, hq, hkv, t, d, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(b, hq, t, d, generator=g), torch.randn(b, hkv, t, d, generator=g),
+            torch.randn(b, hkv, t, d, generator=g))
+
+
+def cfg(**kw):
+    base = dict(n_heads=4, n_kv_heads=2, head_dim=64, block_size=16, window_size=32,
+                topk_blocks=3, topk_tokens=48, compress_ratio=8, sink_size=2)
+    base.update(kw)
+    return AttnConfig(**base)
+
+
+def quest_oracle(q, k, v, c, chunk, union):
+    """QuestAttention.forward semantics chunk by chunk: metadata over every key
+    pushed so far, selection at the chunk's offset, causal attention."""
+    T = q.shape[2]
+    ps = c.extras.get("page_size", c.block_size)
+    outs, reads = [], []
+    for s in range(0, T, chunk):
+        e = min(T, s + chunk)
+        kk, vv = k[:, :, :e], v[:, :, :e]
+        mn, mx = oracle.page_bounds(kk, ps)
+        ids = oracle.quest_select(q[:, :, s:e], mn, mx, page_size=ps, topk=c.topk_blocks,
+                                  offset=s, gqa_union=union)
+        outs.append(oracle.attend_lists(q[:, :, s:e], kk, vv, ids, unit=ps, causal=True,
+                                        offset=s))
+        lim = np.minimum(np.arange(e - s) + s + 1, e)[None, None, :, None]
+        n = np.clip(lim - ids.astype(np.int64) * ps, 0, ps) * (ids >= 0)
+        reads.append(float(n.sum(-1).mean()))
+    return np.concatenate(outs, axis=2), reads
+
+
+@pytest.mark.parametrize("union", [True, False])
+@pytest.mark.parametrize("chunk", [192, 64])
+def test_hip_quest_matches_oracle(dev, union, chunk):
+    c = cfg(extras={"gqa_union": union})
+    q, k, v = inputs(2, 4, 2, 192, 64, seed=1)
+    var = build("hip_quest", c)
+    out, _, stats = var.forward(q.to(dev), k.to(dev), v.to(dev), chunk=chunk, collect_stats=True)
+    ref, reads = quest_oracle(q, k, v, c, chunk, union)
+    assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
+    for s, r in zip(stats, reads):
+        assert abs(s["reads_per_query"] - r) < 1.0
+
+
+def test_hip_quest_full_budget_recovers_dense(dev):
+    """The parity gate (test_budgets.py:64-81), float64 in and out."""
+    q, k, v = inputs(1, 4, 2, 192, 64, seed=2)
+    c = cfg(topk_blocks=192 // 16 + 2)
+    out, _ = build("hip_quest", c).forward(q.double().to(dev), k.double().to(dev),
+                                           v.double().to(dev), chunk=192)
+    assert out.dtype == torch.float64
+    ref = oracle.dense_attention(q, k, v)
+    assert np.abs(out.cpu().numpy() - ref).max() < 1e-5
+
+
+def test_hip_quest_decode_equals_prefill(dev):
+    """Token-by-token decode with state equals one prefill (the cache contract
+    of test_reference.py:64-77): visible pages before the own page are full in
+    both modes and the own page is always read."""
+    q, k, v = inputs(1, 4, 2, 80, 64, seed=3)
+    var = build("hip_quest", cfg())
+    pre, _ = var.forward(q.to(dev), k.to(dev), v.to(dev), chunk=80)
+    state, pieces = None, []
+    for i in range(80):
+        o, state = var.forward(q[:, :, i:i + 1].to(dev), k[:, :, i:i + 1].to(dev),
+                               v[:, :, i:i + 1].to(dev), state=state)
+        pieces.append(o)
+    dec = torch.cat(pieces, dim=2)
+    assert state["pos"] == 80
+    assert (pre - dec).abs().max().item() < 1e-5
+
+
+@pytest.mark.parametrize("name", ["hip_sliding_window", "hip_streaming_sink"])
+def test_hip_window_matches_oracle(dev, name):
+    q, k, v = inputs(2, 4, 2, 150, 64, seed=4)
+    c = cfg()
+    out, _, stats = build(name, c).forward(q.to(dev), k.to(dev), v.to(dev), chunk=64,
+                                           collect_stats=True)
+    mask = oracle.window_mask(150, 150, 0, c.window_size, c.sink_size)
+    ref = oracle.dense_attention(q, k, v, mask=mask)
+    assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
+    last = oracle.window_mask(150 - 128, 150, 128, c.window_size, c.sink_size)
+    assert abs(stats[-1]["reads_per_query"] - last.sum(-1).mean()) < 1.0
+
+
+@pytest.mark.parametrize("ratio", [1, 8])
+def test_hip_dsa_matches_oracle(dev, ratio):
+    """Indexer top-k (per attention head, the reference's projections) plus sink
+    and window, then causal attention over the kept tokens."""
+    c = cfg(compress_ratio=ratio, extras={"indexer_heads": 4, "indexer_dim": 16})
+    q, k, v = inputs(1, 4, 2, 128, 64, seed=5)
+    var = build("hip_dsa", c)
+    out, _ = var.forward(q.to(dev), k.to(dev), v.to(dev), chunk=128)
+    q_idx, k_idx, w = var.indexer_inputs(q.to(dev), k.to(dev))
+    B, H, T = 1, 4, 128
+    if ratio > 1:
+        n_keep = max(1, c.topk_tokens // ratio)
+        _, grp = oracle.indexer_topk(q_idx.cpu(), k_idx.cpu(), w.cpu(), n_keep, causal=True,
+                                     causal_unit=ratio)
+        sel = [[set() for _ in range(T)] for _ in range(H)]
+        for h in range(H):
+            for t in range(T):
+                for gi in grp[h, t]:
+                    if gi >= 0:
+                        sel[h][t].update(range(gi * ratio, gi * ratio + ratio))
+    else:
+        _, idx = oracle.indexer_topk(q_idx.cpu(), k_idx.cpu(), w.cpu(), min(c.topk_tokens, T))
+        sel = [[set(int(x) for x in idx[h, t] if x >= 0) for t in range(T)] for h in range(H)]
+    mask = np.zeros((1, H, T, T), dtype=bool)
+    for h in range(H):
+        for t in range(T):
+            s = sel[h][t] | set(range(c.sink_size)) | set(range(max(0, t - c.window_size + 1), t + 1))
+            for j in s:
+                if j <= t:
+                    mask[0, h, t, j] = True
+    ref = oracle.dense_attention(q, k, v, mask=mask)
+    assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
