@@ -185,6 +185,74 @@ __global__ __launch_bounds__(256) void indexer_decode_kernel(IdxKP p) {
   }
 }
 
+// Few queries over a long key axis with 2-byte keys whose (head, dim) block
+// is contiguous and 16-byte aligned (the decode shape of config C5).  128 keys
+// per workgroup: the key rows are staged with coalesced 16-byte loads (16 in
+// flight per thread) into LDS rows padded to 528 bytes (conflict-free 16-byte
+// reads at a row stride), then thread t scores key t for every query of the
+// chunk, heads in order, d in order.
+constexpr int IDF_KEYS = 128, IDF_NT = 128, IDF_ROWB = 528, IDF_BATCH = 16;
+
+__device__ __forceinline__ float half_bits_to_f32(uint32_t bits16, int dt) {
+  return dt == LA_BF16 ? bf16_bits_to_f32(bits16) : __half2float(__ushort_as_half((uint16_t)bits16));
+}
+
+__global__ __launch_bounds__(IDF_NT) void indexer_decode16_kernel(IdxKP p) {
+  __shared__ __align__(16) unsigned char sk[IDF_KEYS * IDF_ROWB];
+  __shared__ double sqd[ID_MAXQ][ID_MAXHD];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t k0 = (int64_t)blockIdx.x * IDF_KEYS;
+  const int hd = (int)(p.HI * p.d);
+  const int cpr = hd / 8;  // 16-byte chunks per key row
+  for (int i = tid; i < p.tn * hd; i += IDF_NT) {
+    const int tl = i / hd, c = i % hd;
+    const int h = c / (int)p.d, dd = c % (int)p.d;
+    sqd[tl][c] = load_as_f64(p.q, b * p.q_sb + (p.t0 + tl) * p.q_st + h * p.q_sh + dd, p.dt);
+  }
+  const uint16_t *kb = (const uint16_t *)p.k + b * p.k_sb;
+  const int total = IDF_KEYS * cpr;
+  for (int base = 0; base < total; base += IDF_NT * IDF_BATCH) {
+    uint4 v[IDF_BATCH];
+#pragma unroll
+    for (int u = 0; u < IDF_BATCH; ++u) {
+      const int c = base + u * IDF_NT + tid;
+      const int r = c / cpr, col = c % cpr;
+      const int64_t s = k0 + r;
+      v[u] = (c < total && s < p.Tk) ? *(const uint4 *)(kb + s * p.k_st + col * 8) : uint4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < IDF_BATCH; ++u) {
+      const int c = base + u * IDF_NT + tid;
+      if (c < total) *(uint4 *)(sk + (c / cpr) * IDF_ROWB + (c % cpr) * 16) = v[u];
+    }
+  }
+  __syncthreads();
+  const int64_t s = k0 + tid;
+  if (s >= p.Tk) return;
+  const unsigned char *row = sk + tid * IDF_ROWB;
+  for (int tl = 0; tl < p.tn; ++tl) {
+    const int64_t t = p.t0 + tl;
+    double acc = 0.0;
+    for (int h = 0; h < p.HI; ++h) {
+      double dot = 0.0;
+      for (int dd = 0; dd < p.d; dd += 8) {
+        const uint4 kv = *(const uint4 *)(row + (h * p.d + dd) * 2);
+        const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+        const double *qv = &sqd[tl][h * p.d + dd];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dot = __builtin_fma(qv[2 * e], (double)half_bits_to_f32(w4[e] & 0xffffu, p.dt), dot);
+          dot = __builtin_fma(qv[2 * e + 1], (double)half_bits_to_f32(w4[e] >> 16, p.dt), dot);
+        }
+      }
+      const double rl = dot > 0.0 ? dot : 0.0;
+      acc = add_product(acc, (double)p.w[b * p.w_sb + t * p.w_st + h * p.w_sh], rl);
+    }
+    p.scores[(b * p.tn + tl) * p.Tk + s] = acc;
+  }
+}
+
 static int64_t pick_chunk(const la_indexer_args *a) {
   if (a->q_chunk > 0) return std::min(a->q_chunk, a->Tq);
   const int64_t budget = (int64_t)1 << 30;  // 1 GiB of fp64 scores per pass
@@ -209,21 +277,52 @@ static int validate(const la_indexer_args *a) {
 
 using namespace la;
 
+// Top-k parameters for the queries [t0, t0 + tn) whose scores are in `scores`.
+static TopkKParams topk_params(const la_indexer_args *a, double *scores, int64_t t0, int64_t tn) {
+  TopkKParams tp{};
+  tp.scores = scores;
+  tp.row_stride = a->Tk;
+  tp.G = 1;
+  tp.Tq = tn;
+  tp.NG = a->B * tn;
+  tp.t_base = t0;
+  tp.out_tq = a->Tq;
+  tp.n = a->Tk;
+  tp.k = a->k;
+  tp.width = a->k;
+  tp.pos_off = a->causal ? a->offset : 0;
+  tp.pos_unit = a->causal ? std::max<int64_t>(1, a->causal_unit) : 0;
+  tp.order = 0;
+  tp.out_idx = a->out_idx;
+  tp.out_val = a->out_val;
+  return tp;
+}
+
+static int64_t scores_bytes(const la_indexer_args *a, int64_t chunk) {
+  return (a->B * chunk * a->Tk * 8 + 255) / 256 * 256;
+}
+
 extern "C" size_t la_indexer_topk_workspace(const la_indexer_args *a) {
   if (validate(a) != LA_OK) return 0;
-  return (size_t)(a->B * pick_chunk(a) * a->Tk * 8);
+  const int64_t chunk = pick_chunk(a);
+  return (size_t)(scores_bytes(a, chunk) + topk_workspace_bytes(topk_params(a, nullptr, 0, chunk)));
 }
 
 extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
   int rc = validate(a);
   if (rc != LA_OK) return rc;
   const int64_t chunk = pick_chunk(a);
-  const size_t need = (size_t)(a->B * chunk * a->Tk * 8);
+  const int64_t sc_bytes = scores_bytes(a, chunk);
+  const size_t need = (size_t)(sc_bytes + topk_workspace_bytes(topk_params(a, nullptr, 0, chunk)));
   if (!a->workspace || (size_t)a->ws_bytes < need)
     return fail(LA_ERR_WORKSPACE, "la_indexer_topk: workspace %lld < %zu bytes",
                 (long long)a->ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   const bool decode = a->Tq <= ID_MAXQ && a->HI * a->d <= ID_MAXHD;
+  // fast decode form: 2-byte keys, (head, dim) block contiguous and 16-byte aligned
+  const bool decode16 = decode && (a->in_dtype == LA_BF16 || a->in_dtype == LA_F16) &&
+                        a->k_sh == a->d && a->d % 8 == 0 && a->k_st % 8 == 0 &&
+                        a->k_sb % 8 == 0 && (uintptr_t)a->kk % 16 == 0;
   for (int64_t t0 = 0; t0 < a->Tq; t0 += chunk) {
     IdxKP p{};
     p.q = a->q;
@@ -244,7 +343,10 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     p.dt = a->in_dtype;
     p.causal = a->causal;
     p.unit = std::max<int64_t>(1, a->causal_unit);
-    if (decode) {
+    if (decode16) {
+      indexer_decode16_kernel<<<dim3((unsigned)ceil_div(a->Tk, IDF_KEYS), (unsigned)a->B), IDF_NT,
+                                0, st>>>(p);
+    } else if (decode) {
       indexer_decode_kernel<<<dim3((unsigned)ceil_div(a->Tk, ID_KEYS), (unsigned)a->B), 256, 0,
                               st>>>(p);
     } else {
@@ -253,23 +355,8 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
                             IT_NT, 0, st>>>(p);
     }
     LA_LAUNCHED();
-    TopkKParams tp{};
-    tp.scores = p.scores;
-    tp.row_stride = a->Tk;
-    tp.G = 1;
-    tp.Tq = p.tn;
-    tp.NG = a->B * p.tn;
-    tp.t_base = t0;
-    tp.out_tq = a->Tq;
-    tp.n = a->Tk;
-    tp.k = a->k;
-    tp.width = a->k;
-    tp.pos_off = a->causal ? a->offset : 0;
-    tp.pos_unit = a->causal ? std::max<int64_t>(1, a->causal_unit) : 0;
-    tp.order = 0;
-    tp.out_idx = a->out_idx;
-    tp.out_val = a->out_val;
-    rc = topk_launch(tp, st);
+    rc = topk_launch_ws(topk_params(a, p.scores, t0, p.tn), (char *)a->workspace + sc_bytes,
+                        a->ws_bytes - sc_bytes, st);
     if (rc != LA_OK) return rc;
   }
   return LA_OK;

@@ -12,12 +12,15 @@
 // (kernels/triton/quest_pages.py:58-78) and indexer_topk_torch
 // (kernels/triton/fused_indexer.py:63-73).  torch.topk leaves tie order
 // unspecified; here ties go to the lowest index.
+#include <algorithm>
+
 #include "topk.h"
 
 namespace la {
 
 constexpr int TK_NT = 256;
 constexpr int TK_NW = TK_NT / 64;
+constexpr int TK_BATCH = 8;  // keys read per thread before they are used
 
 struct TkShared {
   uint32_t hist[256];
@@ -84,9 +87,20 @@ __device__ void tk_select(const RowKeys &key, int64_t n_v, int64_t K, TkShared &
     for (int shift = 56; shift >= 0; shift -= 8) {
       sh.hist[tid] = 0;
       __syncthreads();
-      for (int64_t i = tid; i < n_v; i += TK_NT) {
-        const uint64_t u = key(i);
-        if ((u & mask) == prefix) atomicAdd(&sh.hist[(u >> shift) & 255u], 1u);
+      // TK_BATCH keys per thread are read before any is counted (memory-level
+      // parallelism when the keys come from global memory)
+      for (int64_t base = tid; base < n_v; base += TK_NT * TK_BATCH) {
+        uint64_t u[TK_BATCH];
+#pragma unroll
+        for (int e = 0; e < TK_BATCH; ++e) {
+          const int64_t i = base + e * TK_NT;
+          u[e] = i < n_v ? key(i) : 0ull;
+        }
+#pragma unroll
+        for (int e = 0; e < TK_BATCH; ++e) {
+          const int64_t i = base + e * TK_NT;
+          if (i < n_v && (u[e] & mask) == prefix) atomicAdd(&sh.hist[(u[e] >> shift) & 255u], 1u);
+        }
       }
       __syncthreads();
       const uint32_t c = sh.hist[255 - tid];
@@ -114,10 +128,20 @@ __device__ void tk_select(const RowKeys &key, int64_t n_v, int64_t K, TkShared &
   const int64_t beg = (int64_t)w * per;
   const int64_t end = min(n_v, beg + per);
   uint32_t c_gt = 0, c_eq = 0;
-  for (int64_t i = beg + lane; i < end; i += 64) {
-    const uint64_t um = key(i) & mask;
-    c_gt += um > prefix;
-    c_eq += um == prefix;
+  for (int64_t base = beg + lane; base < end; base += 64 * TK_BATCH) {
+    uint64_t u[TK_BATCH];
+#pragma unroll
+    for (int e = 0; e < TK_BATCH; ++e) {
+      const int64_t i = base + e * 64;
+      u[e] = i < end ? key(i) : 0ull;
+    }
+#pragma unroll
+    for (int e = 0; e < TK_BATCH; ++e) {
+      const int64_t i = base + e * 64;
+      const uint64_t um = u[e] & mask;
+      c_gt += (i < end) && um > prefix;
+      c_eq += (i < end) && um == prefix;
+    }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -141,19 +165,28 @@ __device__ void tk_select(const RowKeys &key, int64_t n_v, int64_t K, TkShared &
   __syncthreads();
   const uint64_t lt = lanemask_lt(lane);
   uint32_t eq_seen = eq_before, pos = sel_before;
-  for (int64_t base = beg; base < end; base += 64) {
-    const int64_t i = base + lane;
-    const bool valid = i < end;
-    const uint64_t um = valid ? (key(i) & mask) : 0ull;
-    const bool is_gt = valid && um > prefix;
-    const bool is_eq = valid && um == prefix;
-    const uint64_t em = __ballot(is_eq);
-    const uint32_t rank = eq_seen + (uint32_t)__popcll(em & lt);
-    const bool take = is_gt || (is_eq && (all_in || rank < need));
-    const uint64_t tm = __ballot(take);
-    if (take) emit(i, pos + (uint32_t)__popcll(tm & lt));
-    eq_seen += (uint32_t)__popcll(em);
-    pos += (uint32_t)__popcll(tm);
+  for (int64_t base0 = beg; base0 < end; base0 += 64 * TK_BATCH) {
+    uint64_t u[TK_BATCH];
+#pragma unroll
+    for (int e = 0; e < TK_BATCH; ++e) {
+      const int64_t i = base0 + e * 64 + lane;
+      u[e] = i < end ? key(i) : 0ull;
+    }
+#pragma unroll
+    for (int e = 0; e < TK_BATCH; ++e) {
+      const int64_t i = base0 + e * 64 + lane;
+      const bool valid = i < end;
+      const uint64_t um = u[e] & mask;
+      const bool is_gt = valid && um > prefix;
+      const bool is_eq = valid && um == prefix;
+      const uint64_t em = __ballot(is_eq);
+      const uint32_t rank = eq_seen + (uint32_t)__popcll(em & lt);
+      const bool take = is_gt || (is_eq && (all_in || rank < need));
+      const uint64_t tm = __ballot(take);
+      if (take) emit(i, pos + (uint32_t)__popcll(tm & lt));
+      eq_seen += (uint32_t)__popcll(em);
+      pos += (uint32_t)__popcll(tm);
+    }
   }
   __syncthreads();
 }
@@ -161,11 +194,14 @@ __device__ void tk_select(const RowKeys &key, int64_t n_v, int64_t K, TkShared &
 __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ TkShared sh;
-  const int64_t gi = blockIdx.x;
   const int tid = threadIdx.x;
-  const int64_t tl = gi % p.Tq;
+  // Segmented mode: workgroup gi handles segment gi % nseg of row gi / nseg.
+  const int64_t br = p.seg_len > 0 ? (int64_t)blockIdx.x / p.nseg : (int64_t)blockIdx.x;
+  const int64_t seg = p.seg_len > 0 ? (int64_t)blockIdx.x % p.nseg : 0;
+  const int64_t seg0 = seg * p.seg_len;
+  const int64_t tl = br % p.Tq;
   const int64_t t = tl + p.t_base;
-  const int64_t orow = (gi / p.Tq) * p.out_tq + t;
+  const int64_t orow = p.seg_len > 0 ? (int64_t)blockIdx.x : (br / p.Tq) * p.out_tq + t;
   int64_t n_v = p.n;
   int64_t own = -1;
   if (p.pos_unit > 0) {
@@ -176,6 +212,7 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
   }
   if (p.n_valid_tab) n_v = min(p.n, (int64_t)p.n_valid_tab[t]);
   if (p.own_tab) own = (int64_t)p.own_tab[t];
+  if (p.seg_len > 0) n_v = min(n_v - seg0, min(p.seg_len, p.n - seg0));
   n_v = max(n_v, (int64_t)0);
   const bool force = p.force_own && own >= 0 && own < n_v;
   const int64_t K = min(p.k, n_v);
@@ -184,7 +221,7 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
   uint64_t *lkeys = nullptr;
   if (p.lds_keys) {
     lkeys = (uint64_t *)ptr;
-    ptr += ((p.n * 8 + 15) / 16) * 16;
+    ptr += ((p.n_lds * 8 + 15) / 16) * 16;
   }
   int32_t *sel = nullptr;
   uint64_t *skey = nullptr;  // keys of sel[], kept beside them for the sort
@@ -199,11 +236,23 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
   __syncthreads();
 
   for (int64_t j = 0; j < p.G; ++j) {
-    const int64_t row = ((gi / p.Tq) * p.G + j) * p.Tq + tl;
-    const double *rp = p.scores + row * p.row_stride;
+    const int64_t row = ((br / p.Tq) * p.G + j) * p.Tq + tl;
+    const double *rp = p.scores + row * p.row_stride + seg0;
+    const int32_t *cand = p.cand_idx ? p.cand_idx + row * p.row_stride + seg0 : nullptr;
     if (lkeys) {
-      for (int64_t i = tid; i < n_v; i += TK_NT)
-        lkeys[i] = (force && i == own) ? KEY_FORCED : ord_key(rp[i]);
+      for (int64_t base = tid; base < n_v; base += TK_NT * TK_BATCH) {
+        double v[TK_BATCH];
+#pragma unroll
+        for (int e = 0; e < TK_BATCH; ++e) {
+          const int64_t i = base + e * TK_NT;
+          v[e] = i < n_v ? rp[i] : 0.0;
+        }
+#pragma unroll
+        for (int e = 0; e < TK_BATCH; ++e) {
+          const int64_t i = base + e * TK_NT;
+          if (i < n_v) lkeys[i] = (force && i == own) ? KEY_FORCED : ord_key(v[e]);
+        }
+      }
       __syncthreads();
     }
     const RowKeys key{rp, lkeys, own, force};
@@ -245,17 +294,31 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
           __syncthreads();
         }
       }
+      // Candidate rows carry the original index of every slot; padding slots
+      // (index -1) hold the lowest key, so they sort after every real one and
+      // the first of them ends the list.
+      if (tid == 0) sh.above = (uint32_t)K;
+      __syncthreads();
       int32_t *oi = p.out_idx + orow * p.width;
       for (int64_t jj = tid; jj < p.width; jj += TK_NT) {
-        const int32_t s = jj < K ? sel[jj] : -1;
-        oi[jj] = s;
+        int32_t s = jj < K ? sel[jj] : -1;
+        int32_t id = s;
+        if (cand && s >= 0) {
+          id = cand[s];
+          if (id < 0) {
+            s = -1;
+            atomicMin(&sh.above, (uint32_t)jj);
+          }
+        }
+        oi[jj] = id;
         if (p.out_val) {
           float v = __int_as_float(0xff800000);
           if (s >= 0) v = (force && s == own) ? __int_as_float(0x7f800000) : (float)rp[s];
           p.out_val[orow * p.width + jj] = v;
         }
       }
-      if (p.out_count && tid == 0) p.out_count[orow] = (int32_t)K;
+      __syncthreads();
+      if (p.out_count && tid == 0) p.out_count[orow] = (int32_t)sh.above;
       __syncthreads();
     }
   }
@@ -299,7 +362,7 @@ static int64_t align16(int64_t x) { return (x + 15) / 16 * 16; }
 
 int64_t topk_lds_bytes(const TopkKParams &p) {
   int64_t b = 0;
-  if (p.lds_keys) b += align16(p.n * 8);
+  if (p.lds_keys) b += align16(p.n_lds * 8);
   if (p.use_bitmap)
     b += align16(p.bitmap_words * 4);
   else
@@ -321,10 +384,139 @@ static int max_dynamic_lds() {
   return cached;
 }
 
+// Gather the segment winners into candidate rows: slot (row, seg*k + j) gets
+// the score and the original index of winner j of segment seg, or padding
+// (lowest key, index -1).
+// Segments are laid out in order and winners in increasing position, so slot
+// order is original-index order and position ties keep the lowest-index rule.
+__global__ __launch_bounds__(256) void topk_gather_kernel(
+    const double *scores, int64_t row_stride, const int32_t *prev_idx, const int32_t *win,
+    const int32_t *win_count, int64_t nseg, int64_t seg_len, int64_t k, double *cand_sc,
+    int32_t *cand_id) {
+  const int64_t g = blockIdx.x;  // (row, seg)
+  const int64_t row = g / nseg, seg = g % nseg;
+  const int64_t cnt = win_count[g];
+  const int64_t n_c = nseg * k;
+  for (int64_t j = threadIdx.x; j < k; j += blockDim.x) {
+    const int32_t pos = j < cnt ? win[g * k + j] : -1;
+    // padding: the all-ones pattern maps to key 0, below every real score
+    double s = __longlong_as_double((long long)0xffffffffffffffffull);
+    int32_t id = -1;
+    if (pos >= 0) {
+      const int64_t src = seg * seg_len + pos;
+      s = scores[row * row_stride + src];
+      id = prev_idx ? prev_idx[row * row_stride + src] : (int32_t)src;
+    }
+    cand_sc[row * n_c + seg * k + j] = s;
+    cand_id[row * n_c + seg * k + j] = id;
+  }
+}
+
+struct LongPlan {
+  int64_t levels = 0;    // segmented levels before the final select
+  int64_t seg_len = 0;
+  int64_t n[4] = {0, 0, 0, 0};  // row length at each level (n[levels] is final)
+  int64_t bytes = 0;
+};
+
+static int64_t lds_limit() { return (int64_t)max_dynamic_lds() - (int64_t)sizeof(TkShared) - 256; }
+
+// Long rows (keys + sort buffer beyond LDS) of a plain sorted top-k are
+// reduced in segments that fit the LDS; each level keeps k per segment.
+static LongPlan long_plan(const TopkKParams &p) {
+  LongPlan L;
+  const bool plain = p.G == 1 && p.sink == 0 && p.window == 0 && p.order == 0 && !p.force_own &&
+                     !p.cand_idx && p.seg_len == 0;
+  int64_t p2 = 1;
+  while (p2 < p.k) p2 <<= 1;
+  const int64_t limit = lds_limit();
+  if (!plain || p.n * 8 + p2 * 12 + 64 <= limit) return L;
+  int64_t seg = 1;
+  while ((seg * 2) * 8 + (seg * 2) / 8 + 64 <= limit) seg *= 2;
+  if (p.k * 2 > seg) return L;  // segments would not shrink the rows
+  int64_t n = p.n;
+  L.seg_len = seg;
+  L.n[0] = n;
+  while (n * 8 + p2 * 12 + 64 > limit && L.levels < 3) {
+    const int64_t nseg = (n + seg - 1) / seg;
+    const int64_t n_next = nseg * p.k;
+    // winners (positions + counts) and candidate rows (fp64 score + int32 index)
+    L.bytes += align16(p.NG * nseg * p.k * 4) + align16(p.NG * nseg * 4) +
+               align16(p.NG * n_next * 8) + align16(p.NG * n_next * 4);
+    n = n_next;
+    L.n[++L.levels] = n;
+  }
+  if (n * 8 + p2 * 12 + 64 > limit) L.levels = -1;  // would not converge
+  return L;
+}
+
+int64_t topk_workspace_bytes(const TopkKParams &p) {
+  const LongPlan L = long_plan(p);
+  return L.levels > 0 ? L.bytes : 0;
+}
+
+int topk_launch_ws(TopkKParams p, void *ws, int64_t ws_bytes, hipStream_t st) {
+  const LongPlan L = long_plan(p);
+  if (L.levels <= 0) return topk_launch(p, st);
+  if (!ws || ws_bytes < L.bytes)
+    return fail(LA_ERR_WORKSPACE, "topk: long rows need %lld workspace bytes",
+                (long long)L.bytes);
+  char *w = (char *)ws;
+  const double *src_sc = p.scores;
+  int64_t src_stride = p.row_stride;
+  const int32_t *src_id = nullptr;
+  for (int64_t lev = 0; lev < L.levels; ++lev) {
+    const int64_t n = L.n[lev];
+    const int64_t nseg = (n + L.seg_len - 1) / L.seg_len;
+    const int64_t n_next = L.n[lev + 1];
+    int32_t *win = (int32_t *)w;
+    w += align16(p.NG * nseg * p.k * 4);
+    int32_t *cnt = (int32_t *)w;
+    w += align16(p.NG * nseg * 4);
+    double *csc = (double *)w;
+    w += align16(p.NG * n_next * 8);
+    int32_t *cid = (int32_t *)w;
+    w += align16(p.NG * n_next * 4);
+    TopkKParams s = p;
+    s.scores = src_sc;
+    s.row_stride = src_stride;
+    s.n = n;
+    s.width = p.k;
+    s.order = 1;
+    s.out_idx = win;
+    s.out_val = nullptr;
+    s.out_count = cnt;
+    s.seg_len = L.seg_len;
+    s.nseg = nseg;
+    s.NG = p.NG * nseg;
+    if (lev > 0) {  // candidate rows: every slot is valid (padding is -inf)
+      s.pos_unit = 0;
+      s.n_valid_tab = nullptr;
+    }
+    int rc = topk_launch(s, st);
+    if (rc != LA_OK) return rc;
+    topk_gather_kernel<<<dim3((unsigned)(p.NG * nseg)), 256, 0, st>>>(
+        src_sc, src_stride, src_id, win, cnt, nseg, L.seg_len, p.k, csc, cid);
+    LA_LAUNCHED();
+    src_sc = csc;
+    src_stride = n_next;
+    src_id = cid;
+  }
+  TopkKParams f = p;
+  f.scores = src_sc;
+  f.row_stride = src_stride;
+  f.n = L.n[L.levels];
+  f.pos_unit = 0;
+  f.n_valid_tab = nullptr;
+  f.cand_idx = src_id;
+  return topk_launch(f, st);
+}
+
 int topk_launch(TopkKParams p, hipStream_t st) {
   if (p.NG <= 0) return LA_OK;
   p.use_bitmap = (p.G > 1 || p.sink > 0 || p.window > 0 || p.order == 1) ? 1 : 0;
-  p.bitmap_words = (p.n + 31) / 32;
+  p.n_lds = p.seg_len > 0 ? std::min(p.seg_len, p.n) : p.n;
+  p.bitmap_words = (p.n_lds + 31) / 32;
   int64_t p2 = 1;
   while (p2 < p.k) p2 <<= 1;
   p.p2k = p2;
@@ -355,21 +547,7 @@ int topk_launch(TopkKParams p, hipStream_t st) {
 
 using namespace la;
 
-extern "C" size_t la_topk_rows_workspace(const la_topk_args *) { return 0; }
-
-extern "C" int la_topk_rows(const la_topk_args *a, void *stream) {
-  LA_REQUIRE(a && a->scores && a->out_idx, "la_topk_rows: null pointer");
-  LA_REQUIRE(a->B > 0 && a->H > 0 && a->Tq > 0 && a->n > 0, "la_topk_rows: bad shape");
-  LA_REQUIRE(a->row_stride >= a->n, "la_topk_rows: row_stride < n");
-  LA_REQUIRE(a->group >= 1 && a->H % a->group == 0, "la_topk_rows: H must be a multiple of group");
-  LA_REQUIRE(a->k >= 1 && a->width >= 1, "la_topk_rows: k and width must be >= 1");
-  LA_REQUIRE(a->order == 0 || a->order == 1, "la_topk_rows: order must be 0 or 1");
-  const bool bitmap = a->group > 1 || a->sink_units > 0 || a->window_units > 0 || a->order == 1;
-  LA_REQUIRE(!(bitmap && a->out_val), "la_topk_rows: values are only produced for order 0");
-  LA_REQUIRE(!(a->order == 0 && bitmap), "la_topk_rows: union/sink/window need order 1");
-  if (a->order == 0) LA_REQUIRE(a->width >= a->k, "la_topk_rows: width < k");
-  if (a->window_units > 0 || a->force_own)
-    LA_REQUIRE(a->own != nullptr || a->pos_unit > 0, "la_topk_rows: window/force_own need own[]");
+static TopkKParams params_from_args(const la_topk_args *a) {
   TopkKParams p{};
   p.scores = a->scores;
   p.row_stride = a->row_stride;
@@ -392,5 +570,32 @@ extern "C" int la_topk_rows(const la_topk_args *a, void *stream) {
   p.out_idx = a->out_idx;
   p.out_val = a->out_val;
   p.out_count = a->out_count;
-  return topk_launch(p, (hipStream_t)stream);
+  return p;
+}
+
+static int validate(const la_topk_args *a) {
+  LA_REQUIRE(a && a->scores && a->out_idx, "la_topk_rows: null pointer");
+  LA_REQUIRE(a->B > 0 && a->H > 0 && a->Tq > 0 && a->n > 0, "la_topk_rows: bad shape");
+  LA_REQUIRE(a->row_stride >= a->n, "la_topk_rows: row_stride < n");
+  LA_REQUIRE(a->group >= 1 && a->H % a->group == 0, "la_topk_rows: H must be a multiple of group");
+  LA_REQUIRE(a->k >= 1 && a->width >= 1, "la_topk_rows: k and width must be >= 1");
+  LA_REQUIRE(a->order == 0 || a->order == 1, "la_topk_rows: order must be 0 or 1");
+  const bool bitmap = a->group > 1 || a->sink_units > 0 || a->window_units > 0 || a->order == 1;
+  LA_REQUIRE(!(bitmap && a->out_val), "la_topk_rows: values are only produced for order 0");
+  LA_REQUIRE(!(a->order == 0 && bitmap), "la_topk_rows: union/sink/window need order 1");
+  if (a->order == 0) LA_REQUIRE(a->width >= a->k, "la_topk_rows: width < k");
+  if (a->window_units > 0 || a->force_own)
+    LA_REQUIRE(a->own != nullptr || a->pos_unit > 0, "la_topk_rows: window/force_own need own[]");
+  return LA_OK;
+}
+
+extern "C" size_t la_topk_rows_workspace(const la_topk_args *a) {
+  if (validate(a) != LA_OK) return 0;
+  return (size_t)topk_workspace_bytes(params_from_args(a));
+}
+
+extern "C" int la_topk_rows(const la_topk_args *a, void *stream) {
+  const int rc = validate(a);
+  if (rc != LA_OK) return rc;
+  return topk_launch_ws(params_from_args(a), a->workspace, a->ws_bytes, (hipStream_t)stream);
 }

@@ -127,7 +127,11 @@ def _topk(scores: torch.Tensor, *, k: int, width: int, group: int, order: int,
     a.sink_units, a.window_units = sink, window
     a.pos_offset, a.pos_unit = pos_offset, pos_unit
     a.force_own, a.order = int(force_own), order
-    N.check(N.load().la_topk_rows(ctypes.byref(a), N.stream_handle(dev)), "top-k")
+    L = N.load()
+    ws_bytes = L.la_topk_rows_workspace(ctypes.byref(a))
+    ws = N.workspace(ws_bytes, dev)
+    a.workspace, a.ws_bytes = N.ptr(ws), ws_bytes
+    N.check(L.la_topk_rows(ctypes.byref(a), N.stream_handle(dev)), "top-k")
     return ids, counts, vals
 
 

@@ -1,0 +1,45 @@
+"""The row top-k kernel alone against the oracle's ranking (value desc, index
+asc), on rows built to stress it: heavy exact ties, short valid prefixes, and
+rows longer than one workgroup's LDS (selected in segments)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from linattn_amd.kernels.quest_pages import _topk
+
+pytestmark = pytest.mark.gpu
+
+
+def run(scores, k, *, pos_offset=0, pos_unit=0):
+    B, H, Tq, n = scores.shape
+    ids, counts, vals = _topk(scores, k=k, width=k, group=1, order=0, pos_offset=pos_offset,
+                              pos_unit=pos_unit, force_own=False, with_values=True)
+    return ids, vals
+
+
+@pytest.mark.parametrize("n,k", [(1000, 100), (8192, 2048), (40000, 3000), (131072, 4096)])
+def test_topk_ties_and_prefixes(dev, n, k):
+    g = torch.Generator().manual_seed(n)
+    # integer-valued scores: ~n/7 exact ties per value
+    sc = torch.randint(-3, 4, (1, 1, 3, n), generator=g).double()
+    sc[0, 0, 1] = torch.randn(n, generator=g, dtype=torch.float64)  # a tie-free row
+    sc[0, 0, 2, ::3] = 0.0
+    pos_offset = n - 2  # rows t = 0, 1, 2 see n - 1, n, n keys (causal prefix)
+    ids, vals = run(sc.to(dev), k, pos_offset=pos_offset, pos_unit=1)
+    nv = np.minimum(n, np.arange(3) + pos_offset + 1)
+    ri, rv = oracle.topk_rows(sc[0, 0].numpy(), k, n_valid=nv)
+    assert np.array_equal(ids[0, 0].cpu().numpy(), ri)
+    assert np.array_equal(vals[0, 0].cpu().numpy(), rv.astype(np.float32))
+
+
+def test_topk_short_rows_pad(dev):
+    sc = torch.randn(1, 2, 5, 300, dtype=torch.float64)
+    ids, vals = run(sc.to(dev), 64, pos_offset=0, pos_unit=8)  # t visible units: t//8 + 1
+    for h in range(2):
+        ri, rv = oracle.topk_rows(sc[0, h].numpy(), 64, n_valid=np.arange(5) // 8 + 1)
+        assert np.array_equal(ids[0, h].cpu().numpy(), ri)
+    assert (ids[0, :, :, 1:] == -1).all()
