@@ -2,6 +2,8 @@
 //
 // page bounds : quest_pages.py:38-48 (page_bounds_torch), selection.py:181-201
 // page scores : quest_pages.py:51-55 (page_scores_torch), selection.py:203-212
+#include <type_traits>
+
 #include "common.h"
 #include "kv_access.h"
 
@@ -32,6 +34,80 @@ __global__ __launch_bounds__(256) void page_bounds_kernel(la_kv kv, int64_t Hkv,
     const int64_t o = b * m_sb + h * m_sh + p * m_sp + d * m_sd;
     store_from_f32(mn, o, meta_dt, lo);
     store_from_f32(mx, o, meta_dt, hi);
+  }
+}
+
+// Vector form: each thread reads 16-byte chunks of the page's key rows (LPR
+// lanes per row, all rows of the page in flight at once), keeps elementwise
+// min / max, and the row groups are folded through LDS.  Needs D % EPL == 0
+// and 16-byte aligned rows; min / max are exact, so the result equals the
+// scalar form bit for bit.
+template <int KT, int D>
+__global__ __launch_bounds__(256) void page_bounds_vec_kernel(la_kv kv, int64_t Hkv, int64_t ps,
+                                                              int64_t first_page, void *mn, void *mx,
+                                                              int64_t m_sb, int64_t m_sh,
+                                                              int64_t m_sp, int64_t m_sd, int meta_dt) {
+  constexpr int ESZ = KT == LA_BF16 ? 2 : 4;
+  constexpr int EPL = 16 / ESZ;
+  constexpr int LPR = D / EPL;   // lanes per key row
+  constexpr int RPI = 256 / LPR; // rows per pass of the workgroup
+  constexpr int UN = 4;          // passes in flight
+  __shared__ float red[2][RPI][D];
+  const int64_t p = first_page + blockIdx.x;
+  const int64_t h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int64_t len = kv_length(kv, b);
+  const int64_t t0 = p * ps;
+  const int64_t n = max((int64_t)0, min(len, t0 + ps) - t0);
+  const int c = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
+  float lo[EPL], hi[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    lo[e] = __int_as_float(0x7f800000);
+    hi[e] = __int_as_float(0xff800000);
+  }
+  const char *kb = (const char *)kv.k;
+  for (int64_t r = r0; r < n; r += RPI * UN) {
+    uint4 v[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int64_t rr = r + u * RPI;
+      v[u] = rr < n ? *(const uint4 *)(kb + (kv_row(kv, b, h, t0 + rr, Hkv, D, false) + c * EPL) * ESZ)
+                    : uint4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      if (r + u * RPI >= n) break;
+      float x[EPL];
+      if constexpr (KT == LA_BF16) {
+        x[0] = bf16lo(v[u].x); x[1] = bf16hi(v[u].x); x[2] = bf16lo(v[u].y); x[3] = bf16hi(v[u].y);
+        x[4] = bf16lo(v[u].z); x[5] = bf16hi(v[u].z); x[6] = bf16lo(v[u].w); x[7] = bf16hi(v[u].w);
+      } else {
+        x[0] = __uint_as_float(v[u].x); x[1] = __uint_as_float(v[u].y);
+        x[2] = __uint_as_float(v[u].z); x[3] = __uint_as_float(v[u].w);
+      }
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        lo[e] = fminf(lo[e], x[e]);
+        hi[e] = fmaxf(hi[e], x[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    red[0][r0][c * EPL + e] = lo[e];
+    red[1][r0][c * EPL + e] = hi[e];
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float a = red[0][0][d], z = red[1][0][d];
+    for (int i = 1; i < RPI; ++i) {
+      a = fminf(a, red[0][i][d]);
+      z = fmaxf(z, red[1][i][d]);
+    }
+    const int64_t o = b * m_sb + h * m_sh + p * m_sp + d * m_sd;
+    store_from_f32(mn, o, meta_dt, a);
+    store_from_f32(mx, o, meta_dt, z);
   }
 }
 
@@ -75,28 +151,46 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
   };
   if (VEC && p0 + PPT <= n_pages) {
     static_assert(PPT == 4, "vector path loads 4 pages");
-    if constexpr (MT == LA_BF16) {
-      const uint16_t *pl = (const uint16_t *)mn + mbase + p0;
-      const uint16_t *ph = (const uint16_t *)mx + mbase + p0;
-#pragma unroll 8
-      for (int64_t d = 0; d < D; ++d) {
-        const uint2 a = *(const uint2 *)(pl + d * m_sd);
-        const uint2 c = *(const uint2 *)(ph + d * m_sd);
-        const double lo[PPT] = {bf16lo(a.x), bf16hi(a.x), bf16lo(a.y), bf16hi(a.y)};
-        const double hi[PPT] = {bf16lo(c.x), bf16hi(c.x), bf16lo(c.y), bf16hi(c.y)};
-        accumulate(d, lo, hi);
+    // QD dims per batch; the next batch's loads are issued before the current
+    // one is accumulated, so 2*QD loads per array are in flight per thread.
+    constexpr int QD = 8;
+    using V = typename std::conditional<MT == LA_BF16, uint2, float4>::type;
+    const V *pl = (const V *)((const char *)mn + (mbase + p0) * (MT == LA_BF16 ? 2 : 4));
+    const V *ph = (const V *)((const char *)mx + (mbase + p0) * (MT == LA_BF16 ? 2 : 4));
+    const int64_t sd = m_sd / PPT;  // vectors per d step
+    auto widen = [](const V &v, double (&x)[PPT]) {
+      if constexpr (MT == LA_BF16) {
+        x[0] = bf16lo(v.x); x[1] = bf16hi(v.x); x[2] = bf16lo(v.y); x[3] = bf16hi(v.y);
+      } else {
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
       }
-    } else {
-      const float *pl = (const float *)mn + mbase + p0;
-      const float *ph = (const float *)mx + mbase + p0;
-#pragma unroll 8
-      for (int64_t d = 0; d < D; ++d) {
-        const float4 a = *(const float4 *)(pl + d * m_sd);
-        const float4 c = *(const float4 *)(ph + d * m_sd);
-        const double lo[PPT] = {a.x, a.y, a.z, a.w};
-        const double hi[PPT] = {c.x, c.y, c.z, c.w};
-        accumulate(d, lo, hi);
+    };
+    V a[2][QD], c[2][QD];
+    auto fetch = [&](int64_t d0, int buf) {
+#pragma unroll
+      for (int j = 0; j < QD; ++j) {
+        const bool ok = d0 + j < D;
+        a[buf][j] = ok ? pl[(d0 + j) * sd] : V{};
+        c[buf][j] = ok ? ph[(d0 + j) * sd] : V{};
       }
+    };
+    auto consume = [&](int64_t d0, int buf) {
+#pragma unroll
+      for (int j = 0; j < QD; ++j) {
+        if (d0 + j >= D) break;
+        double lo[PPT], hi[PPT];
+        widen(a[buf][j], lo);
+        widen(c[buf][j], hi);
+        accumulate(d0 + j, lo, hi);
+      }
+    };
+    fetch(0, 0);
+    for (int64_t d0 = 0; d0 < D; d0 += 2 * QD) {
+      if (d0 + QD < D) fetch(d0 + QD, 1);
+      consume(d0, 0);
+      if (d0 + QD >= D) break;
+      if (d0 + 2 * QD < D) fetch(d0 + 2 * QD, 0);
+      consume(d0 + QD, 1);
     }
   } else {
     for (int64_t d = 0; d < D; ++d) {
@@ -162,7 +256,22 @@ extern "C" int la_quest_page_bounds(const la_kv *kv, int64_t B, int64_t Hkv, int
   hipStream_t st = (hipStream_t)stream;
   dim3 grid((unsigned)(n_pages - first_page), (unsigned)Hkv, (unsigned)B);
   const int threads = D >= 256 ? 256 : (int)(((D + 63) / 64) * 64);
-  if (kv->dtype == LA_F32)
+  // 16-byte rows: every row offset (pool rows or strides) a multiple of 16 bytes
+  const int64_t esz = kv->dtype == LA_F32 ? 4 : 2;
+  bool vec = (D == 64 || D == 128 || D == 256) && (uintptr_t)kv->k % 16 == 0;
+  if (!kv->page_table)
+    vec = vec && (kv->k_sb * esz) % 16 == 0 && (kv->k_sh * esz) % 16 == 0 && (kv->k_st * esz) % 16 == 0;
+  if (vec) {
+#define LA_PB(KT, DD)                                                                        \
+  page_bounds_vec_kernel<KT, DD><<<grid, 256, 0, st>>>(*kv, Hkv, page_size, first_page, page_min, \
+                                                       page_max, m_sb, m_sh, m_sp, m_sd, meta_dtype)
+    if (kv->dtype == LA_F32) {
+      if (D == 64) LA_PB(LA_F32, 64); else if (D == 128) LA_PB(LA_F32, 128); else LA_PB(LA_F32, 256);
+    } else {
+      if (D == 64) LA_PB(LA_BF16, 64); else if (D == 128) LA_PB(LA_BF16, 128); else LA_PB(LA_BF16, 256);
+    }
+#undef LA_PB
+  } else if (kv->dtype == LA_F32)
     page_bounds_kernel<LA_F32><<<grid, threads, 0, st>>>(*kv, Hkv, D, page_size, first_page, page_min,
                                                          page_max, m_sb, m_sh, m_sp, m_sd, meta_dtype);
   else

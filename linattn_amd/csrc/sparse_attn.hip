@@ -81,6 +81,134 @@ __device__ __forceinline__ void unpack(const typename KvTraits<KT>::Vec &v, floa
   }
 }
 
+// Work of one (row, split): which list entries it covers and where the
+// row's K/V live.  Row r = (b, list head ih, query t).
+struct RowCtx {
+  int64_t b, t, kvh, h0, e0, ne, lim;
+  int64_t k_bh, v_bh, s_bh;  // contiguous-layout bases
+};
+
+// Decodes the row of this workgroup and stages its split's entries in LDS:
+// the logical first token (for masking; -1 = skip) and, for a paged cache,
+// the pool row of that token, so a token costs no page-table lookup.  The
+// caller synchronises before reading the staged entries.
+template <int G, bool PAGED>
+__device__ __forceinline__ RowCtx stage_row(const AttnKP &p, int32_t *s_tok0, int32_t *s_phys) {
+  RowCtx rc;
+  const int tid = threadIdx.x;
+  const int64_t r = blockIdx.y;
+  const int64_t split = blockIdx.x;
+  rc.t = r % p.Tq;
+  const int64_t ih = (r / p.Tq) % p.ids_heads;
+  rc.b = r / (p.Tq * p.ids_heads);
+  const int64_t grp = p.Hq / p.Hkv;
+  rc.kvh = (p.ids_heads == p.Hkv) ? ih : ih / grp;
+  rc.h0 = (p.ids_heads == p.Hkv) ? ih * G : ih;  // first query head
+  const int64_t lrow = (p.ids_rows == 1) ? 0 : rc.t;
+  const int32_t *list = p.ids + rc.b * p.id_sb + ih * p.id_sh + lrow * p.id_st;
+  int64_t n_e = p.N;
+  if (p.counts) n_e = min(n_e, (int64_t)p.counts[(rc.b * p.ids_heads + ih) * p.ids_rows + lrow]);
+  // the row's valid entries are spread evenly over the splits
+  const int64_t eps = (n_e + p.splits - 1) / p.splits;
+  rc.e0 = split * eps;
+  const int64_t e1 = min(n_e, rc.e0 + eps);
+  rc.ne = max((int64_t)0, e1 - rc.e0);
+  const int64_t len = kv_length(p.kv, rc.b);
+  const int64_t qpos = p.causal ? (p.offset + rc.t) : (int64_t)0x7fffffffffffffffLL;
+  rc.lim = min(len - 1, qpos);  // last attendable token
+  for (int64_t e = tid; e < rc.ne; e += SA_NT) {
+    const int32_t id = list[rc.e0 + e];
+    const int64_t tok0 = (int64_t)id * p.unit;
+    const bool ok = id >= 0 && tok0 <= rc.lim;
+    s_tok0[e] = ok ? (int32_t)tok0 : -1;
+    if constexpr (PAGED) {
+      if (p.staged && ok) {
+        const int64_t ps = p.kv.page_size;
+        const int64_t phys = p.kv.page_table[rc.b * p.kv.pt_stride + tok0 / ps];
+        s_phys[e] = (int32_t)((phys * p.Hkv + rc.kvh) * ps + tok0 % ps);
+      }
+    }
+  }
+  rc.k_bh = rc.b * p.kv.k_sb + rc.kvh * p.kv.k_sh;
+  rc.v_bh = rc.b * p.kv.v_sb + rc.kvh * p.kv.v_sh;
+  rc.s_bh = rc.b * p.kv.s_sb + rc.kvh * p.kv.s_sh;
+  return rc;
+}
+
+// Flat token f of the split (entry f / unit, token f % unit of the entry):
+// returns whether it is attended and, if so, the element offsets of its K and
+// V rows and the index of its scale.  Flat indices stay below 2^31 (checked
+// on the host).
+template <int D, bool PAGED>
+__device__ __forceinline__ bool token_rows(const AttnKP &p, const RowCtx &rc, const int32_t *s_tok0,
+                                           const int32_t *s_phys, int32_t f, int32_t F,
+                                           int32_t lim32, int64_t &ko, int64_t &vo, int64_t &so) {
+  int32_t e, j;
+  if (p.unit_shift >= 0) {
+    e = f >> p.unit_shift;
+    j = f & ((1 << p.unit_shift) - 1);
+  } else {
+    e = (int32_t)((uint32_t)f / (uint32_t)p.unit);
+    j = f - e * (int32_t)p.unit;
+  }
+  const int32_t es = min(e, SA_MAX_EPS - 1);
+  const int32_t tok0 = (f < F) ? s_tok0[es] : -1;
+  const int32_t tok = tok0 + j;
+  if (!(tok0 >= 0 && tok <= lim32)) return false;
+  if constexpr (PAGED) {
+    int64_t prow;
+    if (p.staged) {
+      prow = (int64_t)((uint32_t)s_phys[es] + (uint32_t)j);  // pool rows < 2^32
+    } else {
+      const int64_t ps = p.kv.page_size;
+      const int64_t phys = p.kv.page_table[rc.b * p.kv.pt_stride + tok / ps];
+      prow = (phys * p.Hkv + rc.kvh) * ps + tok % ps;
+    }
+    ko = vo = prow * D;
+    so = prow;
+  } else {
+    ko = rc.k_bh + (int64_t)tok * p.kv.k_st;
+    vo = rc.v_bh + (int64_t)tok * p.kv.v_st;
+    so = rc.s_bh + (int64_t)tok * p.kv.s_st;
+  }
+  return true;
+}
+
+// Merges the per-wave softmax states (s_m, s_l, s_acc, filled by every wave
+// before a barrier) and writes the output row, or this split's partial state.
+template <int G, int D>
+__device__ __forceinline__ void finish_row(const AttnKP &p, const RowCtx &rc,
+                                           const float (*s_acc)[G][D], const float (*s_m)[G],
+                                           const float (*s_l)[G]) {
+  const int64_t r = blockIdx.y, split = blockIdx.x;
+  for (int i = threadIdx.x; i < G * D; i += SA_NT) {
+    const int g = i / D, d = i % D;
+    float M = __int_as_float(0xff800000);
+#pragma unroll
+    for (int x = 0; x < SA_NW; ++x) M = fmaxf(M, s_m[x][g]);
+    const float Mu = (M == __int_as_float(0xff800000)) ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int x = 0; x < SA_NW; ++x) {
+      const float sc = fast_exp2(s_m[x][g] - Mu);
+      L += s_l[x][g] * sc;
+      A += s_acc[x][g][d] * sc;
+    }
+    const int64_t h = rc.h0 + g;
+    if (p.splits == 1) {
+      const float o = L > 0.f ? A / L : 0.f;
+      store_from_f32(p.out, rc.b * p.o_sb + h * p.o_sh + rc.t * p.o_st + d, p.out_dt, o);
+    } else {
+      const int64_t pi = (r * G + g) * p.splits + split;
+      p.ws_acc[pi * D + d] = A;
+      if (d == 0) {
+        p.ws_ml[pi * 2 + 0] = M;
+        p.ws_ml[pi * 2 + 1] = L;
+      }
+    }
+  }
+}
+
 template <int KT, int D, int G, int UNR, bool PAGED>
 __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
   using Tr = KvTraits<KT>;
@@ -90,7 +218,7 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
   constexpr int RPI = 64 / LPR;          // rows per wave instruction
   static_assert(LPR >= 1 && LPR <= 64 && 64 % LPR == 0, "row must map onto a wave");
 
-  __shared__ int32_t s_tok0[SA_MAX_EPS];  // logical first token of each entry (-1: skip)
+  __shared__ int32_t s_tok0[SA_MAX_EPS];
   __shared__ int32_t s_phys[PAGED ? SA_MAX_EPS : 1];
   __shared__ float s_acc[SA_NW][G][D];
   __shared__ float s_m[SA_NW][G], s_l[SA_NW][G];
@@ -98,50 +226,14 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = lane % LPR;     // chunk of D this lane owns
   const int slot = lane / LPR;  // row slot within the wave
-  const int64_t r = blockIdx.y;
-  const int64_t split = blockIdx.x;
-  const int64_t t = r % p.Tq;
-  const int64_t ih = (r / p.Tq) % p.ids_heads;
-  const int64_t b = r / (p.Tq * p.ids_heads);
-  const int64_t grp = p.Hq / p.Hkv;
-  const int64_t kvh = (p.ids_heads == p.Hkv) ? ih : ih / grp;
-  const int64_t h0 = (p.ids_heads == p.Hkv) ? ih * G : ih;  // first query head
-  const int64_t lrow = (p.ids_rows == 1) ? 0 : t;
-  const int32_t *list = p.ids + b * p.id_sb + ih * p.id_sh + lrow * p.id_st;
-  int64_t n_e = p.N;
-  if (p.counts) n_e = min(n_e, (int64_t)p.counts[(b * p.ids_heads + ih) * p.ids_rows + lrow]);
-  const int64_t e0 = split * p.eps;
-  const int64_t e1 = min(n_e, e0 + p.eps);
-  const int64_t ne = max((int64_t)0, e1 - e0);
-  const int64_t len = kv_length(p.kv, b);
-  const int64_t qpos = p.causal ? (p.offset + t) : (int64_t)0x7fffffffffffffffLL;
-  const int64_t lim = min(len - 1, qpos);  // last attendable token
-
-  // Stage the split's entries: logical first token (for masking) and, for a
-  // paged cache, the pool row of that token (so a token costs no page lookup).
-  for (int64_t e = tid; e < ne; e += SA_NT) {
-    const int32_t id = list[e0 + e];
-    const int64_t tok0 = (int64_t)id * p.unit;
-    const bool ok = id >= 0 && tok0 <= lim;
-    s_tok0[e] = ok ? (int32_t)tok0 : -1;
-    if constexpr (PAGED) {
-      if (p.staged && ok) {
-        const int64_t ps = p.kv.page_size;
-        const int64_t phys = p.kv.page_table[b * p.kv.pt_stride + tok0 / ps];
-        s_phys[e] = (int32_t)((phys * p.Hkv + kvh) * ps + tok0 % ps);
-      }
-    }
-  }
-  const int64_t k_bh = b * p.kv.k_sb + kvh * p.kv.k_sh;  // contiguous-layout bases
-  const int64_t v_bh = b * p.kv.v_sb + kvh * p.kv.v_sh;
-  const int64_t s_bh = b * p.kv.s_sb + kvh * p.kv.s_sh;
-  const int32_t lim32 = (int32_t)min(lim, (int64_t)0x7fffffff);
+  const RowCtx rc = stage_row<G, PAGED>(p, s_tok0, s_phys);
+  const int32_t lim32 = (int32_t)min(rc.lim, (int64_t)0x7fffffff);
 
   // q chunk of this lane for the G heads, pre-scaled into the log2 domain.
   float qf[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int64_t qo = b * p.q_sb + (h0 + g) * p.q_sh + t * p.q_st + c * EPL;
+    const int64_t qo = rc.b * p.q_sb + (rc.h0 + g) * p.q_sh + rc.t * p.q_st + c * EPL;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) qf[g][e] = load_as_f32(p.q, qo + e, p.q_dt) * p.qscale;
   }
@@ -155,82 +247,44 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
   }
   __syncthreads();
 
-  const int64_t F = ne * p.unit;  // flat tokens of this split
+  const int32_t F = (int32_t)(rc.ne * p.unit);  // flat tokens of this split
   const char *kbase = (const char *)p.kv.k;
   const char *vbase = (const char *)p.kv.v;
-  constexpr int64_t WAVE_SPAN = (int64_t)RPI * UNR;
-  constexpr int64_t STEP = SA_NW * WAVE_SPAN;
+  constexpr int32_t WAVE_SPAN = RPI * UNR;
+  constexpr int32_t STEP = SA_NW * WAVE_SPAN;
   struct Batch {
     Vec kr[UNR], vr[UNR];
     float ksc[UNR], vsc[UNR];
     bool ok[UNR];
   };
   // Issue the loads of the batch starting at flat token `base`.
-  auto load = [&](int64_t base, Batch &bt) {
-    Vec(&kr)[UNR] = bt.kr;
-    Vec(&vr)[UNR] = bt.vr;
-    float(&ksc)[UNR] = bt.ksc;
-    float(&vsc)[UNR] = bt.vsc;
-    bool(&ok)[UNR] = bt.ok;
+  auto load = [&](int32_t base, Batch &bt) {
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
-      // flat token indices stay below 2^31 (checked on the host)
-      const int32_t f = (int32_t)base + w * (int32_t)WAVE_SPAN + u * RPI + slot;
-      int32_t e, j;
-      if (p.unit_shift >= 0) {
-        e = f >> p.unit_shift;
-        j = f & ((1 << p.unit_shift) - 1);
-      } else {
-        e = (int32_t)((uint32_t)f / (uint32_t)p.unit);
-        j = f - e * (int32_t)p.unit;
-      }
-      const int32_t es = min(e, SA_MAX_EPS - 1);
-      const int32_t tok0 = (f < (int32_t)F) ? s_tok0[es] : -1;
-      const int32_t tok = tok0 + j;
-      ok[u] = tok0 >= 0 && tok <= lim32;
-      kr[u] = Vec{};
-      vr[u] = Vec{};
-      ksc[u] = 1.f;
-      vsc[u] = 1.f;
-      if (ok[u]) {
-        int64_t ko, vo, so = 0;
-        if constexpr (PAGED) {
-          int64_t prow;
-          if (p.staged) {
-            prow = (int64_t)((uint32_t)s_phys[es] + (uint32_t)j);  // pool rows < 2^32
-          } else {
-            const int64_t ps = p.kv.page_size;
-            const int64_t phys = p.kv.page_table[b * p.kv.pt_stride + tok / ps];
-            prow = (phys * p.Hkv + kvh) * ps + tok % ps;
-          }
-          ko = vo = prow * D;
-          so = prow;
-        } else {
-          ko = k_bh + (int64_t)tok * p.kv.k_st;
-          vo = v_bh + (int64_t)tok * p.kv.v_st;
-          so = s_bh + (int64_t)tok * p.kv.s_st;
-        }
-        kr[u] = *(const Vec *)(kbase + (ko + c * EPL) * Tr::ESZ);
-        vr[u] = *(const Vec *)(vbase + (vo + c * EPL) * Tr::ESZ);
+      const int32_t f = base + w * WAVE_SPAN + u * RPI + slot;
+      int64_t ko = 0, vo = 0, so = 0;
+      bt.ok[u] = token_rows<D, PAGED>(p, rc, s_tok0, s_phys, f, F, lim32, ko, vo, so);
+      bt.kr[u] = Vec{};
+      bt.vr[u] = Vec{};
+      bt.ksc[u] = 1.f;
+      bt.vsc[u] = 1.f;
+      if (bt.ok[u]) {
+        bt.kr[u] = *(const Vec *)(kbase + (ko + c * EPL) * Tr::ESZ);
+        bt.vr[u] = *(const Vec *)(vbase + (vo + c * EPL) * Tr::ESZ);
         if constexpr (KT == LA_FP8_E4M3) {
-          ksc[u] = p.kv.k_scale[so];
-          vsc[u] = p.kv.v_scale[so];
+          bt.ksc[u] = p.kv.k_scale[so];
+          bt.vsc[u] = p.kv.v_scale[so];
         }
       }
     }
   };
   // Online-softmax update with one loaded batch.
   auto process = [&](Batch &bt) {
-    Vec(&kr)[UNR] = bt.kr;
-    Vec(&vr)[UNR] = bt.vr;
-    float(&ksc)[UNR] = bt.ksc;
-    float(&vsc)[UNR] = bt.vsc;
-    bool(&ok)[UNR] = bt.ok;
     float s[G][UNR];
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
       float kf[EPL];
-      unpack<KT, EPL>(kr[u], kf);
+      unpack<KT, EPL>(bt.kr[u], kf);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float a = 0.f;
@@ -248,7 +302,7 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
       float mb = __int_as_float(0xff800000);
 #pragma unroll
       for (int u = 0; u < UNR; ++u) {
-        s[g][u] = ok[u] ? s[g][u] * ksc[u] : __int_as_float(0xff800000);
+        s[g][u] = bt.ok[u] ? s[g][u] * bt.ksc[u] : __int_as_float(0xff800000);
         mb = fmaxf(mb, s[g][u]);
       }
       const float mn = fmaxf(m[g], mb);
@@ -262,13 +316,13 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
       for (int u = 0; u < UNR; ++u) {
         const float pr = fast_exp2(s[g][u] - mu);
         l[g] += pr;
-        s[g][u] = pr * vsc[u];
+        s[g][u] = pr * bt.vsc[u];
       }
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
       float vf[EPL];
-      unpack<KT, EPL>(vr[u], vf);
+      unpack<KT, EPL>(bt.vr[u], vf);
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -278,7 +332,7 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
   // Double-buffered: the next batch's loads are in flight while one is processed.
   Batch b0, b1;
   if (F > 0) load(0, b0);
-  for (int64_t base = 0; base < F; base += 2 * STEP) {
+  for (int32_t base = 0; base < F; base += 2 * STEP) {
     if (base + STEP < F) load(base + STEP, b1);
     process(b0);
     if (base + STEP >= F) break;
@@ -317,33 +371,250 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
     }
   }
   __syncthreads();
-  // Merge the waves, then write the output or this split's partial state.
-  for (int i = tid; i < G * D; i += SA_NT) {
-    const int g = i / D, d = i % D;
-    float M = __int_as_float(0xff800000);
+  finish_row<G, D>(p, rc, s_acc, s_m, s_l);
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Maximum over the 16 lanes of a DPP row; every lane of the row gets it.
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp_f32<0xB1>(x));
+  x = fmaxf(x, dpp_f32<0x4E>(x));
+  x = fmaxf(x, dpp_f32<0x141>(x));
+  x = fmaxf(x, dpp_f32<0x140>(x));
+  return x;
+}
+
+// bf16 K/V, bf16 q, head dim 128: scores on the matrix cores.
+//
+// Each wave walks its own tokens, 16 per round.  S = Q K^T for the round is
+// four v_mfma_f32_16x16x32_bf16 (A = the G query rows of q, zero above G;
+// B = K^T, lane l holding 8 dims of token l % 16), which leaves lane
+// 16*(h/4) + i holding S[head h][token i], h % 4 in the accumulator element.
+// The softmax reference max is wave-uniform (round maxima by DPP row
+// reductions, then readlane), so the four row slots of the PV product share
+// it and merge by plain sums.  Probabilities pass through LDS to the PV
+// lanes, which read V rows 16 contiguous bytes per lane (a token per 16
+// lanes) and accumulate O on the VALU in fp32.
+template <int G, bool PAGED, bool U16>
+__global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel(AttnKP p) {
+  constexpr int D = 128;
+  constexpr int RT = 16;            // tokens per wave round
+  constexpr int NRG = (G + 3) / 4;  // DPP rows holding heads
+  static_assert(G >= 1 && G <= 8, "group of at most 8 heads");
+
+  __shared__ int32_t s_tok0[SA_MAX_EPS];
+  __shared__ int32_t s_phys[PAGED ? SA_MAX_EPS : 1];
+  __shared__ float s_acc[SA_NW][G][D];
+  __shared__ float s_m[SA_NW][G], s_l[SA_NW][G];
+  __shared__ __align__(16) float s_p[SA_NW][RT][4 * NRG];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c = lane & 15;     // V: 8-dim chunk; K: token of the round
+  const int slot = lane >> 4;  // V: token slot; K: 8-dim group within 32
+  const RowCtx rc = stage_row<G, PAGED>(p, s_tok0, s_phys);
+  const int32_t lim32 = (int32_t)min(rc.lim, (int64_t)0x7fffffff);
+
+  // A operand: q row c (head c < G), dims 32s + 8*slot .. +8, raw bf16 bits.
+  bf16x8 qa[4];
+  {
+    const uint16_t *qp = (const uint16_t *)p.q;
+    const int64_t qo = rc.b * p.q_sb + (rc.h0 + c) * p.q_sh + rc.t * p.q_st + 8 * slot;
 #pragma unroll
-    for (int x = 0; x < SA_NW; ++x) M = fmaxf(M, s_m[x][g]);
-    const float Mu = (M == __int_as_float(0xff800000)) ? 0.f : M;
-    float L = 0.f, A = 0.f;
+    for (int s = 0; s < 4; ++s) {
+      uint16_t x[8];
 #pragma unroll
-    for (int x = 0; x < SA_NW; ++x) {
-      const float sc = fast_exp2(s_m[x][g] - Mu);
-      L += s_l[x][g] * sc;
-      A += s_acc[x][g][d] * sc;
+      for (int e = 0; e < 8; ++e) x[e] = c < G ? qp[qo + 32 * s + e] : (uint16_t)0;
+      qa[s] = __builtin_bit_cast(bf16x8, x);
     }
-    const int64_t h = h0 + g;
-    if (p.splits == 1) {
-      const float o = L > 0.f ? A / L : 0.f;
-      store_from_f32(p.out, b * p.o_sb + h * p.o_sh + t * p.o_st + d, p.out_dt, o);
+  }
+  float ms[4], ls[4];  // per DPP row: max and partial sums of heads 4*slot + e
+  float acc[G][8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    ms[e] = __int_as_float(0xff800000);
+    ls[e] = 0.f;
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  __syncthreads();
+
+  const int32_t F = (int32_t)(rc.ne * p.unit);
+  const char *kbase = (const char *)p.kv.k;
+  const char *vbase = (const char *)p.kv.v;
+  constexpr int32_t STEP = SA_NW * RT;
+  // One set of K/V registers, refilled as it is consumed: the next round's K
+  // loads are issued once the current K is in the matrix core, and each V
+  // row of the next round once the current one has been accumulated.
+  uint4 kr[4], vr[4];
+  bool kok = false;
+  // U16 (units of 16k tokens lying inside one page): the 16 tokens of a round
+  // are consecutive rows of one entry, so the entry lookup is wave-uniform and
+  // every row address is a scalar base plus a lane offset.
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  struct Round {
+    int32_t tok;    // first token of the round (-1: nothing to attend)
+    int64_t kb, vb; // element offsets of its K and V rows
+  };
+  auto round_of = [&](int32_t base) {
+    Round rd{-1, 0, 0};
+    const int32_t fw = base + wu * RT;
+    if (fw >= F) return rd;
+    int32_t e, j;
+    if (p.unit_shift >= 0) {
+      e = fw >> p.unit_shift;
+      j = fw & ((1 << p.unit_shift) - 1);
     } else {
-      const int64_t pi = (r * G + g) * p.splits + split;
-      p.ws_acc[pi * D + d] = A;
-      if (d == 0) {
-        p.ws_ml[pi * 2 + 0] = M;
-        p.ws_ml[pi * 2 + 1] = L;
+      e = (int32_t)((uint32_t)fw / (uint32_t)p.unit);
+      j = fw - e * (int32_t)p.unit;
+    }
+    const int32_t t0 = __builtin_amdgcn_readfirstlane(s_tok0[e]);
+    if (t0 < 0) return rd;
+    rd.tok = t0 + j;
+    if constexpr (PAGED) {
+      const uint32_t prow = (uint32_t)__builtin_amdgcn_readfirstlane(s_phys[e]) + (uint32_t)j;
+      rd.kb = rd.vb = (int64_t)prow * D;
+    } else {
+      rd.kb = rc.k_bh + (int64_t)rd.tok * p.kv.k_st;
+      rd.vb = rc.v_bh + (int64_t)rd.tok * p.kv.v_st;
+    }
+    return rd;
+  };
+  Round rd_next{-1, 0, 0};
+  // U16 loads are issued for every lane: the 16 rows of a round lie in one
+  // pool page, so every row address is valid; a round with nothing to attend
+  // reads the first rows of the pool instead.  Tokens that are not attended
+  // have their K columns masked and their V rows zeroed after the load.
+  const uint32_t koff = (uint32_t)((c * D + 8 * slot) * 2);
+  const uint32_t voff = (uint32_t)((slot * D + 8 * c) * 2);
+  auto load_k = [&](int32_t base) {
+    if constexpr (U16) {
+      rd_next = round_of(base);
+      kok = rd_next.tok >= 0 && rd_next.tok + c <= lim32;
+      const char *rp = rd_next.tok >= 0 ? kbase + rd_next.kb * 2 : kbase;  // wave-uniform
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kr[s] = *(const uint4 *)(rp + koff + 64 * s);
+    } else {
+      int64_t ko = 0, vo = 0, so = 0;
+      kok = token_rows<D, PAGED>(p, rc, s_tok0, s_phys, base + w * RT + c, F, lim32, ko, vo, so);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        kr[s] = kok ? *(const uint4 *)(kbase + (ko + 32 * s + 8 * slot) * 2) : uint4{0, 0, 0, 0};
+    }
+  };
+  auto load_v = [&](int32_t base, int u) {
+    if constexpr (U16) {
+      const bool ok = rd_next.tok >= 0 && rd_next.tok + 4 * u + slot <= lim32;
+      const char *rp = rd_next.tok >= 0 ? vbase + rd_next.vb * 2 : vbase;  // wave-uniform
+      const uint4 x = *(const uint4 *)(rp + voff + 4 * u * D * 2);
+      vr[u] = ok ? x : uint4{0, 0, 0, 0};
+    } else {
+      int64_t ko = 0, vo = 0, so = 0;
+      const bool ok =
+          token_rows<D, PAGED>(p, rc, s_tok0, s_phys, base + w * RT + 4 * u + slot, F, lim32, ko, vo, so);
+      vr[u] = ok ? *(const uint4 *)(vbase + (vo + 8 * c) * 2) : uint4{0, 0, 0, 0};
+    }
+  };
+  if (F > 0) {
+    load_k(0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_v(0, u);
+  }
+  for (int32_t base = 0; base < F; base += STEP) {
+    const bool more = base + STEP < F;
+    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], __builtin_bit_cast(bf16x8, kr[s]), sacc, 0, 0, 0);
+    const bool cur_ok = kok;
+    if (U16 || more) load_k(base + STEP);
+    __builtin_amdgcn_sched_barrier(0);
+    float sv[4], mn[4];
+    bool grow = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sv[e] = cur_ok ? sacc[e] * p.qscale : __int_as_float(0xff800000);
+      mn[e] = fmaxf(ms[e], row_max16(sv[e]));
+      grow = grow || (slot < NRG && mn[e] > ms[e]);
+    }
+    // the G heads' maxima are wave-uniform (DPP row 0: heads 0-3, row 1: 4-7)
+    if (__ballot(grow) != 0) {
+      float al[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float u = (mn[e] == __int_as_float(0xff800000)) ? 0.f : mn[e];
+        al[e] = fast_exp2(ms[e] - u);
+        ls[e] *= al[e];
+        ms[e] = mn[e];
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float af = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al[g & 3]), 16 * (g >> 2)));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= af;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float u = (ms[e] == __int_as_float(0xff800000)) ? 0.f : ms[e];
+      sv[e] = fast_exp2(sv[e] - u);
+      ls[e] += sv[e];
+    }
+    if (slot < NRG) *(float4 *)&s_p[w][c][4 * slot] = float4{sv[0], sv[1], sv[2], sv[3]};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float pg[4 * NRG];
+#pragma unroll
+      for (int x = 0; x < NRG; ++x) {
+        const float4 v4 = *(const float4 *)&s_p[w][4 * u + slot][4 * x];
+        pg[4 * x + 0] = v4.x;
+        pg[4 * x + 1] = v4.y;
+        pg[4 * x + 2] = v4.z;
+        pg[4 * x + 3] = v4.w;
+      }
+      float vf[8];
+      unpack<LA_BF16, 8>(vr[u], vf);
+      if (U16 || more) load_v(base + STEP, u);
+      // keep each refill after the use of the registers it replaces
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = __builtin_fmaf(pg[g], vf[e], acc[g][e]);
+    }
+  }
+
+  // The four token slots share the wave's reference maxima: plain sums.
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      acc[g][e] += __shfl_xor(acc[g][e], 16, 64);
+      acc[g][e] += __shfl_xor(acc[g][e], 32, 64);
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ls[e] = group_sum<16>(ls[e]);
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_acc[w][g][8 * c + e] = acc[g][e];
+  }
+  if (c == 0 && slot < NRG) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int g = 4 * slot + e;
+      if (g < G) {
+        s_m[w][g] = ms[e];
+        s_l[w][g] = ls[e];
       }
     }
   }
+  __syncthreads();
+  finish_row<G, D>(p, rc, s_acc, s_m, s_l);
 }
 
 // Merge the split partials of one (row, head): one workgroup, D threads.
@@ -380,7 +651,14 @@ template <int KT, int D, int G, bool PAGED>
 static int launch_attn(const AttnKP &p, hipStream_t st) {
   constexpr int UNR = unroll_for<KT>(D);
   dim3 grid((unsigned)p.splits, (unsigned)(p.B * p.ids_heads * p.Tq));
-  sparse_attn_kernel<KT, D, G, UNR, PAGED><<<grid, SA_NT, 0, st>>>(p);
+  // U16: paged, and every 16-row round lies inside one entry of one page
+  const bool u16 = PAGED && p.staged && p.unit % 16 == 0;
+  if (KT == LA_BF16 && D == 128 && p.q_dt == LA_BF16 && u16)
+    sparse_attn_mfma_kernel<G, PAGED, true><<<grid, SA_NT, 0, st>>>(p);
+  else if (KT == LA_BF16 && D == 128 && p.q_dt == LA_BF16)
+    sparse_attn_mfma_kernel<G, PAGED, false><<<grid, SA_NT, 0, st>>>(p);
+  else
+    sparse_attn_kernel<KT, D, G, UNR, PAGED><<<grid, SA_NT, 0, st>>>(p);
   LA_LAUNCHED();
   if (p.splits > 1) {
     sparse_attn_combine<<<dim3((unsigned)(p.B * p.ids_heads * p.Tq * G)), D, 0, st>>>(p, G, D);
@@ -416,6 +694,19 @@ static int dispatch_d(const AttnKP &p, int64_t D, int64_t G, hipStream_t st) {
     case 128: return dispatch_g<KT, 128>(p, G, st);
     default: return fail(LA_ERR_UNSUPPORTED, "sparse attention: head_dim %lld not in {64,128}", (long long)D);
   }
+}
+
+static int num_cus() {
+  static int cached = 0;
+  if (cached <= 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      cached = v;
+    else
+      cached = 256;
+  }
+  return cached;
 }
 
 struct Plan {
@@ -455,7 +746,10 @@ static int plan_attn(const la_sparse_attn_args *a, const la_kv *kv, Plan &pl) {
   const int64_t min_splits = ceil_div(a->N, SA_MAX_EPS);
   int64_t splits = a->num_splits;
   if (splits <= 0) {
-    const int64_t target = 2048;  // workgroups: 8 per CU
+    // workgroups to aim for: the matrix-core kernel keeps 4 resident per CU
+    // (so one full wave of workgroups), the VALU kernel 8 per CU
+    const bool mfma = kv->dtype == LA_BF16 && a->q_dtype == LA_BF16 && a->D == 128;
+    const int64_t target = (int64_t)num_cus() * (mfma ? 4 : 8);
     const int64_t tokens = a->N * a->unit;
     const int64_t by_tokens = std::max<int64_t>(1, tokens / 256);
     splits = std::min(ceil_div(target, pl.R), by_tokens);

@@ -300,21 +300,32 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
       if (tid == 0) sh.above = (uint32_t)K;
       __syncthreads();
       int32_t *oi = p.out_idx + orow * p.width;
-      for (int64_t jj = tid; jj < p.width; jj += TK_NT) {
-        int32_t s = jj < K ? sel[jj] : -1;
-        int32_t id = s;
-        if (cand && s >= 0) {
-          id = cand[s];
-          if (id < 0) {
-            s = -1;
+      for (int64_t base = tid; base < p.width; base += TK_NT * TK_BATCH) {
+        int32_t sl[TK_BATCH], id[TK_BATCH];
+#pragma unroll
+        for (int e = 0; e < TK_BATCH; ++e) {
+          const int64_t jj = base + e * TK_NT;
+          sl[e] = jj < K ? sel[jj] : -1;
+        }
+#pragma unroll
+        for (int e = 0; e < TK_BATCH; ++e) id[e] = (cand && sl[e] >= 0) ? cand[sl[e]] : sl[e];
+#pragma unroll
+        for (int e = 0; e < TK_BATCH; ++e) {
+          const int64_t jj = base + e * TK_NT;
+          if (jj >= p.width) break;
+          if (cand && sl[e] >= 0 && id[e] < 0) {
+            sl[e] = -1;
             atomicMin(&sh.above, (uint32_t)jj);
           }
-        }
-        oi[jj] = id;
-        if (p.out_val) {
-          float v = __int_as_float(0xff800000);
-          if (s >= 0) v = (force && s == own) ? __int_as_float(0x7f800000) : (float)rp[s];
-          p.out_val[orow * p.width + jj] = v;
+          oi[jj] = id[e];
+          if (p.out_val) {
+            // the sort keys map back to the exact scores (-0 reads as +0)
+            float v = __int_as_float(0xff800000);
+            if (sl[e] >= 0)
+              v = (force && sl[e] == own) ? __int_as_float(0x7f800000)
+                                          : (float)key_to_double(skey[jj]);
+            p.out_val[orow * p.width + jj] = v;
+          }
         }
       }
       __syncthreads();

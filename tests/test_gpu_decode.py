@@ -177,6 +177,41 @@ def test_sparse_attention_bf16(dev):
     assert np.abs(out.cpu().double().numpy() - ref).max() < 2e-3
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 4), (32, 8), (16, 2)])
+@pytest.mark.parametrize("unit,paged", [(64, True), (16, True), (32, False), (1, True), (8, True)])
+def test_sparse_attention_bf16_matrix_core_paths(dev, hq, hkv, unit, paged):
+    """bf16 q and K/V at head dim 128 take the matrix-core kernel: whole
+    16-row rounds inside one page (unit a multiple of 16, paged) or per-token
+    row lookups (any other unit or layout).  Causal masking with an offset, a
+    ragged kv length, per-list counts and several split counts."""
+    B, T, D, ps = 2, 1024, 128, 64
+    q, k, v = make_inputs(B, hq, hkv, 2, T, D, seed=hq + unit)
+    q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    n_units = T // unit
+    n = min(24, n_units) if unit > 1 else 300
+    ids = _lists(B, hkv, 2, n, n_units, seed=unit, holes=True)
+    counts = torch.tensor([[[n, n - 3]] * hkv, [[n - 7, n]] * hkv], dtype=torch.int32)
+    kv_len = torch.tensor([T, 700], dtype=torch.int32)
+    offset = 900
+    kw = dict(unit=unit, counts=counts.to(dev), causal=True, offset=offset, kv_len=kv_len.to(dev),
+              out_dtype=torch.float32)
+    if paged:
+        pk, pv, pt = to_pool(k, v, ps)
+        args = (pk.to(dev), pv.to(dev))
+        kw.update(page_table=pt.to(dev), page_size=ps)
+    else:
+        args = (k.to(dev), v.to(dev))
+    ref = np.zeros((B, hq, 2, D))
+    for b in range(B):
+        ref[b:b + 1] = oracle.attend_lists(q[b:b + 1], k[b:b + 1], v[b:b + 1], ids[b:b + 1].numpy(),
+                                           unit=unit, counts=counts[b:b + 1].numpy(), causal=True,
+                                           offset=offset, kv_len=[int(kv_len[b])])
+    for splits in (1, 0, 3):
+        out = sparse_attention(q.to(dev), *args, ids.to(dev), num_splits=splits, **kw)
+        err = np.abs(out.cpu().double().numpy() - ref).max()
+        assert err < 2e-3, (splits, err)
+
+
 @pytest.mark.parametrize("paged", [False, True])
 def test_sparse_attention_fp8(dev, paged):
     """fp8 e4m3 K/V with per-token scales (kv/quant.py:90-93, group = head_dim)."""
