@@ -191,31 +191,86 @@ __device__ void tk_select(const RowKeys &key, int64_t n_v, int64_t K, TkShared &
   __syncthreads();
 }
 
-__global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
-  extern __shared__ __align__(16) unsigned char dyn[];
-  __shared__ TkShared sh;
-  const int tid = threadIdx.x;
+// The row (group) a workgroup selects for, its valid prefix and forced unit.
+struct TkRow {
+  int64_t br, seg0, tl, t, orow, n_v, own, K;
+  bool force;
+};
+
+__device__ __forceinline__ TkRow tk_row(const TopkKParams &p) {
+  TkRow r;
   // Segmented mode: workgroup gi handles segment gi % nseg of row gi / nseg.
-  const int64_t br = p.seg_len > 0 ? (int64_t)blockIdx.x / p.nseg : (int64_t)blockIdx.x;
+  r.br = p.seg_len > 0 ? (int64_t)blockIdx.x / p.nseg : (int64_t)blockIdx.x;
   const int64_t seg = p.seg_len > 0 ? (int64_t)blockIdx.x % p.nseg : 0;
-  const int64_t seg0 = seg * p.seg_len;
-  const int64_t tl = br % p.Tq;
-  const int64_t t = tl + p.t_base;
-  const int64_t orow = p.seg_len > 0 ? (int64_t)blockIdx.x : (br / p.Tq) * p.out_tq + t;
+  r.seg0 = seg * p.seg_len;
+  r.tl = r.br % p.Tq;
+  r.t = r.tl + p.t_base;
+  r.orow = p.seg_len > 0 ? (int64_t)blockIdx.x : (r.br / p.Tq) * p.out_tq + r.t;
   int64_t n_v = p.n;
   int64_t own = -1;
   if (p.pos_unit > 0) {
-    const int64_t pos = p.pos_off + t;
+    const int64_t pos = p.pos_off + r.t;
     const int64_t u = pos >= 0 ? pos / p.pos_unit : -1;
     n_v = min(p.n, u + 1);
     own = min(u, p.n - 1);
   }
-  if (p.n_valid_tab) n_v = min(p.n, (int64_t)p.n_valid_tab[t]);
-  if (p.own_tab) own = (int64_t)p.own_tab[t];
-  if (p.seg_len > 0) n_v = min(n_v - seg0, min(p.seg_len, p.n - seg0));
-  n_v = max(n_v, (int64_t)0);
-  const bool force = p.force_own && own >= 0 && own < n_v;
-  const int64_t K = min(p.k, n_v);
+  if (p.n_valid_tab) n_v = min(p.n, (int64_t)p.n_valid_tab[r.t]);
+  if (p.own_tab) own = (int64_t)p.own_tab[r.t];
+  if (p.seg_len > 0) n_v = min(n_v - r.seg0, min(p.seg_len, p.n - r.seg0));
+  r.n_v = max(n_v, (int64_t)0);
+  r.own = own;
+  r.force = p.force_own && own >= 0 && own < r.n_v;
+  r.K = min(p.k, r.n_v);
+  return r;
+}
+
+// Sink and window units are OR'd into the bitmap, which is then emitted in
+// ascending index order, -1 padded, with the count of kept units.
+__device__ void tk_emit_bitmap(const TopkKParams &p, uint32_t *bm, const TkRow &rw,
+                               uint32_t *wtmp) {
+  const int tid = threadIdx.x;
+  const int64_t n_v = rw.n_v, own = rw.own;
+  if (n_v > 0) {
+    const int64_t s_end = min(p.sink, n_v);
+    for (int64_t i = tid; i < s_end; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    if (p.window > 0 && own >= 0) {
+      const int64_t w0 = max((int64_t)0, own - p.window + 1);
+      const int64_t w1 = min(own, n_v - 1);
+      for (int64_t i = w0 + tid; i <= w1; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    }
+  }
+  __syncthreads();
+  // each thread owns a run of bitmap words
+  const int64_t words = (n_v + 31) / 32;
+  const int64_t wpt = (words + TK_NT - 1) / TK_NT;
+  const int64_t w_beg = min(words, (int64_t)tid * wpt), w_end = min(words, w_beg + wpt);
+  uint32_t cnt = 0;
+  for (int64_t x = w_beg; x < w_end; ++x) cnt += __popc(bm[x]);
+  uint32_t total;
+  const uint32_t incl = tk_block_incl_scan(cnt, wtmp, total);
+  uint32_t pos = incl - cnt;
+  int32_t *oi = p.out_idx + rw.orow * p.width;
+  for (int64_t x = w_beg; x < w_end; ++x) {
+    uint32_t bits = bm[x];
+    while (bits) {
+      const int b = __ffs(bits) - 1;
+      if (pos < (uint32_t)p.width) oi[pos] = (int32_t)(x * 32 + b);
+      ++pos;
+      bits &= bits - 1;
+    }
+  }
+  for (int64_t jj = (int64_t)total + tid; jj < p.width; jj += TK_NT) oi[jj] = -1;
+  if (p.out_count && tid == 0) p.out_count[rw.orow] = (int32_t)min((int64_t)total, p.width);
+}
+
+__global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ TkShared sh;
+  const int tid = threadIdx.x;
+  const TkRow rw = tk_row(p);
+  const int64_t seg0 = rw.seg0, tl = rw.tl, orow = rw.orow, n_v = rw.n_v, own = rw.own, K = rw.K;
+  const int64_t br = rw.br;
+  const bool force = rw.force;
 
   unsigned char *ptr = dyn;
   uint64_t *lkeys = nullptr;
@@ -334,39 +389,300 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
     }
   }
   if (!bm) return;
+  tk_emit_bitmap(p, bm, rw, sh.wtmp[1]);
+}
 
-  // Sink and window units, OR'd after the top-k.
-  if (n_v > 0) {
-    const int64_t s_end = min(p.sink, n_v);
-    for (int64_t i = tid; i < s_end; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
-    if (p.window > 0 && own >= 0) {
-      const int64_t w0 = max((int64_t)0, own - p.window + 1);
-      const int64_t w1 = min(own, n_v - 1);
-      for (int64_t i = w0 + tid; i <= w1; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+// x precedes y: valid before padding (-1), higher key, then lower index.
+__device__ __forceinline__ bool tk_precedes(uint64_t kx, int32_t ix, uint64_t ky, int32_t iy) {
+  return ix >= 0 && (iy < 0 || kx > ky || (kx == ky && ix < iy));
+}
+
+// Bitonic compare-exchange of register pairs (e, e | S) of this thread
+// (positions tid*E + e): ascending runs put the preceding element first.
+template <int S, int E>
+__device__ __forceinline__ void tk_local_stage(uint64_t (&key)[E], int32_t (&idx)[E], int tid,
+                                               int size) {
+  if constexpr (S < E) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (e & S) continue;
+      const int el = e | S;
+      const bool up = ((tid * E + e) & size) == 0;
+      const bool sw = up ? tk_precedes(key[el], idx[el], key[e], idx[e])
+                         : tk_precedes(key[e], idx[e], key[el], idx[el]);
+      const uint64_t ka = key[e], kb = key[el];
+      const int32_t ia = idx[e], ib = idx[el];
+      key[e] = sw ? kb : ka;
+      key[el] = sw ? ka : kb;
+      idx[e] = sw ? ib : ia;
+      idx[el] = sw ? ia : ib;
     }
   }
+}
+
+// Register-resident top-k for rows of at most 256*KPT keys (thread t holds
+// the keys of units t + 256*j).  Selection is the radix select above, started
+// at the highest bit where the row's valid keys differ (common leading bits
+// cost no pass), with per-wave histograms.  The survivors are either OR'd
+// into a bitmap (BITMAP: unions, sink, window, index order) or sorted by
+// (key desc, index asc) with a bitonic network over E registers per thread:
+// partners in the same thread are swapped in place, in other lanes of the
+// wave they are exchanged by shuffles, in other waves through LDS.
+template <int KPT, int E, bool BITMAP>
+__global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
+  constexpr int P = TK_NT * E;  // sort width (sorted form)
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ uint32_t hist[TK_NW][256];
+  __shared__ uint32_t eqc[KPT][TK_NW];
+  __shared__ uint64_t red[2][TK_NW];
+  __shared__ uint32_t wtmp[2][TK_NW];
+  __shared__ uint32_t s_bin, s_above, s_cnt, s_fill, s_first_pad;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint64_t lt = lanemask_lt(lane);
+  const TkRow rw = tk_row(p);
+  const int32_t n_v = (int32_t)rw.n_v;  // n_v <= 256*KPT
+  const int32_t own = (int32_t)rw.own;
+  uint32_t *bm = nullptr;
+  uint64_t *skey = nullptr;
+  int32_t *sidx = nullptr;
+  if constexpr (BITMAP) {
+    bm = (uint32_t *)dyn;
+    for (int64_t i = tid; i < p.bitmap_words; i += TK_NT) bm[i] = 0u;
+  } else {
+    skey = (uint64_t *)dyn;
+    sidx = (int32_t *)(dyn + (size_t)P * 8);
+  }
+  if (tid == 0) s_fill = 0;
   __syncthreads();
-  // Ascending emission: each thread owns a run of bitmap words.
-  const int64_t words = (n_v + 31) / 32;
-  const int64_t wpt = (words + TK_NT - 1) / TK_NT;
-  const int64_t w_beg = min(words, (int64_t)tid * wpt), w_end = min(words, w_beg + wpt);
-  uint32_t cnt = 0;
-  for (int64_t x = w_beg; x < w_end; ++x) cnt += __popc(bm[x]);
-  uint32_t total;
-  const uint32_t incl = tk_block_incl_scan(cnt, sh.wtmp[1], total);
-  uint32_t pos = incl - cnt;
-  int32_t *oi = p.out_idx + orow * p.width;
-  for (int64_t x = w_beg; x < w_end; ++x) {
-    uint32_t bits = bm[x];
-    while (bits) {
-      const int b = __ffs(bits) - 1;
-      if (pos < (uint32_t)p.width) oi[pos] = (int32_t)(x * 32 + b);
-      ++pos;
-      bits &= bits - 1;
+
+  for (int64_t g = 0; g < p.G; ++g) {
+    const int64_t row = ((rw.br / p.Tq) * p.G + g) * p.Tq + rw.tl;
+    const double *rp = p.scores + row * p.row_stride + rw.seg0;
+    // raw fp64 bits, mapped in place to order keys (ord_key: -0 reads as +0)
+    uint64_t u[KPT];
+    const uint64_t *rb = (const uint64_t *)rp;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int32_t i = tid + TK_NT * j;
+      u[j] = i < n_v ? rb[i] : 0ull;
     }
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int32_t i = tid + TK_NT * j;
+      uint64_t x = (u[j] << 1) == 0 ? 0ull : u[j];
+      x = (x >> 63) ? ~x : (x | 0x8000000000000000ull);
+      u[j] = (rw.force && i == own) ? KEY_FORCED : x;
+    }
+    const uint32_t K = (uint32_t)rw.K;
+    uint64_t prefix = 0, mask = 0;
+    uint32_t need = K;
+    bool all_in = (int32_t)K >= n_v;
+    if (!all_in) {
+      // leading bits shared by every valid key are fixed without a pass
+      uint64_t o = 0, a = ~0ull;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        if (tid + TK_NT * j < n_v) {
+          o |= u[j];
+          a &= u[j];
+        }
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        o |= __shfl_xor(o, off, 64);
+        a &= __shfl_xor(a, off, 64);
+      }
+      if (lane == 0) {
+        red[0][w] = o;
+        red[1][w] = a;
+      }
+      __syncthreads();
+      o = 0;
+      a = ~0ull;
+#pragma unroll
+      for (int x = 0; x < TK_NW; ++x) {
+        o |= red[0][x];
+        a &= red[1][x];
+      }
+      const uint64_t diff = o ^ a;
+      int top = diff ? 63 - __clzll((long long)diff) : -1;
+      mask = top >= 0 ? ~((2ull << top) - 1ull) : ~0ull;  // 2ull << 63 wraps to 0
+      prefix = a & mask;
+      while (top >= 0) {
+        const int shift = top >= 7 ? top - 7 : 0;
+        const uint32_t dm = (2u << (top - shift)) - 1u;  // digit of top-shift+1 <= 8 bits
+#pragma unroll
+        for (int x = 0; x < TK_NW; ++x) hist[x][tid] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+          if (tid + TK_NT * j < n_v && (u[j] & mask) == prefix)
+            atomicAdd(&hist[w][(uint32_t)(u[j] >> shift) & dm], 1u);
+        }
+        __syncthreads();
+        uint32_t c = 0;
+#pragma unroll
+        for (int x = 0; x < TK_NW; ++x) c += hist[x][255 - tid];
+        uint32_t tot;
+        const uint32_t incl = tk_block_incl_scan(c, wtmp[0], tot);
+        if (incl >= need && incl - c < need) {
+          s_bin = 255 - tid;
+          s_above = incl - c;
+          s_cnt = c;
+        }
+        __syncthreads();
+        need -= s_above;
+        prefix |= (uint64_t)s_bin << shift;
+        mask |= (uint64_t)dm << shift;
+        const bool done = s_cnt == need;
+        __syncthreads();
+        if (done) {
+          all_in = true;
+          break;
+        }
+        top = shift - 1;
+      }
+    }
+    // Keys above the threshold are all taken; keys equal to it are taken in
+    // index order until `need` is met (lowest index first).
+    if (!all_in) {
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const bool eq = tid + TK_NT * j < n_v && (u[j] & mask) == prefix;
+        const uint64_t b = __ballot(eq);
+        if (lane == 0) eqc[j][w] = (uint32_t)__popcll(b);
+      }
+      __syncthreads();
+    }
+    uint32_t eq_before = 0;  // threshold keys in earlier register slots
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int32_t i = tid + TK_NT * j;
+      const bool valid = i < n_v;
+      const uint64_t um = u[j] & mask;
+      const bool gt = valid && um > prefix;
+      const bool eq = valid && um == prefix;
+      bool take = gt || (eq && all_in);
+      if (!all_in) {
+        const uint64_t b = __ballot(eq);
+        uint32_t rank = eq_before + (uint32_t)__popcll(b & lt);
+#pragma unroll
+        for (int x = 0; x < TK_NW; ++x) rank += x < w ? eqc[j][x] : 0u;
+        take = gt || (eq && rank < need);
+#pragma unroll
+        for (int x = 0; x < TK_NW; ++x) eq_before += eqc[j][x];
+      }
+      if constexpr (BITMAP) {
+        if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
+      } else {
+        const uint64_t tm = __ballot(take);
+        uint32_t base = 0;
+        if (lane == 0 && tm) base = atomicAdd(&s_fill, (uint32_t)__popcll(tm));
+        base = __shfl(base, 0, 64);
+        if (take) {
+          const uint32_t pos = base + (uint32_t)__popcll(tm & lt);
+          skey[pos] = u[j];
+          sidx[pos] = i;
+        }
+      }
+    }
+    __syncthreads();
   }
-  for (int64_t jj = (int64_t)total + tid; jj < p.width; jj += TK_NT) oi[jj] = -1;
-  if (p.out_count && tid == 0) p.out_count[orow] = (int32_t)min((int64_t)total, p.width);
+  if constexpr (BITMAP) {
+    tk_emit_bitmap(p, bm, rw, wtmp[1]);
+  } else {
+    // sorted form (one row per workgroup)
+    const int32_t K = (int32_t)rw.K;
+    for (int32_t i = K + tid; i < P; i += TK_NT) {
+      skey[i] = 0;
+      sidx[i] = -1;
+    }
+    if (tid == 0) s_first_pad = (uint32_t)K;
+    __syncthreads();
+    uint64_t key[E];
+    int32_t idx[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      key[e] = skey[tid * E + e];
+      idx[e] = sidx[tid * E + e];
+    }
+    const auto precedes = tk_precedes;
+    // position i keeps, of itself and its partner, the one that comes first
+    // (ascending run) or last (descending run)
+    auto exchange = [&](int e, int i, int size, int stride, uint64_t pk, int32_t pi) {
+      const bool lower = (i & stride) == 0, up = (i & size) == 0;
+      const bool want_first = lower == up;
+      const bool take = want_first ? precedes(pk, pi, key[e], idx[e]) : precedes(key[e], idx[e], pk, pi);
+      if (take) {
+        key[e] = pk;
+        idx[e] = pi;
+      }
+    };
+    for (int size = 2; size <= P; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        if (stride < E) {
+          // partner in the same thread: constant register indices per stride
+          switch (stride) {
+            case 1: tk_local_stage<1, E>(key, idx, tid, size); break;
+            case 2: tk_local_stage<2, E>(key, idx, tid, size); break;
+            case 4: tk_local_stage<4, E>(key, idx, tid, size); break;
+            case 8: tk_local_stage<8, E>(key, idx, tid, size); break;
+            default: break;
+          }
+        } else if (stride < 64 * E) {
+          const int lx = stride / E;
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const uint64_t pk = __shfl_xor(key[e], lx, 64);
+            const int32_t pi = __shfl_xor(idx[e], lx, 64);
+            exchange(e, tid * E + e, size, stride, pk, pi);
+          }
+        } else {
+          __syncthreads();
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            skey[tid * E + e] = key[e];
+            sidx[tid * E + e] = idx[e];
+          }
+          __syncthreads();
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const int i = tid * E + e;
+            exchange(e, i, size, stride, skey[i ^ stride], sidx[i ^ stride]);
+          }
+        }
+      }
+    }
+    const int32_t *cand = p.cand_idx ? p.cand_idx + ((rw.br / p.Tq) * p.G * p.Tq + rw.tl) * p.row_stride + rw.seg0 : nullptr;
+    int32_t *oi = p.out_idx + rw.orow * p.width;
+    int32_t id[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) id[e] = (cand && idx[e] >= 0) ? cand[idx[e]] : idx[e];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int64_t jj = (int64_t)tid * E + e;
+      if (jj >= p.width) break;
+      int32_t s = idx[e];
+      if (cand && s >= 0 && id[e] < 0) {
+        s = -1;
+        atomicMin(&s_first_pad, (uint32_t)jj);
+      }
+      oi[jj] = id[e];
+      if (p.out_val) {
+        float v = __int_as_float(0xff800000);
+        if (s >= 0)
+          v = (rw.force && s == own) ? __int_as_float(0x7f800000) : (float)key_to_double(key[e]);
+        p.out_val[rw.orow * p.width + jj] = v;
+      }
+    }
+    for (int64_t jj = P + tid; jj < p.width; jj += TK_NT) {
+      oi[jj] = -1;
+      if (p.out_val) p.out_val[rw.orow * p.width + jj] = __int_as_float(0xff800000);
+    }
+    __syncthreads();
+    if (p.out_count && tid == 0) p.out_count[rw.orow] = (int32_t)s_first_pad;
+  }
 }
 
 static int64_t align16(int64_t x) { return (x + 15) / 16 * 16; }
@@ -523,6 +839,54 @@ int topk_launch_ws(TopkKParams p, void *ws, int64_t ws_bytes, hipStream_t st) {
   return topk_launch(f, st);
 }
 
+template <bool BITMAP, int KPT>
+static int launch_reg_e(const TopkKParams &p, int E, size_t bytes, hipStream_t st) {
+  const dim3 grid((unsigned)p.NG);
+  if constexpr (BITMAP) {
+    topk_reg_kernel<KPT, 1, true><<<grid, TK_NT, bytes, st>>>(p);
+  } else {
+    switch (E) {
+      case 1: topk_reg_kernel<KPT, 1, false><<<grid, TK_NT, bytes, st>>>(p); break;
+      case 2: if constexpr (KPT >= 2) topk_reg_kernel<KPT, 2, false><<<grid, TK_NT, bytes, st>>>(p); break;
+      case 4: if constexpr (KPT >= 4) topk_reg_kernel<KPT, 4, false><<<grid, TK_NT, bytes, st>>>(p); break;
+      case 8: if constexpr (KPT >= 8) topk_reg_kernel<KPT, 8, false><<<grid, TK_NT, bytes, st>>>(p); break;
+      case 16: if constexpr (KPT >= 16) topk_reg_kernel<KPT, 16, false><<<grid, TK_NT, bytes, st>>>(p); break;
+      default: return fail(LA_ERR_UNSUPPORTED, "topk: sort width");
+    }
+  }
+  LA_LAUNCHED();
+  return LA_OK;
+}
+
+// Register-resident form: rows of at most 8192 keys (a segment's length in
+// segmented mode); sorted output for k up to 4096 of one row per group.
+static int launch_reg(const TopkKParams &p, hipStream_t st) {
+  int kpt = 1;
+  while (kpt * TK_NT < p.n_lds) kpt <<= 1;
+  const int64_t kk = std::min(p.k, p.n_lds);
+  int64_t p2 = TK_NT;
+  while (p2 < kk) p2 <<= 1;
+  const int E = (int)(p2 / TK_NT);
+  const size_t bytes = p.use_bitmap ? (size_t)align16(p.bitmap_words * 4) : (size_t)p2 * 12;
+#define LA_TKR(B)                                          \
+  switch (kpt) {                                           \
+    case 1: return launch_reg_e<B, 1>(p, E, bytes, st);   \
+    case 2: return launch_reg_e<B, 2>(p, E, bytes, st);   \
+    case 4: return launch_reg_e<B, 4>(p, E, bytes, st);   \
+    case 8: return launch_reg_e<B, 8>(p, E, bytes, st);   \
+    case 16: return launch_reg_e<B, 16>(p, E, bytes, st); \
+    case 32: return launch_reg_e<B, 32>(p, E, bytes, st); \
+    default: break;                                        \
+  }
+  if (p.use_bitmap) {
+    LA_TKR(true)
+  } else {
+    LA_TKR(false)
+  }
+#undef LA_TKR
+  return fail(LA_ERR_UNSUPPORTED, "topk: row of %lld keys", (long long)p.n_lds);
+}
+
 int topk_launch(TopkKParams p, hipStream_t st) {
   if (p.NG <= 0) return LA_OK;
   p.use_bitmap = (p.G > 1 || p.sink > 0 || p.window > 0 || p.order == 1) ? 1 : 0;
@@ -531,6 +895,8 @@ int topk_launch(TopkKParams p, hipStream_t st) {
   int64_t p2 = 1;
   while (p2 < p.k) p2 <<= 1;
   p.p2k = p2;
+  if (p.n_lds <= 32 * TK_NT && (p.use_bitmap || (p.G == 1 && std::min(p.k, p.n_lds) <= 16 * TK_NT)))
+    return launch_reg(p, st);
   const int64_t limit = (int64_t)max_dynamic_lds() - (int64_t)sizeof(TkShared) - 256;
   p.lds_keys = 1;
   int64_t bytes = topk_lds_bytes(p);
