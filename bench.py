@@ -32,6 +32,9 @@ if str(ROOT) not in sys.path:
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
 
 C4 = dict(B=64, Hq=32, Hkv=8, T=65536, D=128, page=64, topk=32, seed=0)
+ATTN_KERNEL = "sparse_attn_mfma_kernel"  # the dominant kernel of the C4 step
+COPY_MIB = 1024
+TRAFFIC_FILE = "profiles/c4_attention_traffic.json"
 
 
 def parse():
@@ -43,6 +46,12 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences timed on the CPU")
     ap.add_argument("--shared", action="store_true",
                     help="per-query-head page lists instead of the GQA union")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="C4 only, then a device copy of COPY_MIB MiB (the counter scale "
+                         "reference); run under rocprofv3 --pmc")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two rocprofv3 --pmc runs of --pmc-probe (FETCH_SIZE, then "
+                         "WRITE_SIZE) into " + TRAFFIC_FILE)
     return ap.parse_args()
 
 
@@ -210,8 +219,47 @@ def bench_c5(dev, steps, warmup):
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def _counter_rows(d):
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    return list(csv.DictReader(open(files[0])))
+
+
+def traffic_from(fetch_dir, write_dir):
+    """HBM bytes per launch of the attention kernel from FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads
+    for the device copy of COPY_MIB MiB that --pmc-probe ends with."""
+    copy_bytes = COPY_MIB << 20
+    out = {"kernel": ATTN_KERNEL, "copy_bytes": copy_bytes}
+    for d, name in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
+        rows = [r for r in _counter_rows(d) if r["Counter_Name"] == name]
+        kern = [float(r["Counter_Value"]) for r in rows if ATTN_KERNEL in r["Kernel_Name"]]
+        copies = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        if not kern or not copies:
+            raise SystemExit(f"{name}: kernel or copy dispatches missing in {d}")
+        ref = max(copies)  # the COPY_MIB copy is the largest copy in the probe
+        factor = copy_bytes / (ref * 1024.0)
+        out[name] = {"kib_per_launch": sum(kern) / len(kern), "launches": len(kern),
+                     "copy_kib": ref, "scale": round(factor, 4),
+                     "bytes_per_launch": round(sum(kern) / len(kern) * 1024.0 * factor)}
+    out["traffic_bytes"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
+    out["commands"] = [
+        f"rocprofv3 --pmc {c} --output-format csv -d <dir> -o run -- python -u bench.py --pmc-probe"
+        for c in ("FETCH_SIZE", "WRITE_SIZE")]
+    path = ROOT / TRAFFIC_FILE
+    path.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+    return 0
+
+
 def main() -> int:
     args = parse()
+    if args.traffic_from:
+        return traffic_from(*args.traffic_from)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
@@ -272,6 +320,19 @@ def main() -> int:
         sel.scatter_(-1, idl, True)
         att_bytes = int(sel.sum()) * ps * kv_row_bytes
     att_bytes += q.numel() * 2 + B * Hq * D * 2 + ids.numel() * 4
+    if args.pmc_probe:
+        a = torch.empty(COPY_MIB << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": True, "attn_bytes": att_bytes, "copy_bytes": COPY_MIB << 20}))
+        return 0
+    traffic = None
+    tpath = ROOT / TRAFFIC_FILE
+    if tpath.exists():
+        rec = json.loads(tpath.read_text())
+        if rec.get("kernel") == ATTN_KERNEL:
+            traffic = rec.get("traffic_bytes")
     meta_bytes = 2 * mins.numel() * 2 + B * Hq * (T // ps) * 8 * 2  # min+max, scores w+r
     step_bytes = att_bytes + meta_bytes
     tok_s = B / (ms_step * 1e-3)
@@ -294,9 +355,9 @@ def main() -> int:
         "config": {"workload": "C4 paged Quest sparse decode", "batch": B, "context": T,
                    "page_size": ps, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
                    "budget_tokens": cfg["topk"] * ps, "gqa": "union" if union else "per-head"},
-        "roofline": {"bound": "hbm", "kernel": "sparse_attn_kernel (+ split combine)",
+        "roofline": {"bound": "hbm", "kernel": ATTN_KERNEL + " (+ split combine)",
                      "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": att_bytes, "ms_per_launch": round(ms_att, 4)},
         "step": {"ms_select": round(ms_sel, 4), "ms_attend": round(ms_att, 4),
                  "bytes": step_bytes, "GBps": round(step_gbs, 1),

@@ -186,67 +186,88 @@ __global__ __launch_bounds__(256) void indexer_decode_kernel(IdxKP p) {
 }
 
 // Few queries over a long key axis with 2-byte keys whose (head, dim) block
-// is contiguous and 16-byte aligned (the decode shape of config C5).  128 keys
-// per workgroup: the key rows are staged with coalesced 16-byte loads (16 in
-// flight per thread) into LDS rows padded to 528 bytes (conflict-free 16-byte
-// reads at a row stride), then thread t scores key t for every query of the
-// chunk, heads in order, d in order.
-constexpr int IDF_KEYS = 128, IDF_NT = 128, IDF_ROWB = 528, IDF_BATCH = 16;
+// is contiguous and 16-byte aligned (the decode shape of config C5).  64 keys
+// per workgroup, HI threads per key: the key rows are staged with coalesced
+// 16-byte loads (all in flight at once) into LDS rows padded to 528 bytes;
+// thread (key, head) computes that head's dot for every query of the chunk,
+// d in order, and thread (query, key) then adds the heads in order.
+constexpr int IDF_KEYS = 64, IDF_ROWB = 528;
 
 __device__ __forceinline__ float half_bits_to_f32(uint32_t bits16, int dt) {
   return dt == LA_BF16 ? bf16_bits_to_f32(bits16) : __half2float(__ushort_as_half((uint16_t)bits16));
 }
 
-__global__ __launch_bounds__(IDF_NT) void indexer_decode16_kernel(IdxKP p) {
+template <int HI>
+__global__ __launch_bounds__(IDF_KEYS * HI) void indexer_decode16_kernel(IdxKP p) {
+  constexpr int NT = IDF_KEYS * HI;
+  constexpr int CPT = (IDF_KEYS * ID_MAXHD / 8 + NT - 1) / NT;  // 16-byte chunks per thread (max)
   __shared__ __align__(16) unsigned char sk[IDF_KEYS * IDF_ROWB];
   __shared__ double sqd[ID_MAXQ][ID_MAXHD];
+  __shared__ double sdot[ID_MAXQ][IDF_KEYS][HI];
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.y;
   const int64_t k0 = (int64_t)blockIdx.x * IDF_KEYS;
-  const int hd = (int)(p.HI * p.d);
+  const int d = (int)p.d;
+  const int hd = HI * d;
   const int cpr = hd / 8;  // 16-byte chunks per key row
-  for (int i = tid; i < p.tn * hd; i += IDF_NT) {
-    const int tl = i / hd, c = i % hd;
-    const int h = c / (int)p.d, dd = c % (int)p.d;
-    sqd[tl][c] = load_as_f64(p.q, b * p.q_sb + (p.t0 + tl) * p.q_st + h * p.q_sh + dd, p.dt);
-  }
   const uint16_t *kb = (const uint16_t *)p.k + b * p.k_sb;
-  const int total = IDF_KEYS * cpr;
-  for (int base = 0; base < total; base += IDF_NT * IDF_BATCH) {
-    uint4 v[IDF_BATCH];
+  {
+    uint4 v[CPT];
 #pragma unroll
-    for (int u = 0; u < IDF_BATCH; ++u) {
-      const int c = base + u * IDF_NT + tid;
+    for (int u = 0; u < CPT; ++u) {
+      const int c = tid + u * NT;
       const int r = c / cpr, col = c % cpr;
       const int64_t s = k0 + r;
-      v[u] = (c < total && s < p.Tk) ? *(const uint4 *)(kb + s * p.k_st + col * 8) : uint4{0, 0, 0, 0};
+      v[u] = (r < IDF_KEYS && s < p.Tk) ? *(const uint4 *)(kb + s * p.k_st + col * 8) : uint4{0, 0, 0, 0};
+    }
+    for (int i = tid; i < p.tn * hd; i += NT) {
+      const int tl = i / hd, c = i % hd;
+      const int h = c / d, dd = c % d;
+      sqd[tl][c] = load_as_f64(p.q, b * p.q_sb + (p.t0 + tl) * p.q_st + h * p.q_sh + dd, p.dt);
     }
 #pragma unroll
-    for (int u = 0; u < IDF_BATCH; ++u) {
-      const int c = base + u * IDF_NT + tid;
-      if (c < total) *(uint4 *)(sk + (c / cpr) * IDF_ROWB + (c % cpr) * 16) = v[u];
+    for (int u = 0; u < CPT; ++u) {
+      const int c = tid + u * NT;
+      if (c < IDF_KEYS * cpr) *(uint4 *)(sk + (c / cpr) * IDF_ROWB + (c % cpr) * 16) = v[u];
     }
   }
   __syncthreads();
-  const int64_t s = k0 + tid;
-  if (s >= p.Tk) return;
-  const unsigned char *row = sk + tid * IDF_ROWB;
-  for (int tl = 0; tl < p.tn; ++tl) {
+  {
+    const int h = tid % HI, r = tid / HI;
+    const unsigned char *row = sk + r * IDF_ROWB + h * d * 2;
+    double dot[ID_MAXQ] = {0.0, 0.0, 0.0, 0.0};
+    for (int dd = 0; dd < d; dd += 8) {
+      const uint4 kv = *(const uint4 *)(row + dd * 2);
+      const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+      double kf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kf[2 * e] = (double)half_bits_to_f32(w4[e] & 0xffffu, p.dt);
+        kf[2 * e + 1] = (double)half_bits_to_f32(w4[e] >> 16, p.dt);
+      }
+#pragma unroll
+      for (int tl = 0; tl < ID_MAXQ; ++tl) {
+        if (tl >= p.tn) break;
+        const double *qv = &sqd[tl][h * d + dd];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dot[tl] = __builtin_fma(qv[e], kf[e], dot[tl]);
+      }
+    }
+#pragma unroll
+    for (int tl = 0; tl < ID_MAXQ; ++tl)
+      if (tl < p.tn) sdot[tl][r][h] = dot[tl];
+  }
+  __syncthreads();
+  for (int i = tid; i < IDF_KEYS * p.tn; i += NT) {
+    const int r = i % IDF_KEYS, tl = i / IDF_KEYS;
+    const int64_t s = k0 + r;
+    if (s >= p.Tk) continue;
     const int64_t t = p.t0 + tl;
     double acc = 0.0;
-    for (int h = 0; h < p.HI; ++h) {
-      double dot = 0.0;
-      for (int dd = 0; dd < p.d; dd += 8) {
-        const uint4 kv = *(const uint4 *)(row + (h * p.d + dd) * 2);
-        const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
-        const double *qv = &sqd[tl][h * p.d + dd];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dot = __builtin_fma(qv[2 * e], (double)half_bits_to_f32(w4[e] & 0xffffu, p.dt), dot);
-          dot = __builtin_fma(qv[2 * e + 1], (double)half_bits_to_f32(w4[e] >> 16, p.dt), dot);
-        }
-      }
-      const double rl = dot > 0.0 ? dot : 0.0;
+    for (int h = 0; h < HI; ++h) {
+      const double dv = sdot[tl][r][h];
+      const double rl = dv > 0.0 ? dv : 0.0;
       acc = add_product(acc, (double)p.w[b * p.w_sb + t * p.w_st + h * p.w_sh], rl);
     }
     p.scores[(b * p.tn + tl) * p.Tk + s] = acc;
@@ -321,6 +342,7 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
   const bool decode = a->Tq <= ID_MAXQ && a->HI * a->d <= ID_MAXHD;
   // fast decode form: 2-byte keys, (head, dim) block contiguous and 16-byte aligned
   const bool decode16 = decode && (a->in_dtype == LA_BF16 || a->in_dtype == LA_F16) &&
+                        (a->HI == 1 || a->HI == 2 || a->HI == 4 || a->HI == 8) &&
                         a->k_sh == a->d && a->d % 8 == 0 && a->k_st % 8 == 0 &&
                         a->k_sb % 8 == 0 && (uintptr_t)a->kk % 16 == 0;
   for (int64_t t0 = 0; t0 < a->Tq; t0 += chunk) {
@@ -344,8 +366,13 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     p.causal = a->causal;
     p.unit = std::max<int64_t>(1, a->causal_unit);
     if (decode16) {
-      indexer_decode16_kernel<<<dim3((unsigned)ceil_div(a->Tk, IDF_KEYS), (unsigned)a->B), IDF_NT,
-                                0, st>>>(p);
+      const dim3 grid((unsigned)ceil_div(a->Tk, IDF_KEYS), (unsigned)a->B);
+      switch (a->HI) {
+        case 1: indexer_decode16_kernel<1><<<grid, IDF_KEYS * 1, 0, st>>>(p); break;
+        case 2: indexer_decode16_kernel<2><<<grid, IDF_KEYS * 2, 0, st>>>(p); break;
+        case 4: indexer_decode16_kernel<4><<<grid, IDF_KEYS * 4, 0, st>>>(p); break;
+        default: indexer_decode16_kernel<8><<<grid, IDF_KEYS * 8, 0, st>>>(p); break;
+      }
     } else if (decode) {
       indexer_decode_kernel<<<dim3((unsigned)ceil_div(a->Tk, ID_KEYS), (unsigned)a->B), 256, 0,
                               st>>>(p);

@@ -60,9 +60,12 @@ def test_indexer_causal_with_offset(dev):
 
 
 @pytest.mark.parametrize("tq", [1, 3])
-def test_indexer_decode_form(dev, tq):
-    """A few queries against a long key axis (the per-key kernel)."""
-    q, k, w = inputs(3, tq, 5000, 4, 64, seed=5, dtype=torch.bfloat16)
+@pytest.mark.parametrize("hi,d,dtype", [(4, 64, torch.bfloat16), (1, 256, torch.bfloat16),
+                                        (2, 128, torch.float16), (8, 32, torch.bfloat16)])
+def test_indexer_decode_form(dev, tq, hi, d, dtype):
+    """A few queries against a long key axis (the per-key kernel: 2-byte keys,
+    hi threads per key)."""
+    q, k, w = inputs(3, tq, 5000, hi, d, seed=5 + hi, dtype=dtype)
     check(q, k, w, 512, dev, causal=True, offset=5000 - tq)
 
 
