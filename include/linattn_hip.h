@@ -159,6 +159,37 @@ int la_quest_scores(const void *q, int32_t q_dtype, int64_t B, int64_t Hq, int64
                     void *stream);
 
 /*
+ * Quest page selection in one pass (scores + top-k + GQA union), for the
+ * default union mode of QuestAttention.page_selection (variants/selection.py:
+ * 214-237, union at :232-235) over page-minor metadata from
+ * la_quest_page_bounds: for every (b, KV head, query t) the Hq/Hkv query
+ * heads score all pages exactly as la_quest_scores does, each head keeps its
+ * top k = max(1, min(k, n_pages)) visible pages (page start <= pos_offset + t)
+ * with the own page forced, and the union of the heads' pages is written in
+ * ascending order to out_idx[((b*Hkv + kvh)*Tq + t)*(G*k) + i], -1 padded,
+ * with the number kept in out_count.  Identical to la_quest_scores followed by
+ * la_topk_rows with group = G, order = 1, force_own = 1, pos_unit = page_size.
+ * Returns LA_ERR_UNSUPPORTED (nothing launched) when the metadata is not
+ * page-minor (m_sp == 1, m_sd a multiple of 4) or has more pages than one
+ * workgroup holds (4096 for G <= 4, 2048 for G = 8); callers then use the two
+ * separate entry points.
+ */
+typedef struct {
+  const void *q;
+  const void *page_min;
+  const void *page_max;
+  int32_t *out_idx;
+  int32_t *out_count;
+  int64_t B, Hq, Hkv, Tq, D;
+  int64_t q_sb, q_sh, q_st;
+  int64_t n_pages, m_sb, m_sh, m_sp, m_sd;
+  int64_t page_size, pos_offset, k;
+  int32_t q_dtype, meta_dtype;
+} la_quest_select_args;
+
+int la_quest_select(const la_quest_select_args *a, void *stream);
+
+/*
  * Row-wise top-k with ties broken by lowest index.
  * Replaces topk_blocks (variants/selection.py:51-59), the torch.topk calls of
  * page_select_torch / page_select_triton (quest_pages.py:76-77, 159-160),

@@ -28,6 +28,7 @@ EXPORTED = (
     "la_sparse_attention",
     "la_quest_page_bounds",
     "la_quest_scores",
+    "la_quest_select",
     "la_topk_rows_workspace",
     "la_topk_rows",
     "la_indexer_topk_workspace",
@@ -67,6 +68,15 @@ class LaTopkArgs(ctypes.Structure):
                 ("group", _i64), ("k", _i64), ("width", _i64), ("sink_units", _i64),
                 ("window_units", _i64), ("pos_offset", _i64), ("pos_unit", _i64),
                 ("force_own", _i32), ("order", _i32)]
+
+
+class LaQuestSelectArgs(ctypes.Structure):
+    _fields_ = [("q", _vp), ("page_min", _vp), ("page_max", _vp), ("out_idx", _vp),
+                ("out_count", _vp), ("B", _i64), ("Hq", _i64), ("Hkv", _i64), ("Tq", _i64),
+                ("D", _i64), ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64), ("n_pages", _i64),
+                ("m_sb", _i64), ("m_sh", _i64), ("m_sp", _i64), ("m_sd", _i64),
+                ("page_size", _i64), ("pos_offset", _i64), ("k", _i64), ("q_dtype", _i32),
+                ("meta_dtype", _i32)]
 
 
 class LaIndexerArgs(ctypes.Structure):
@@ -123,6 +133,7 @@ def load() -> ctypes.CDLL:
                                        _i64, _i64, _i64, _i64, _i32, _vp]
     L.la_quest_scores.argtypes = [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp,
                                   _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]
+    L.la_quest_select.argtypes = [P(LaQuestSelectArgs), _vp]
     L.la_topk_rows_workspace.argtypes = [P(LaTopkArgs)]
     L.la_topk_rows_workspace.restype = ctypes.c_size_t
     L.la_topk_rows.argtypes = [P(LaTopkArgs), _vp]

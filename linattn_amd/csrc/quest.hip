@@ -6,6 +6,7 @@
 
 #include "common.h"
 #include "kv_access.h"
+#include "topk_select.h"
 
 namespace la {
 
@@ -214,6 +215,123 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
   }
 }
 
+// Quest selection of one (b, KV head, query) in a single pass: the page
+// scores of the G query heads (as in quest_scores_kernel, page-minor metadata)
+// go to LDS as order keys, with the query's own page forced; each head's top-k
+// is selected from there (register radix select) into a union bitmap, which
+// is written in ascending page order.  Equals quest_scores_kernel followed by
+// the union top-k, without the score rows leaving the chip.
+struct QsKP {
+  const void *q, *mn, *mx;
+  int32_t *out_idx, *out_count;
+  int64_t Hq, Hkv, Tq, D, q_sb, q_sh, q_st, n_pages, m_sb, m_sh, m_sd;
+  int64_t page_size, pos_offset, k, width;
+  int32_t q_dt;
+};
+
+template <int MT, int G, int KPT>
+__global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
+  constexpr int NP = TK_NT * KPT;  // pages held (>= n_pages)
+  constexpr int PPT = 4, QD = 8;
+  extern __shared__ __align__(16) uint64_t keys[];  // [G][NP]
+  __shared__ double qd[G * 256];
+  __shared__ TkRegShared<KPT> sr;
+  __shared__ uint32_t bm[NP / 32];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;  // (b, kvh, t)
+  const int64_t t = row % a.Tq;
+  const int64_t kvh = (row / a.Tq) % a.Hkv;
+  const int64_t b = row / (a.Tq * a.Hkv);
+  const int64_t D = a.D;
+  for (int64_t i = tid; i < G * D; i += TK_NT) {
+    const int64_t g = i / D, d = i % D;
+    qd[g * D + d] = load_as_f64(a.q, b * a.q_sb + (kvh * G + g) * a.q_sh + t * a.q_st + d, a.q_dt);
+  }
+  for (int i = tid; i < NP / 32; i += TK_NT) bm[i] = 0u;
+  const int64_t pos = a.pos_offset + t;
+  const int64_t u_own = pos >= 0 ? pos / a.page_size : -1;
+  const int32_t n_v = (int32_t)min(a.n_pages, u_own + 1);
+  const int32_t own = (int32_t)min(u_own, a.n_pages - 1);
+  const bool force = own >= 0 && own < n_v;
+  __syncthreads();
+
+  using V = typename std::conditional<MT == LA_BF16, uint2, float4>::type;
+  constexpr int ESZ = MT == LA_BF16 ? 2 : 4;
+  const int64_t mbase = b * a.m_sb + kvh * a.m_sh;
+  const int64_t sd = a.m_sd / PPT;  // vectors per d step
+  for (int c = 0; c < KPT / 4; ++c) {
+    const int p0 = c * TK_NT * PPT + tid * PPT;
+    double acc[G][PPT];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) acc[g][i] = 0.0;
+    if (p0 < a.m_sd) {  // m_sd = pages rounded up to 4: the padded storage
+      const V *pl = (const V *)((const char *)a.mn + (mbase + p0) * ESZ);
+      const V *ph = (const V *)((const char *)a.mx + (mbase + p0) * ESZ);
+      V lo_v[2][QD], hi_v[2][QD];
+      auto fetch = [&](int64_t d0, int buf) {
+#pragma unroll
+        for (int j = 0; j < QD; ++j) {
+          const bool ok = d0 + j < D;
+          lo_v[buf][j] = ok ? pl[(d0 + j) * sd] : V{};
+          hi_v[buf][j] = ok ? ph[(d0 + j) * sd] : V{};
+        }
+      };
+      auto widen = [](const V &v, double (&x)[PPT]) {
+        if constexpr (MT == LA_BF16) {
+          x[0] = bf16lo(v.x); x[1] = bf16hi(v.x); x[2] = bf16lo(v.y); x[3] = bf16hi(v.y);
+        } else {
+          x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+        }
+      };
+      auto consume = [&](int64_t d0, int buf) {
+#pragma unroll
+        for (int j = 0; j < QD; ++j) {
+          if (d0 + j >= D) break;
+          double lo[PPT], hi[PPT];
+          widen(lo_v[buf][j], lo);
+          widen(hi_v[buf][j], hi);
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const double qv = qd[g * D + d0 + j];
+            const bool pos_q = qv >= 0.0;
+#pragma unroll
+            for (int i = 0; i < PPT; ++i) acc[g][i] = __builtin_fma(qv, pos_q ? hi[i] : lo[i], acc[g][i]);
+          }
+        }
+      };
+      fetch(0, 0);
+      for (int64_t d0 = 0; d0 < D; d0 += 2 * QD) {
+        if (d0 + QD < D) fetch(d0 + QD, 1);
+        consume(d0, 0);
+        if (d0 + QD >= D) break;
+        if (d0 + 2 * QD < D) fetch(d0 + 2 * QD, 0);
+        consume(d0 + QD, 1);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int pg = p0 + i;
+        keys[g * NP + pg] = (force && pg == own) ? KEY_FORCED : ord_key(acc[g][i]);
+      }
+  }
+  __syncthreads();
+  const uint32_t K = (uint32_t)min(a.k, (int64_t)n_v);
+  for (int g = 0; g < G; ++g) {
+    uint64_t u[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) u[j] = keys[g * NP + tid + TK_NT * j];
+    tk_reg_select<KPT>(u, n_v, K, sr, [&](int j, int32_t i, bool take) {
+      if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    });
+  }
+  tk_emit_bitmap_row(bm, n_v, own, 0, 0, a.width, a.out_idx + row * a.width,
+                     a.out_count ? a.out_count + row : nullptr, sr.wtmp[1]);
+}
+
 template <int MT, int G>
 static int launch_scores(const void *q, int q_dt, int64_t B, int64_t Hq, int64_t Tq, int64_t D,
                          int64_t q_sb, int64_t q_sh, int64_t q_st, const void *mn, const void *mx,
@@ -316,4 +434,85 @@ extern "C" int la_quest_scores(const void *q, int32_t q_dtype, int64_t B, int64_
 #undef LA_QS_G
 #undef LA_QS
   return fail(LA_ERR_UNSUPPORTED, "la_quest_scores: GQA group %lld not in {1,2,4,8}", (long long)G);
+}
+
+template <int MT, int G, int KPT>
+static int launch_select(const QsKP &k, int64_t rows, hipStream_t st) {
+  const size_t bytes = (size_t)G * TK_NT * KPT * 8;
+  if (bytes > 65536) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      LA_HIP(hipFuncSetAttribute((const void *)quest_select_kernel<MT, G, KPT>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+      attr_set = true;
+    }
+  }
+  quest_select_kernel<MT, G, KPT><<<dim3((unsigned)rows), TK_NT, bytes, st>>>(k);
+  LA_LAUNCHED();
+  return LA_OK;
+}
+
+template <int MT, int G>
+static int launch_select_kpt(const QsKP &k, int64_t rows, hipStream_t st) {
+  if (k.n_pages <= 1024) return launch_select<MT, G, 4>(k, rows, st);
+  if (k.n_pages <= 2048) return launch_select<MT, G, 8>(k, rows, st);
+  if constexpr (G <= 4) return launch_select<MT, G, 16>(k, rows, st);
+  return fail(LA_ERR_UNSUPPORTED, "la_quest_select: too many pages for one workgroup");
+}
+
+extern "C" int la_quest_select(const la_quest_select_args *a, void *stream) {
+  LA_REQUIRE(a && a->q && a->page_min && a->page_max && a->out_idx, "la_quest_select: null pointer");
+  LA_REQUIRE(a->B > 0 && a->Hq > 0 && a->Tq > 0 && a->Hkv > 0 && a->n_pages > 0 && a->k > 0,
+             "la_quest_select: bad shape");
+  LA_REQUIRE(a->D > 0 && a->D <= 256, "la_quest_select: head_dim must be in [1, 256]");
+  LA_REQUIRE(a->Hq % a->Hkv == 0, "la_quest_select: n_heads must be a multiple of n_kv_heads");
+  LA_REQUIRE(a->page_size > 0, "la_quest_select: page_size");
+  LA_REQUIRE(a->q_dtype == LA_F32 || a->q_dtype == LA_BF16 || a->q_dtype == LA_F16,
+             "la_quest_select: q dtype");
+  LA_REQUIRE(a->meta_dtype == LA_F32 || a->meta_dtype == LA_BF16, "la_quest_select: meta dtype");
+  const int64_t G = a->Hq / a->Hkv;
+  const int64_t esz = a->meta_dtype == LA_BF16 ? 2 : 4;
+  // page-minor metadata, 4 pages per aligned vector
+  const bool layout = a->m_sp == 1 && a->m_sd % 4 == 0 && a->m_sd >= a->n_pages &&
+                      a->m_sb % 4 == 0 && a->m_sh % 4 == 0 &&
+                      (uintptr_t)a->page_min % (4 * esz) == 0 && (uintptr_t)a->page_max % (4 * esz) == 0;
+  if (!layout || a->n_pages > (G <= 4 ? 4096 : 2048) || !(G == 1 || G == 2 || G == 4 || G == 8))
+    return fail(LA_ERR_UNSUPPORTED, "la_quest_select: shape or metadata layout not fused");
+  QsKP k{};
+  k.q = a->q;
+  k.mn = a->page_min;
+  k.mx = a->page_max;
+  k.out_idx = a->out_idx;
+  k.out_count = a->out_count;
+  k.Hq = a->Hq;
+  k.Hkv = a->Hkv;
+  k.Tq = a->Tq;
+  k.D = a->D;
+  k.q_sb = a->q_sb;
+  k.q_sh = a->q_sh;
+  k.q_st = a->q_st;
+  k.n_pages = a->n_pages;
+  k.m_sb = a->m_sb;
+  k.m_sh = a->m_sh;
+  k.m_sd = a->m_sd;
+  k.page_size = a->page_size;
+  k.pos_offset = a->pos_offset;
+  k.k = std::max<int64_t>(1, std::min(a->k, a->n_pages));
+  k.width = G * k.k;
+  k.q_dt = a->q_dtype;
+  const int64_t rows = a->B * a->Hkv * a->Tq;
+  hipStream_t st = (hipStream_t)stream;
+#define LA_QSEL(MT)                                                  \
+  switch (G) {                                                       \
+    case 1: return launch_select_kpt<MT, 1>(k, rows, st);           \
+    case 2: return launch_select_kpt<MT, 2>(k, rows, st);           \
+    case 4: return launch_select_kpt<MT, 4>(k, rows, st);           \
+    default: return launch_select_kpt<MT, 8>(k, rows, st);          \
+  }
+  if (a->meta_dtype == LA_BF16) {
+    LA_QSEL(LA_BF16)
+  } else {
+    LA_QSEL(LA_F32)
+  }
+#undef LA_QSEL
 }

@@ -15,11 +15,10 @@
 #include <algorithm>
 
 #include "topk.h"
+#include "topk_select.h"
 
 namespace la {
 
-constexpr int TK_NT = 256;
-constexpr int TK_NW = TK_NT / 64;
 constexpr int TK_BATCH = 8;  // keys read per thread before they are used
 
 struct TkShared {
@@ -27,32 +26,6 @@ struct TkShared {
   uint32_t wtmp[2][TK_NW];
   uint32_t sel_bin, above, bin_cnt;
 };
-
-__device__ __forceinline__ uint64_t lanemask_lt(int lane) {
-  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
-}
-
-// Inclusive scan of one value per thread across the workgroup.
-__device__ __forceinline__ uint32_t tk_block_incl_scan(uint32_t v, uint32_t *wtmp, uint32_t &total) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(v, off, 64);
-    if (lane >= off) v += y;
-  }
-  if (lane == 63) wtmp[w] = v;
-  __syncthreads();
-  uint32_t base = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < TK_NW; ++i) {
-    const uint32_t x = wtmp[i];
-    base += (i < w) ? x : 0u;
-    tot += x;
-  }
-  __syncthreads();
-  total = tot;
-  return v + base;
-}
 
 struct RowKeys {
   const double *row;
@@ -224,43 +197,10 @@ __device__ __forceinline__ TkRow tk_row(const TopkKParams &p) {
   return r;
 }
 
-// Sink and window units are OR'd into the bitmap, which is then emitted in
-// ascending index order, -1 padded, with the count of kept units.
-__device__ void tk_emit_bitmap(const TopkKParams &p, uint32_t *bm, const TkRow &rw,
-                               uint32_t *wtmp) {
-  const int tid = threadIdx.x;
-  const int64_t n_v = rw.n_v, own = rw.own;
-  if (n_v > 0) {
-    const int64_t s_end = min(p.sink, n_v);
-    for (int64_t i = tid; i < s_end; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
-    if (p.window > 0 && own >= 0) {
-      const int64_t w0 = max((int64_t)0, own - p.window + 1);
-      const int64_t w1 = min(own, n_v - 1);
-      for (int64_t i = w0 + tid; i <= w1; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
-    }
-  }
-  __syncthreads();
-  // each thread owns a run of bitmap words
-  const int64_t words = (n_v + 31) / 32;
-  const int64_t wpt = (words + TK_NT - 1) / TK_NT;
-  const int64_t w_beg = min(words, (int64_t)tid * wpt), w_end = min(words, w_beg + wpt);
-  uint32_t cnt = 0;
-  for (int64_t x = w_beg; x < w_end; ++x) cnt += __popc(bm[x]);
-  uint32_t total;
-  const uint32_t incl = tk_block_incl_scan(cnt, wtmp, total);
-  uint32_t pos = incl - cnt;
-  int32_t *oi = p.out_idx + rw.orow * p.width;
-  for (int64_t x = w_beg; x < w_end; ++x) {
-    uint32_t bits = bm[x];
-    while (bits) {
-      const int b = __ffs(bits) - 1;
-      if (pos < (uint32_t)p.width) oi[pos] = (int32_t)(x * 32 + b);
-      ++pos;
-      bits &= bits - 1;
-    }
-  }
-  for (int64_t jj = (int64_t)total + tid; jj < p.width; jj += TK_NT) oi[jj] = -1;
-  if (p.out_count && tid == 0) p.out_count[rw.orow] = (int32_t)min((int64_t)total, p.width);
+__device__ __forceinline__ void tk_emit_bitmap(const TopkKParams &p, uint32_t *bm, const TkRow &rw,
+                                               uint32_t *wtmp) {
+  tk_emit_bitmap_row(bm, rw.n_v, rw.own, p.sink, p.window, p.width, p.out_idx + rw.orow * p.width,
+                     p.out_count ? p.out_count + rw.orow : nullptr, wtmp);
 }
 
 __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
@@ -432,13 +372,10 @@ template <int KPT, int E, bool BITMAP>
 __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
   constexpr int P = TK_NT * E;  // sort width (sorted form)
   extern __shared__ __align__(16) unsigned char dyn[];
-  __shared__ uint32_t hist[TK_NW][256];
-  __shared__ uint32_t eqc[KPT][TK_NW];
-  __shared__ uint64_t red[2][TK_NW];
-  __shared__ uint32_t wtmp[2][TK_NW];
-  __shared__ uint32_t s_bin, s_above, s_cnt, s_fill, s_first_pad;
+  __shared__ TkRegShared<KPT> sr;
+  __shared__ uint32_t s_fill, s_first_pad;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
   const uint64_t lt = lanemask_lt(lane);
   const TkRow rw = tk_row(p);
   const int32_t n_v = (int32_t)rw.n_v;  // n_v <= 256*KPT
@@ -475,107 +412,12 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
       u[j] = (rw.force && i == own) ? KEY_FORCED : x;
     }
     const uint32_t K = (uint32_t)rw.K;
-    uint64_t prefix = 0, mask = 0;
-    uint32_t need = K;
-    bool all_in = (int32_t)K >= n_v;
-    if (!all_in) {
-      // leading bits shared by every valid key are fixed without a pass
-      uint64_t o = 0, a = ~0ull;
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        if (tid + TK_NT * j < n_v) {
-          o |= u[j];
-          a &= u[j];
-        }
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        o |= __shfl_xor(o, off, 64);
-        a &= __shfl_xor(a, off, 64);
-      }
-      if (lane == 0) {
-        red[0][w] = o;
-        red[1][w] = a;
-      }
-      __syncthreads();
-      o = 0;
-      a = ~0ull;
-#pragma unroll
-      for (int x = 0; x < TK_NW; ++x) {
-        o |= red[0][x];
-        a &= red[1][x];
-      }
-      const uint64_t diff = o ^ a;
-      int top = diff ? 63 - __clzll((long long)diff) : -1;
-      mask = top >= 0 ? ~((2ull << top) - 1ull) : ~0ull;  // 2ull << 63 wraps to 0
-      prefix = a & mask;
-      while (top >= 0) {
-        const int shift = top >= 7 ? top - 7 : 0;
-        const uint32_t dm = (2u << (top - shift)) - 1u;  // digit of top-shift+1 <= 8 bits
-#pragma unroll
-        for (int x = 0; x < TK_NW; ++x) hist[x][tid] = 0u;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-          if (tid + TK_NT * j < n_v && (u[j] & mask) == prefix)
-            atomicAdd(&hist[w][(uint32_t)(u[j] >> shift) & dm], 1u);
-        }
-        __syncthreads();
-        uint32_t c = 0;
-#pragma unroll
-        for (int x = 0; x < TK_NW; ++x) c += hist[x][255 - tid];
-        uint32_t tot;
-        const uint32_t incl = tk_block_incl_scan(c, wtmp[0], tot);
-        if (incl >= need && incl - c < need) {
-          s_bin = 255 - tid;
-          s_above = incl - c;
-          s_cnt = c;
-        }
-        __syncthreads();
-        need -= s_above;
-        prefix |= (uint64_t)s_bin << shift;
-        mask |= (uint64_t)dm << shift;
-        const bool done = s_cnt == need;
-        __syncthreads();
-        if (done) {
-          all_in = true;
-          break;
-        }
-        top = shift - 1;
-      }
-    }
-    // Keys above the threshold are all taken; keys equal to it are taken in
-    // index order until `need` is met (lowest index first).
-    if (!all_in) {
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        const bool eq = tid + TK_NT * j < n_v && (u[j] & mask) == prefix;
-        const uint64_t b = __ballot(eq);
-        if (lane == 0) eqc[j][w] = (uint32_t)__popcll(b);
-      }
-      __syncthreads();
-    }
-    uint32_t eq_before = 0;  // threshold keys in earlier register slots
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const int32_t i = tid + TK_NT * j;
-      const bool valid = i < n_v;
-      const uint64_t um = u[j] & mask;
-      const bool gt = valid && um > prefix;
-      const bool eq = valid && um == prefix;
-      bool take = gt || (eq && all_in);
-      if (!all_in) {
-        const uint64_t b = __ballot(eq);
-        uint32_t rank = eq_before + (uint32_t)__popcll(b & lt);
-#pragma unroll
-        for (int x = 0; x < TK_NW; ++x) rank += x < w ? eqc[j][x] : 0u;
-        take = gt || (eq && rank < need);
-#pragma unroll
-        for (int x = 0; x < TK_NW; ++x) eq_before += eqc[j][x];
-      }
-      if constexpr (BITMAP) {
+    if constexpr (BITMAP) {
+      tk_reg_select<KPT>(u, n_v, K, sr, [&](int j, int32_t i, bool take) {
         if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
-      } else {
+      });
+    } else {
+      tk_reg_select<KPT>(u, n_v, K, sr, [&](int j, int32_t i, bool take) {
         const uint64_t tm = __ballot(take);
         uint32_t base = 0;
         if (lane == 0 && tm) base = atomicAdd(&s_fill, (uint32_t)__popcll(tm));
@@ -585,12 +427,11 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
           skey[pos] = u[j];
           sidx[pos] = i;
         }
-      }
+      });
     }
-    __syncthreads();
   }
   if constexpr (BITMAP) {
-    tk_emit_bitmap(p, bm, rw, wtmp[1]);
+    tk_emit_bitmap(p, bm, rw, sr.wtmp[1]);
   } else {
     // sorted form (one row per workgroup)
     const int32_t K = (int32_t)rw.K;

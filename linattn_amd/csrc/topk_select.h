@@ -1,0 +1,202 @@
+// Workgroup-collective pieces of the row top-k, shared by the top-k kernels
+// and the fused Quest selection.  Ordering: order-preserving 64-bit image of
+// the fp64 score (ord_key), higher first; equal keys go to the lower index.
+#pragma once
+
+#include "common.h"
+
+namespace la {
+
+constexpr int TK_NT = 256;  // threads of a selecting workgroup
+constexpr int TK_NW = TK_NT / 64;
+
+__device__ __forceinline__ uint64_t lanemask_lt(int lane) {
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Inclusive scan of one value per thread across the workgroup.
+__device__ __forceinline__ uint32_t tk_block_incl_scan(uint32_t v, uint32_t *wtmp, uint32_t &total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(v, off, 64);
+    if (lane >= off) v += y;
+  }
+  if (lane == 63) wtmp[w] = v;
+  __syncthreads();
+  uint32_t base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < TK_NW; ++i) {
+    const uint32_t x = wtmp[i];
+    base += (i < w) ? x : 0u;
+    tot += x;
+  }
+  __syncthreads();
+  total = tot;
+  return v + base;
+}
+
+template <int KPT>
+struct TkRegShared {
+  uint32_t hist[TK_NW][256];
+  uint32_t eqc[KPT][TK_NW];
+  uint64_t red[2][TK_NW];
+  uint32_t wtmp[2][TK_NW];
+  uint32_t bin, above, cnt;
+};
+
+// Top K of the keys u[j] of units t + 256*j (t = thread), j < KPT, among the
+// first n_v units.  A radix select fixes the leading bits every valid key
+// shares without a pass, then resolves 8-bit digits (per-wave histograms)
+// until the threshold digit is taken whole or all bits are fixed; keys equal
+// to the final threshold are taken lowest index first.  emit(j, i, take) is
+// then called by every thread for every slot j, in increasing j (so it may
+// use wave-collective operations); `take` marks the K selected units.
+// Collective over the workgroup; ends with the workgroup in step.
+template <int KPT, class Emit>
+__device__ __forceinline__ void tk_reg_select(const uint64_t (&u)[KPT], int32_t n_v, uint32_t K,
+                                              TkRegShared<KPT> &sh, Emit emit) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint64_t lt = lanemask_lt(lane);
+  uint64_t prefix = 0, mask = 0;
+  uint32_t need = K;
+  bool all_in = (int32_t)K >= n_v;
+  if (!all_in) {
+    uint64_t o = 0, a = ~0ull;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      if (tid + TK_NT * j < n_v) {
+        o |= u[j];
+        a &= u[j];
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      o |= __shfl_xor(o, off, 64);
+      a &= __shfl_xor(a, off, 64);
+    }
+    if (lane == 0) {
+      sh.red[0][w] = o;
+      sh.red[1][w] = a;
+    }
+    __syncthreads();
+    o = 0;
+    a = ~0ull;
+#pragma unroll
+    for (int x = 0; x < TK_NW; ++x) {
+      o |= sh.red[0][x];
+      a &= sh.red[1][x];
+    }
+    const uint64_t diff = o ^ a;
+    int top = diff ? 63 - __clzll((long long)diff) : -1;
+    mask = top >= 0 ? ~((2ull << top) - 1ull) : ~0ull;  // 2ull << 63 wraps to 0
+    prefix = a & mask;
+    while (top >= 0) {
+      const int shift = top >= 7 ? top - 7 : 0;
+      const uint32_t dm = (2u << (top - shift)) - 1u;  // digit of top-shift+1 <= 8 bits
+#pragma unroll
+      for (int x = 0; x < TK_NW; ++x) sh.hist[x][tid] = 0u;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        if (tid + TK_NT * j < n_v && (u[j] & mask) == prefix)
+          atomicAdd(&sh.hist[w][(uint32_t)(u[j] >> shift) & dm], 1u);
+      }
+      __syncthreads();
+      uint32_t c = 0;
+#pragma unroll
+      for (int x = 0; x < TK_NW; ++x) c += sh.hist[x][255 - tid];
+      uint32_t tot;
+      const uint32_t incl = tk_block_incl_scan(c, sh.wtmp[0], tot);
+      if (incl >= need && incl - c < need) {
+        sh.bin = 255 - tid;
+        sh.above = incl - c;
+        sh.cnt = c;
+      }
+      __syncthreads();
+      need -= sh.above;
+      prefix |= (uint64_t)sh.bin << shift;
+      mask |= (uint64_t)dm << shift;
+      const bool done = sh.cnt == need;
+      __syncthreads();
+      if (done) {
+        all_in = true;
+        break;
+      }
+      top = shift - 1;
+    }
+  }
+  // Keys above the threshold are all taken; keys equal to it are taken in
+  // index order until `need` is met.
+  if (!all_in) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool eq = tid + TK_NT * j < n_v && (u[j] & mask) == prefix;
+      const uint64_t b = __ballot(eq);
+      if (lane == 0) sh.eqc[j][w] = (uint32_t)__popcll(b);
+    }
+    __syncthreads();
+  }
+  uint32_t eq_before = 0;  // threshold keys in earlier slots
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int32_t i = tid + TK_NT * j;
+    const bool valid = i < n_v;
+    const uint64_t um = u[j] & mask;
+    const bool gt = valid && um > prefix;
+    const bool eq = valid && um == prefix;
+    bool take = gt || (eq && all_in);
+    if (!all_in) {
+      const uint64_t b = __ballot(eq);
+      uint32_t rank = eq_before + (uint32_t)__popcll(b & lt);
+#pragma unroll
+      for (int x = 0; x < TK_NW; ++x) rank += x < w ? sh.eqc[j][x] : 0u;
+      take = gt || (eq && rank < need);
+#pragma unroll
+      for (int x = 0; x < TK_NW; ++x) eq_before += sh.eqc[j][x];
+    }
+    emit(j, i, take);
+  }
+  __syncthreads();
+}
+
+// Sink units [0, sink) and the window (own - window, own] are OR'd into the
+// bitmap of kept units, which is then written in ascending index order to
+// out[0, width), -1 padded; *count (if given) gets the number kept.
+__device__ __forceinline__ void tk_emit_bitmap_row(uint32_t *bm, int64_t n_v, int64_t own,
+                                                   int64_t sink, int64_t window, int64_t width,
+                                                   int32_t *out, int32_t *count, uint32_t *wtmp) {
+  const int tid = threadIdx.x;
+  if (n_v > 0) {
+    const int64_t s_end = min(sink, n_v);
+    for (int64_t i = tid; i < s_end; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    if (window > 0 && own >= 0) {
+      const int64_t w0 = max((int64_t)0, own - window + 1);
+      const int64_t w1 = min(own, n_v - 1);
+      for (int64_t i = w0 + tid; i <= w1; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    }
+  }
+  __syncthreads();
+  // each thread owns a run of bitmap words
+  const int64_t words = (n_v + 31) / 32;
+  const int64_t wpt = (words + TK_NT - 1) / TK_NT;
+  const int64_t w_beg = min(words, (int64_t)tid * wpt), w_end = min(words, w_beg + wpt);
+  uint32_t cnt = 0;
+  for (int64_t x = w_beg; x < w_end; ++x) cnt += __popc(bm[x]);
+  uint32_t total;
+  const uint32_t incl = tk_block_incl_scan(cnt, wtmp, total);
+  uint32_t pos = incl - cnt;
+  for (int64_t x = w_beg; x < w_end; ++x) {
+    uint32_t bits = bm[x];
+    while (bits) {
+      const int b = __ffs(bits) - 1;
+      if (pos < (uint32_t)width) out[pos] = (int32_t)(x * 32 + b);
+      ++pos;
+      bits &= bits - 1;
+    }
+  }
+  for (int64_t jj = (int64_t)total + tid; jj < width; jj += TK_NT) out[jj] = -1;
+  if (count && tid == 0) *count = (int32_t)min((int64_t)total, width);
+}
+
+}  // namespace la

@@ -146,11 +146,31 @@ def quest_select_hip(q: torch.Tensor, mins: torch.Tensor, maxs: torch.Tensor, *,
     the union of their pages: ids (B, Hkv, Tq, G*k) ascending, -1 padded.
     Otherwise each query head keeps its own list: ids (B, Hq, Tq, k) by
     (score desc, index asc).  Also returns counts (valid entries per list)."""
-    scores = page_scores_hip(q, mins, maxs)
-    B, Hq, Tq, P = scores.shape
-    Hkv = mins.shape[1]
+    dev = N.require_gpu(q, mins, maxs, what="quest_select_hip")
+    B, Hq, Tq, D = q.shape
+    Hkv, P = mins.shape[1], mins.shape[2]
     G = Hq // Hkv
     k = max(1, min(int(topk), P))
+    if mins.shape != (B, Hkv, P, D) or maxs.shape != mins.shape or Hq % Hkv:
+        raise ValueError("mins/maxs must be (B, Hkv, P, D) with Hq a multiple of Hkv")
+    if gqa_union and G > 1 and mins.stride() == maxs.stride() and mins.dtype == maxs.dtype:
+        # one pass: scores, per-head top-k and the union (la_quest_select)
+        ids = torch.empty(B, Hkv, Tq, G * k, dtype=torch.int32, device=dev)
+        counts = torch.empty(B, Hkv, Tq, dtype=torch.int32, device=dev)
+        a = N.LaQuestSelectArgs()
+        a.q, a.page_min, a.page_max = q.data_ptr(), mins.data_ptr(), maxs.data_ptr()
+        a.out_idx, a.out_count = ids.data_ptr(), counts.data_ptr()
+        a.B, a.Hq, a.Hkv, a.Tq, a.D = B, Hq, Hkv, Tq, D
+        a.q_sb, a.q_sh, a.q_st = q.stride(0), q.stride(1), q.stride(2)
+        a.n_pages = P
+        a.m_sb, a.m_sh, a.m_sp, a.m_sd = mins.stride()
+        a.page_size, a.pos_offset, a.k = page_size, offset, k
+        a.q_dtype, a.meta_dtype = N.dtype_code(q.dtype), N.dtype_code(mins.dtype)
+        rc = N.load().la_quest_select(ctypes.byref(a), N.stream_handle(dev))
+        if rc != N.LA_ERR_UNSUPPORTED:
+            N.check(rc, "quest_select_hip")
+            return ids, counts
+    scores = page_scores_hip(q, mins, maxs)
     if gqa_union and G > 1:
         ids, counts, _ = _topk(scores, k=k, width=G * k, group=G, order=1, pos_offset=offset,
                                pos_unit=page_size, force_own=True)

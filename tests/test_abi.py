@@ -20,6 +20,7 @@ STRUCTS = {
     "la_kv": N.LaKV,
     "la_sparse_attn_args": N.LaSparseAttnArgs,
     "la_topk_args": N.LaTopkArgs,
+    "la_quest_select_args": N.LaQuestSelectArgs,
     "la_indexer_args": N.LaIndexerArgs,
     "la_block_select_args": N.LaBlockSelectArgs,
     "la_prefill_args": N.LaPrefillArgs,

@@ -95,6 +95,21 @@ def test_quest_select_bit_exact(dev, union, hq, hkv, tq, offset):
     assert np.array_equal(counts.cpu().numpy(), (ref >= 0).sum(-1))
 
 
+@pytest.mark.parametrize("hq,hkv,ps,t", [(32, 8, 16, 16384), (16, 2, 64, 65536), (8, 4, 8, 4000)])
+def test_quest_select_fused_equals_two_pass(dev, hq, hkv, ps, t):
+    """The one-pass union selection (page-minor metadata) equals scores +
+    top-k run separately (row-major metadata takes that path), including
+    queries whose position cuts the page range short."""
+    q, k, _ = make_inputs(2, hq, hkv, 3, t, 64, seed=hq + ps)
+    q, k = q.bfloat16(), k.bfloat16()
+    mins, maxs = page_update_hip(k.to(dev), ps)
+    for offset in (t - 3, t // 3, 5):
+        a, ca = quest_select_hip(q.to(dev), mins, maxs, page_size=ps, topk=24, offset=offset)
+        b, cb = quest_select_hip(q.to(dev), mins.contiguous(), maxs.contiguous(), page_size=ps,
+                                 topk=24, offset=offset)
+        assert torch.equal(a, b) and torch.equal(ca, cb), offset
+
+
 def test_page_select_api_matches_reference_semantics(dev):
     """page_select_torch (quest_pages.py:58-78) with the D1 fix."""
     q, k, _ = make_inputs(1, 4, 4, 24, 96, 32, seed=5)
