@@ -116,6 +116,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     }
   };
 
+  // m: running max of the raw (unscaled) scores of this lane's query
   float m = __int_as_float(0xff800000), l = 0.f;
   f32x4 acc[8];
 #pragma unroll
@@ -142,32 +143,36 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       }
       st[kt] = sacc;
     }
-    // scale, mask, online softmax (column c16 = this lane's query)
+    // mask, online softmax (column c16 = this lane's query); the positive
+    // scale commutes with the max, so it is applied inside the exponent
     const int64_t key0 = (int64_t)kb * PF_BS;
     const bool need_mask =
         kb < 0 || (p.causal && key0 + PF_BS - 1 > qb * PF_BS + w * 16) || key0 + PF_BS > p.T;
+    if (need_mask) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t key = key0 + 16 * kt + 4 * g + e;
+          if (kb < 0 || (p.causal && key > q_row) || key >= p.T) st[kt][e] = __int_as_float(0xff800000);
+        }
+    }
     float mx = __int_as_float(0xff800000);
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float s = st[kt][e] * p.qscale;
-        if (need_mask) {
-          const int64_t key = key0 + 16 * kt + 4 * g + e;
-          if (kb < 0 || (p.causal && key > q_row) || key >= p.T) s = __int_as_float(0xff800000);
-        }
-        st[kt][e] = s;
-        mx = fmaxf(mx, s);
-      }
+      mx = fmaxf(mx, fmaxf(fmaxf(st[kt][0], st[kt][1]), fmaxf(st[kt][2], st[kt][3])));
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float mn = fmaxf(m, mx);
-    const float mu = (mn == __int_as_float(0xff800000)) ? 0.f : mn;
-    const float alpha = fast_exp2(m - mu);
-    m = mn;
-    l *= alpha;
+    // rescale only when some lane's maximum grew (rare after the first blocks)
+    if (__ballot(mn > m) != 0) {
+      const float alpha = mn > m ? fast_exp2((m - mn) * p.qscale) : 1.f;
+      l *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      m = mn;
+    }
+    const float mu = (m == __int_as_float(0xff800000)) ? 0.f : m * p.qscale;
     // P = P_hi + P_lo in bf16 (P_lo = bf16(P - P_hi)): the product keeps ~16
     // mantissa bits of each weight, so bf16 rounding of P costs ~2^-17
     // relative instead of 2^-9 (which alone exceeds 2e-3 on rows whose mass
@@ -178,8 +183,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pv[e] = fast_exp2(st[2 * s2][e] - mu);
-        pv[4 + e] = fast_exp2(st[2 * s2 + 1][e] - mu);
+        pv[e] = fast_exp2(__builtin_fmaf(st[2 * s2][e], p.qscale, -mu));
+        pv[4 + e] = fast_exp2(__builtin_fmaf(st[2 * s2 + 1][e], p.qscale, -mu));
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) l += pv[e];
