@@ -319,15 +319,19 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
       }
   }
   __syncthreads();
+  // each wave selects its heads' pages (w, w + 4, ...) into the union bitmap
   const uint32_t K = (uint32_t)min(a.k, (int64_t)n_v);
-  for (int g = 0; g < G; ++g) {
-    uint64_t u[KPT];
+  const int w = tid >> 6, lane = tid & 63;
+  constexpr int KPL = NP / 64;
+  for (int g = w; g < G; g += TK_NW) {
+    uint64_t u[KPL];
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) u[j] = keys[g * NP + tid + TK_NT * j];
-    tk_reg_select<KPT>(u, n_v, K, sr, [&](int j, int32_t i, bool take) {
+    for (int j = 0; j < KPL; ++j) u[j] = keys[g * NP + lane + 64 * j];
+    tk_wave_select<KPL>(u, n_v, K, sr.hist[w], [&](int j, int32_t i, bool take) {
       if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
     });
   }
+  __syncthreads();
   tk_emit_bitmap_row(bm, n_v, own, 0, 0, a.width, a.out_idx + row * a.width,
                      a.out_count ? a.out_count + row : nullptr, sr.wtmp[1]);
 }
