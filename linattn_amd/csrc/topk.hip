@@ -360,6 +360,67 @@ __device__ __forceinline__ void tk_local_stage(uint64_t (&key)[E], int32_t (&idx
   }
 }
 
+// Sorts 256*E unsigned 64-bit values descending, E per thread (thread t holds
+// positions t*E .. t*E + E - 1): bitonic network with in-register, in-wave
+// (shuffle) and cross-wave (LDS, `buf` of 256*E values) stages.
+template <int S, int E>
+__device__ __forceinline__ void tk_local_desc(uint64_t (&c)[E], int tid, int size) {
+  if constexpr (S < E) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (e & S) continue;
+      const int el = e | S;
+      const bool down = ((tid * E + e) & size) == 0;  // descending run
+      const uint64_t a = c[e], b = c[el];
+      const bool sw = down ? (b > a) : (a > b);
+      c[e] = sw ? b : a;
+      c[el] = sw ? a : b;
+    }
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void tk_bitonic_desc(uint64_t (&c)[E], int tid, uint64_t *buf) {
+  constexpr int P = TK_NT * E;
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride < E) {
+        switch (stride) {
+          case 1: tk_local_desc<1, E>(c, tid, size); break;
+          case 2: tk_local_desc<2, E>(c, tid, size); break;
+          case 4: tk_local_desc<4, E>(c, tid, size); break;
+          case 8: tk_local_desc<8, E>(c, tid, size); break;
+          default: break;
+        }
+      } else if (stride < 64 * E) {
+        const int lx = stride / E;
+        // position i keeps the larger of the pair when it is the lower one of
+        // a descending run (or the upper one of an ascending run)
+        const int i0 = tid * E;
+        const bool keep_max = (((i0 & stride) == 0) == ((i0 & size) == 0));
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const uint64_t pc = __shfl_xor(c[e], lx, 64);
+          c[e] = keep_max ? (pc > c[e] ? pc : c[e]) : (pc < c[e] ? pc : c[e]);
+        }
+      } else {
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e) buf[tid * E + e] = c[e];
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int i = tid * E + e;
+          const uint64_t pc = buf[i ^ stride];
+          const bool keep_max = (((i & stride) == 0) == ((i & size) == 0));
+          c[e] = keep_max ? (pc > c[e] ? pc : c[e]) : (pc < c[e] ? pc : c[e]);
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
 // Register-resident top-k for rows of at most 256*KPT keys (thread t holds
 // the keys of units t + 256*j).  Selection is the radix select above, started
 // at the highest bit where the row's valid keys differ (common leading bits
@@ -392,6 +453,8 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
   }
   if (tid == 0) s_fill = 0;
   __syncthreads();
+  // the scores of the (single) row of the sorted form
+  const double *rp_row = p.scores + ((rw.br / p.Tq) * p.G * p.Tq + rw.tl) * p.row_stride + rw.seg0;
 
   for (int64_t g = 0; g < p.G; ++g) {
     const int64_t row = ((rw.br / p.Tq) * p.G + g) * p.Tq + rw.tl;
@@ -433,21 +496,57 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
   if constexpr (BITMAP) {
     tk_emit_bitmap(p, bm, rw, sr.wtmp[1]);
   } else {
-    // sorted form (one row per workgroup)
+    // sorted form (one row per workgroup).  The K survivors are first sorted
+    // as single 64-bit composites: the key with its low 13 bits replaced by
+    // 8191 - index (rows hold at most 8192 units), so one unsigned compare
+    // orders them by (key desc, index asc) unless two keys differ only in
+    // their low 13 bits.  The result is then checked with the full keys
+    // (re-read from the row) and, if any neighbouring pair is out of order,
+    // sorted again on (key, index).
     const int32_t K = (int32_t)rw.K;
     for (int32_t i = K + tid; i < P; i += TK_NT) {
       skey[i] = 0;
       sidx[i] = -1;
     }
-    if (tid == 0) s_first_pad = (uint32_t)K;
+    if (tid == 0) {
+      s_first_pad = (uint32_t)K;
+      s_fill = 0;  // reused as the order-violation flag
+    }
     __syncthreads();
-    uint64_t key[E];
-    int32_t idx[E];
+    uint64_t c[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      key[e] = skey[tid * E + e];
-      idx[e] = sidx[tid * E + e];
+      const uint64_t k0 = skey[tid * E + e];
+      const int32_t i0 = sidx[tid * E + e];
+      c[e] = i0 >= 0 ? ((k0 & ~0x1FFFull) | (uint64_t)(0x1FFF - i0)) : 0ull;
     }
+    tk_bitonic_desc<E>(c, tid, skey);
+    uint64_t key[E];
+    int32_t idx[E];
+    {
+      double v[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        idx[e] = c[e] ? 0x1FFF - (int32_t)(c[e] & 0x1FFF) : -1;
+        v[e] = idx[e] >= 0 ? rp_row[idx[e]] : 0.0;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        key[e] = idx[e] < 0 ? 0ull : (rw.force && idx[e] == own) ? KEY_FORCED : ord_key(v[e]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      skey[tid * E + e] = key[e];
+      sidx[tid * E + e] = idx[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = tid * E + e;
+      if (i + 1 < K && !tk_precedes(key[e], idx[e], skey[i + 1], sidx[i + 1])) atomicOr(&s_fill, 1u);
+    }
+    __syncthreads();
     const auto precedes = tk_precedes;
     // position i keeps, of itself and its partner, the one that comes first
     // (ascending run) or last (descending run)
@@ -460,37 +559,39 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
         idx[e] = pi;
       }
     };
-    for (int size = 2; size <= P; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        if (stride < E) {
-          // partner in the same thread: constant register indices per stride
-          switch (stride) {
-            case 1: tk_local_stage<1, E>(key, idx, tid, size); break;
-            case 2: tk_local_stage<2, E>(key, idx, tid, size); break;
-            case 4: tk_local_stage<4, E>(key, idx, tid, size); break;
-            case 8: tk_local_stage<8, E>(key, idx, tid, size); break;
-            default: break;
-          }
-        } else if (stride < 64 * E) {
-          const int lx = stride / E;
+    if (s_fill) {  // exact (key, index) sort; rare
+      for (int size = 2; size <= P; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          if (stride < E) {
+            // partner in the same thread: constant register indices per stride
+            switch (stride) {
+              case 1: tk_local_stage<1, E>(key, idx, tid, size); break;
+              case 2: tk_local_stage<2, E>(key, idx, tid, size); break;
+              case 4: tk_local_stage<4, E>(key, idx, tid, size); break;
+              case 8: tk_local_stage<8, E>(key, idx, tid, size); break;
+              default: break;
+            }
+          } else if (stride < 64 * E) {
+            const int lx = stride / E;
 #pragma unroll
-          for (int e = 0; e < E; ++e) {
-            const uint64_t pk = __shfl_xor(key[e], lx, 64);
-            const int32_t pi = __shfl_xor(idx[e], lx, 64);
-            exchange(e, tid * E + e, size, stride, pk, pi);
-          }
-        } else {
-          __syncthreads();
+            for (int e = 0; e < E; ++e) {
+              const uint64_t pk = __shfl_xor(key[e], lx, 64);
+              const int32_t pi = __shfl_xor(idx[e], lx, 64);
+              exchange(e, tid * E + e, size, stride, pk, pi);
+            }
+          } else {
+            __syncthreads();
 #pragma unroll
-          for (int e = 0; e < E; ++e) {
-            skey[tid * E + e] = key[e];
-            sidx[tid * E + e] = idx[e];
-          }
-          __syncthreads();
+            for (int e = 0; e < E; ++e) {
+              skey[tid * E + e] = key[e];
+              sidx[tid * E + e] = idx[e];
+            }
+            __syncthreads();
 #pragma unroll
-          for (int e = 0; e < E; ++e) {
-            const int i = tid * E + e;
-            exchange(e, i, size, stride, skey[i ^ stride], sidx[i ^ stride]);
+            for (int e = 0; e < E; ++e) {
+              const int i = tid * E + e;
+              exchange(e, i, size, stride, skey[i ^ stride], sidx[i ^ stride]);
+            }
           }
         }
       }

@@ -43,3 +43,18 @@ def test_topk_short_rows_pad(dev):
         ri, rv = oracle.topk_rows(sc[0, h].numpy(), 64, n_valid=np.arange(5) // 8 + 1)
         assert np.array_equal(ids[0, h].cpu().numpy(), ri)
     assert (ids[0, :, :, 1:] == -1).all()
+
+
+def test_topk_sorted_keys_differing_in_low_bits(dev):
+    """Scores that differ only in their lowest mantissa bits (the sorted form
+    first orders truncated keys, then must detect and repair the order)."""
+    g = torch.Generator().manual_seed(7)
+    n = 3000
+    base = torch.full((1, 1, 2, n), 1.5, dtype=torch.float64)
+    steps = torch.randperm(n, generator=g).to(torch.float64)
+    sc = base + steps * 2.0 ** -51  # ulps apart: equal above the low 13 bits
+    sc[0, 0, 1] = torch.randn(n, generator=g, dtype=torch.float64)  # an ordinary row
+    ids, vals = run(sc.to(dev), 700)
+    ri, rv = oracle.topk_rows(sc[0, 0].numpy(), 700)
+    assert np.array_equal(ids[0, 0].cpu().numpy(), ri)
+    assert np.array_equal(vals[0, 0].cpu().numpy(), rv.astype(np.float32))
