@@ -800,8 +800,9 @@ static int launch_reg_e(const TopkKParams &p, int E, size_t bytes, hipStream_t s
   return LA_OK;
 }
 
-// Register-resident form: rows of at most 8192 keys (a segment's length in
-// segmented mode); sorted output for k up to 4096 of one row per group.
+// Register-resident form: rows of at most 8192 keys (16384 for the bitmap
+// form; a segment's length in segmented mode); sorted output for k up to 4096
+// of one row per group.
 static int launch_reg(const TopkKParams &p, hipStream_t st) {
   int kpt = 1;
   while (kpt * TK_NT < p.n_lds) kpt <<= 1;
@@ -818,6 +819,7 @@ static int launch_reg(const TopkKParams &p, hipStream_t st) {
     case 8: return launch_reg_e<B, 8>(p, E, bytes, st);   \
     case 16: return launch_reg_e<B, 16>(p, E, bytes, st); \
     case 32: return launch_reg_e<B, 32>(p, E, bytes, st); \
+    case 64: if constexpr (B) return launch_reg_e<B, 64>(p, E, bytes, st); break; \
     default: break;                                        \
   }
   if (p.use_bitmap) {
@@ -837,7 +839,9 @@ int topk_launch(TopkKParams p, hipStream_t st) {
   int64_t p2 = 1;
   while (p2 < p.k) p2 <<= 1;
   p.p2k = p2;
-  if (p.n_lds <= 32 * TK_NT && (p.use_bitmap || (p.G == 1 && std::min(p.k, p.n_lds) <= 16 * TK_NT)))
+  // register-resident rows: up to 8192 keys (16384 for the bitmap form)
+  if ((p.use_bitmap && p.n_lds <= 64 * TK_NT) ||
+      (p.n_lds <= 32 * TK_NT && p.G == 1 && std::min(p.k, p.n_lds) <= 16 * TK_NT))
     return launch_reg(p, st);
   const int64_t limit = (int64_t)max_dynamic_lds() - (int64_t)sizeof(TkShared) - 256;
   p.lds_keys = 1;
