@@ -8,7 +8,8 @@
 //
 // Per workgroup: 4 waves x 16 queries.  For every listed key block the K block
 // (64 x 128) and V^T (128 x 64) are staged in LDS, double buffered, with the
-// next block's global loads in flight while the current one is multiplied.
+// global loads of the two following blocks in flight (two register stages)
+// while the current one is multiplied.
 //   S^T = K Q^T   : v_mfma_f32_16x16x32_bf16, A = K rows from LDS, B = Q rows
 //                   held in registers; lane (g = lane/16, c = lane%16) ends
 //                   with S^T[key 16*kt + 4g + e][query c].
@@ -83,30 +84,33 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // global -> register staging of one key block
   const int kq = tid & 15;  // V: keys 4kq..4kq+3
   const int dc = tid >> 4;  // V: dims 8dc..8dc+7
-  uint4 kr[4], vr[4];
-  auto gload = [&](int kb) {
+  // register staging of one key block (global -> registers -> LDS)
+  struct Stage {
+    uint4 k[4], v[4];
+  };
+  auto gload = [&](int kb, Stage &r) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ch = tid + i * PF_NT;  // K chunk: key ch/16, 8 dims at (ch%16)*8
       const int64_t key = (int64_t)kb * PF_BS + (ch >> 4);
       const bool kok = kb >= 0 && key < p.T;  // -1 list entries read nothing
-      kr[i] = kok ? *(const uint4 *)(kbh + key * p.k_st + (ch & 15) * 8) : uint4{0, 0, 0, 0};
+      r.k[i] = kok ? *(const uint4 *)(kbh + key * p.k_st + (ch & 15) * 8) : uint4{0, 0, 0, 0};
       const int64_t vkey = (int64_t)kb * PF_BS + kq * 4 + i;
       const bool vok = kb >= 0 && vkey < p.T;
-      vr[i] = vok ? *(const uint4 *)(vbh + vkey * p.v_st + dc * 8) : uint4{0, 0, 0, 0};
+      r.v[i] = vok ? *(const uint4 *)(vbh + vkey * p.v_st + dc * 8) : uint4{0, 0, 0, 0};
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, const Stage &r) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ch = tid + i * PF_NT;
-      *(uint4 *)&sK[buf][(ch >> 4) * PF_KP + (ch & 15) * 8] = kr[i];
+      *(uint4 *)&sK[buf][(ch >> 4) * PF_KP + (ch & 15) * 8] = r.k[i];
     }
     // V^T: row d holds keys; 4 keys x 8 dims -> 8 rows of 4 keys (8 bytes)
-    const uint32_t a[4][4] = {{vr[0].x, vr[0].y, vr[0].z, vr[0].w},
-                              {vr[1].x, vr[1].y, vr[1].z, vr[1].w},
-                              {vr[2].x, vr[2].y, vr[2].z, vr[2].w},
-                              {vr[3].x, vr[3].y, vr[3].z, vr[3].w}};
+    const uint32_t a[4][4] = {{r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w},
+                              {r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w},
+                              {r.v[2].x, r.v[2].y, r.v[2].z, r.v[2].w},
+                              {r.v[3].x, r.v[3].y, r.v[3].z, r.v[3].w}};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {  // dims 8dc + 2j, 8dc + 2j + 1
       const uint2 lo = {pack2(a[0][j], a[1][j], 0x05040100u), pack2(a[2][j], a[3][j], 0x05040100u)};
@@ -122,15 +126,19 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Two register stages: while block j is multiplied out of LDS, block j+1
+  // waits in registers for its LDS slot and block j+2 is being loaded.
+  Stage R0, R1;
   if (n > 0) {
-    gload(list[0]);
-    lstore(0);
+    gload(list[0], R0);
+    lstore(0, R0);
+    if (n > 1) gload(list[1], R1);
   }
   __syncthreads();
-  for (int j = 0; j < n; ++j) {
+  auto step = [&](int j, Stage &load_into, const Stage &store_from) {
     const int buf = j & 1;
     const int kb = list[j];
-    if (j + 1 < n) gload(list[j + 1]);  // in flight during the math below
+    if (j + 2 < n) gload(list[j + 2], load_into);  // in flight for two blocks
     // S^T = K Q^T
     f32x4 st[4];
 #pragma unroll
@@ -213,8 +221,13 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[s2], acc[dt], 0, 0, 0);
       }
     }
-    if (j + 1 < n) lstore(buf ^ 1);
+    if (j + 1 < n) lstore(buf ^ 1, store_from);
     __syncthreads();
+  };
+  for (int j = 0; j < n; j += 2) {
+    step(j, R0, R1);
+    if (j + 1 >= n) break;
+    step(j + 1, R1, R0);
   }
   // l is a per-lane partial over this lane's keys; sum the 4 lane groups.
   l += __shfl_xor(l, 16, 64);
