@@ -6,18 +6,23 @@
 // in-kernel on the diagonal block.  Head dim 128, bf16 inputs, fp32 accumulate,
 // online softmax in the log2 domain.
 //
-// Per workgroup: 4 waves x 16 queries.  For every listed key block the K block
-// (64 x 128) and V^T (128 x 64) are staged in LDS, double buffered, with the
-// global loads of the two following blocks in flight (two register stages)
-// while the current one is multiplied.
+// Per workgroup: 4 waves = 2 query halves (32 queries) x 2 key halves (32 of
+// every 64-key block).  For every listed key block the K and V blocks (64 x
+// 128, row-major) are staged in LDS, double buffered, with the global loads of
+// the two following blocks in flight (two register stages) while the current
+// one is multiplied.  Each wave reads only its half of K and V and uses each
+// A operand for both of its 16-query groups, so a block costs 64 KiB of LDS
+// reads instead of 128 KiB; the two key halves keep separate online-softmax
+// states that are merged through LDS at the end.
 //   S^T = K Q^T   : v_mfma_f32_16x16x32_bf16, A = K rows from LDS, B = Q rows
 //                   held in registers; lane (g = lane/16, c = lane%16) ends
 //                   with S^T[key 16*kt + 4g + e][query c].
 //   O^T += V^T P^T: P^T is used straight from those registers as the B
 //                   operand -- the contraction index k = 8g + e is mapped to key
-//                   32s + 4g + e (e < 4) or 32s + 16 + 4g + (e - 4), and the A
-//                   operand (V^T rows) is read with the same key mapping, so no
-//                   shuffle of P is needed.
+//                   4g + e (e < 4) or 16 + 4g + (e - 4) of the wave's half,
+//                   and the A operand (V^T rows) is read with the same key
+//                   mapping by LDS transpose reads of the row-major V block,
+//                   so neither P nor V is shuffled.
 // Workgroups are remapped so that the query heads of one KV head and adjacent
 // query blocks run on the same XCD (shared L2 for their common key blocks).
 #include "common.h"
@@ -28,10 +33,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 constexpr int PF_D = 128, PF_BS = 64, PF_NT = 256;
 constexpr int PF_KP = 136;  // K row stride in LDS (bf16): 272 B, conflict-free b128 reads
-constexpr int PF_VP = 72;   // V^T row stride in LDS (bf16): 144 B
+constexpr int PF_VP = 136;  // V row stride in LDS (bf16): 272 B
 
 struct PfKP {
   const uint16_t *q, *k, *v;
@@ -44,13 +51,9 @@ struct PfKP {
   int32_t causal, out_dt;
 };
 
-__device__ __forceinline__ uint32_t pack2(uint32_t lo_src, uint32_t hi_src, uint32_t sel) {
-  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
-}
-
 __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   __shared__ __align__(16) uint16_t sK[2][PF_BS * PF_KP];
-  __shared__ __align__(16) uint16_t sV[2][PF_D * PF_VP];
+  __shared__ __align__(16) uint16_t sV[2][PF_BS * PF_VP];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
@@ -67,13 +70,15 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   const int64_t b = lid / (G * p.nqb * p.Hkv);
   const int64_t h = kvh * G + hg;
 
-  const int64_t q_row = qb * PF_BS + w * 16 + c16;  // this lane's query
-  const bool q_ok = q_row < p.T;
-  bf16x8 qreg[4];
-  {
-    const uint16_t *qp = p.q + b * p.q_sb + h * p.q_sh + min(q_row, p.T - 1) * p.q_st;
+  const int qh = w >> 1, kh = w & 1;  // query half, key half
+  int64_t q_row[2];                    // this lane's query in each 16-query group
+  bf16x8 qreg[2][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qreg[s] = *(const bf16x8 *)(qp + 32 * s + 8 * g);
+  for (int qg = 0; qg < 2; ++qg) {
+    q_row[qg] = qb * PF_BS + 32 * qh + 16 * qg + c16;
+    const uint16_t *qp = p.q + b * p.q_sb + h * p.q_sh + min(q_row[qg], p.T - 1) * p.q_st;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qreg[qg][s] = *(const bf16x8 *)(qp + 32 * s + 8 * g);
   }
   const int32_t *list = p.ids + ((b * p.Hq + h) * p.nqb + qb) * p.width;
   const int n = p.counts ? min((int)p.counts[(b * p.Hq + h) * p.nqb + qb], (int)p.width)
@@ -82,8 +87,6 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   const uint16_t *kbh = p.k + b * p.k_sb + kvh * p.k_sh;
   const uint16_t *vbh = p.v + b * p.v_sb + kvh * p.v_sh;
   // global -> register staging of one key block
-  const int kq = tid & 15;  // V: keys 4kq..4kq+3
-  const int dc = tid >> 4;  // V: dims 8dc..8dc+7
   // register staging of one key block (global -> registers -> LDS)
   struct Stage {
     uint4 k[4], v[4];
@@ -95,9 +98,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       const int64_t key = (int64_t)kb * PF_BS + (ch >> 4);
       const bool kok = kb >= 0 && key < p.T;  // -1 list entries read nothing
       r.k[i] = kok ? *(const uint4 *)(kbh + key * p.k_st + (ch & 15) * 8) : uint4{0, 0, 0, 0};
-      const int64_t vkey = (int64_t)kb * PF_BS + kq * 4 + i;
-      const bool vok = kb >= 0 && vkey < p.T;
-      r.v[i] = vok ? *(const uint4 *)(vbh + vkey * p.v_st + dc * 8) : uint4{0, 0, 0, 0};
+      r.v[i] = kok ? *(const uint4 *)(vbh + key * p.v_st + (ch & 15) * 8) : uint4{0, 0, 0, 0};
     }
   };
   auto lstore = [&](int buf, const Stage &r) {
@@ -106,25 +107,20 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       const int ch = tid + i * PF_NT;
       *(uint4 *)&sK[buf][(ch >> 4) * PF_KP + (ch & 15) * 8] = r.k[i];
     }
-    // V^T: row d holds keys; 4 keys x 8 dims -> 8 rows of 4 keys (8 bytes)
-    const uint32_t a[4][4] = {{r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w},
-                              {r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w},
-                              {r.v[2].x, r.v[2].y, r.v[2].z, r.v[2].w},
-                              {r.v[3].x, r.v[3].y, r.v[3].z, r.v[3].w}};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {  // dims 8dc + 2j, 8dc + 2j + 1
-      const uint2 lo = {pack2(a[0][j], a[1][j], 0x05040100u), pack2(a[2][j], a[3][j], 0x05040100u)};
-      const uint2 hi = {pack2(a[0][j], a[1][j], 0x07060302u), pack2(a[2][j], a[3][j], 0x07060302u)};
-      *(uint2 *)&sV[buf][(dc * 8 + 2 * j) * PF_VP + kq * 4] = lo;
-      *(uint2 *)&sV[buf][(dc * 8 + 2 * j + 1) * PF_VP + kq * 4] = hi;
+    for (int i = 0; i < 4; ++i) {
+      const int ch = tid + i * PF_NT;
+      *(uint4 *)&sV[buf][(ch >> 4) * PF_VP + (ch & 15) * 8] = r.v[i];
     }
   };
 
-  // m: running max of the raw (unscaled) scores of this lane's query
-  float m = __int_as_float(0xff800000), l = 0.f;
-  f32x4 acc[8];
+  // m: running max of the raw (unscaled) scores of this lane's query, per group
+  float m[2] = {__int_as_float(0xff800000), __int_as_float(0xff800000)}, l[2] = {0.f, 0.f};
+  f32x4 acc[2][8];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int qg = 0; qg < 2; ++qg)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[qg][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Two register stages: while block j is multiplied out of LDS, block j+1
   // waits in registers for its LDS slot and block j+2 is being loaded.
@@ -139,86 +135,89 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     const int buf = j & 1;
     const int kb = list[j];
     if (j + 2 < n) gload(list[j + 2], load_into);  // in flight for two blocks
-    // S^T = K Q^T
-    f32x4 st[4];
+    // S^T = K Q^T over this wave's 32 keys, both query groups
+    f32x4 st[2][2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+    for (int kt2 = 0; kt2 < 2; ++kt2) {
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8 a = *(const bf16x8 *)&sK[buf][(16 * kt + c16) * PF_KP + 32 * s + 8 * g];
-        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[s], sacc, 0, 0, 0);
+        const bf16x8 a = *(const bf16x8 *)&sK[buf][(32 * kh + 16 * kt2 + c16) * PF_KP + 32 * s + 8 * g];
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[0][s], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[1][s], s1, 0, 0, 0);
       }
-      st[kt] = sacc;
+      st[0][kt2] = s0;
+      st[1][kt2] = s1;
     }
     // mask, online softmax (column c16 = this lane's query); the positive
     // scale commutes with the max, so it is applied inside the exponent
-    const int64_t key0 = (int64_t)kb * PF_BS;
-    const bool need_mask =
-        kb < 0 || (p.causal && key0 + PF_BS - 1 > qb * PF_BS + w * 16) || key0 + PF_BS > p.T;
-    if (need_mask) {
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t key = key0 + 16 * kt + 4 * g + e;
-          if (kb < 0 || (p.causal && key > q_row) || key >= p.T) st[kt][e] = __int_as_float(0xff800000);
-        }
-    }
-    float mx = __int_as_float(0xff800000);
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-      mx = fmaxf(mx, fmaxf(fmaxf(st[kt][0], st[kt][1]), fmaxf(st[kt][2], st[kt][3])));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(m, mx);
-    // rescale only when some lane's maximum grew (rare after the first blocks)
-    if (__ballot(mn > m) != 0) {
-      const float alpha = mn > m ? fast_exp2((m - mn) * p.qscale) : 1.f;
-      l *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-      m = mn;
-    }
-    const float mu = (m == __int_as_float(0xff800000)) ? 0.f : m * p.qscale;
-    // P = P_hi + P_lo in bf16 (P_lo = bf16(P - P_hi)): the product keeps ~16
-    // mantissa bits of each weight, so bf16 rounding of P costs ~2^-17
-    // relative instead of 2^-9 (which alone exceeds 2e-3 on rows whose mass
-    // sits on a few keys).
+    const int64_t key0 = (int64_t)kb * PF_BS + 32 * kh;  // first key of this half
+    const bool need_mask = kb < 0 || (p.causal && key0 + 31 > qb * PF_BS + 32 * qh) ||
+                           key0 + 32 > p.T;
     bf16x8 ph[2], pl[2];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
+    for (int qg = 0; qg < 2; ++qg) {
+      if (need_mask) {
+#pragma unroll
+        for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t key = key0 + 16 * kt2 + 4 * g + e;
+            if (kb < 0 || (p.causal && key > q_row[qg]) || key >= p.T)
+              st[qg][kt2][e] = __int_as_float(0xff800000);
+          }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(st[qg][0][0], st[qg][0][1]), fmaxf(st[qg][0][2], st[qg][0][3])),
+                       fmaxf(fmaxf(st[qg][1][0], st[qg][1][1]), fmaxf(st[qg][1][2], st[qg][1][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m[qg], mx);
+      // rescale only when some lane's maximum grew (rare after the first blocks)
+      if (__ballot(mn > m[qg]) != 0) {
+        const float alpha = mn > m[qg] ? fast_exp2((m[qg] - mn) * p.qscale) : 1.f;
+        l[qg] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[qg][dt] *= alpha;
+        m[qg] = mn;
+      }
+      const float mu = (m[qg] == __int_as_float(0xff800000)) ? 0.f : m[qg] * p.qscale;
+      // P = P_hi + P_lo in bf16 (P_lo = bf16(P - P_hi)): the product keeps ~16
+      // mantissa bits of each weight, so bf16 rounding of P costs ~2^-17
+      // relative instead of 2^-9 (which alone exceeds 2e-3 on rows whose mass
+      // sits on a few keys).
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pv[e] = fast_exp2(__builtin_fmaf(st[2 * s2][e], p.qscale, -mu));
-        pv[4 + e] = fast_exp2(__builtin_fmaf(st[2 * s2 + 1][e], p.qscale, -mu));
+        pv[e] = fast_exp2(__builtin_fmaf(st[qg][0][e], p.qscale, -mu));
+        pv[4 + e] = fast_exp2(__builtin_fmaf(st[qg][1][e], p.qscale, -mu));
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) l += pv[e];
+      for (int e = 0; e < 8; ++e) l[qg] += pv[e];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
         const bf16x2 h2 = __builtin_convertvector((f32x2{pv[e], pv[e + 1]}), bf16x2);
         const f32x2 hf = __builtin_convertvector(h2, f32x2);
         const bf16x2 l2 = __builtin_convertvector((f32x2{pv[e] - hf[0], pv[e + 1] - hf[1]}), bf16x2);
-        ph[s2][e] = h2[0];
-        ph[s2][e + 1] = h2[1];
-        pl[s2][e] = l2[0];
-        pl[s2][e + 1] = l2[1];
+        ph[qg][e] = h2[0];
+        ph[qg][e + 1] = h2[1];
+        pl[qg][e] = l2[0];
+        pl[qg][e + 1] = l2[1];
       }
     }
-    // O^T += V^T P^T
+    // O^T += V^T P^T over this wave's keys; each V^T operand serves both groups
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
+      // V^T rows through the LDS transpose read: lane (g, j) of a 16-lane group
+      // gets V[k0 + e][16 dt + j], e < 4, when lane i of the group points at
+      // row k0 + i/4, columns 16 dt + 4 (i%4) .. +3
+      const uint16_t *v0 = &sV[buf][(32 * kh + 4 * g + (c16 >> 2)) * PF_VP + 16 * dt + 4 * (c16 & 3)];
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)v0);
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(v0 + 16 * PF_VP));
+      const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const uint16_t *vrow = &sV[buf][(16 * dt + c16) * PF_VP + 32 * s2 + 4 * g];
-        const uint2 lo = *(const uint2 *)vrow;
-        const uint2 hi = *(const uint2 *)(vrow + 16);
-        const uint4 av = {lo.x, lo.y, hi.x, hi.y};
-        const bf16x8 a = *(const bf16x8 *)&av;
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[s2], acc[dt], 0, 0, 0);
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[s2], acc[dt], 0, 0, 0);
+      for (int qg = 0; qg < 2; ++qg) {
+        acc[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[qg], acc[qg][dt], 0, 0, 0);
+        acc[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[qg], acc[qg][dt], 0, 0, 0);
       }
     }
     if (j + 1 < n) lstore(buf ^ 1, store_from);
@@ -230,24 +229,58 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     step(j + 1, R1, R0);
   }
   // l is a per-lane partial over this lane's keys; sum the 4 lane groups.
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  if (!q_ok) return;
-  const int64_t ob = b * p.o_sb + h * p.o_sh + q_row * p.o_st;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
-    const int64_t o = ob + 16 * dt + 4 * g;
-    const f32x4 r = acc[dt] * inv;
-    if (p.out_dt == LA_BF16) {
-      const bf16x2 a = __builtin_convertvector((f32x2{r[0], r[1]}), bf16x2);
-      const bf16x2 c = __builtin_convertvector((f32x2{r[2], r[3]}), bf16x2);
-      uint2 u;
-      u.x = *(const uint32_t *)&a;
-      u.y = *(const uint32_t *)&c;
-      *(uint2 *)((uint16_t *)p.out + o) = u;
-    } else {
-      *(f32x4 *)((float *)p.out + o) = r;
+  for (int qg = 0; qg < 2; ++qg) {
+    l[qg] += __shfl_xor(l[qg], 16, 64);
+    l[qg] += __shfl_xor(l[qg], 32, 64);
+  }
+  // Merge the two key halves: the kh = 1 wave of each query half hands its
+  // state to the kh = 0 wave through LDS (the K buffers are free now).
+  float *red = (float *)&sK[0][0] + qh * (2 * 128 * 16 + 64);
+  float *red_o = red;                   // [qg][d][query]
+  float *red_ml = red + 2 * 128 * 16;   // [qg][m, l][query]
+  if (kh == 1) {
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red_o[(qg * 128 + 16 * dt + 4 * g + e) * 16 + c16] = acc[qg][dt][e];
+      if (g == 0) {
+        red_ml[(qg * 2 + 0) * 16 + c16] = m[qg];
+        red_ml[(qg * 2 + 1) * 16 + c16] = l[qg];
+      }
+    }
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int qg = 0; qg < 2; ++qg) {
+    const float m2 = red_ml[(qg * 2 + 0) * 16 + c16], l2 = red_ml[(qg * 2 + 1) * 16 + c16];
+    const float M = fmaxf(m[qg], m2);
+    const float a1 = (m[qg] == __int_as_float(0xff800000)) ? 0.f : fast_exp2((m[qg] - M) * p.qscale);
+    const float a2 = (m2 == __int_as_float(0xff800000)) ? 0.f : fast_exp2((m2 - M) * p.qscale);
+    const float L = l[qg] * a1 + l2 * a2;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    if (q_row[qg] >= p.T) continue;
+    const int64_t ob = b * p.o_sb + h * p.o_sh + q_row[qg] * p.o_st;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      f32x4 r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        r[e] = (acc[qg][dt][e] * a1 + red_o[(qg * 128 + 16 * dt + 4 * g + e) * 16 + c16] * a2) * inv;
+      const int64_t o = ob + 16 * dt + 4 * g;
+      if (p.out_dt == LA_BF16) {
+        const bf16x2 x = __builtin_convertvector((f32x2{r[0], r[1]}), bf16x2);
+        const bf16x2 y = __builtin_convertvector((f32x2{r[2], r[3]}), bf16x2);
+        uint2 u;
+        u.x = *(const uint32_t *)&x;
+        u.y = *(const uint32_t *)&y;
+        *(uint2 *)((uint16_t *)p.out + o) = u;
+      } else {
+        *(f32x4 *)((float *)p.out + o) = r;
+      }
     }
   }
 }
