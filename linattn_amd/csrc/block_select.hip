@@ -35,6 +35,55 @@ __global__ __launch_bounds__(128) void mean_pool_kernel(const void *x, int dt, i
   }
 }
 
+// The same pooling with the block staged in LDS first: 16-byte loads, every
+// row of the block in flight at once; thread d then adds the rows in order.
+// Needs bs <= 64, D * element size a multiple of 16 bytes and <= 512 bytes,
+// 16-byte aligned rows.
+template <int ESZ>
+__global__ __launch_bounds__(256) void mean_pool_vec_kernel(const void *x, int dt, int64_t T,
+                                                            int64_t D, int64_t sb, int64_t sh,
+                                                            int64_t st, int64_t bs, int64_t H,
+                                                            int64_t nb, double *out) {
+  __shared__ __align__(16) unsigned char rows[64 * 512];
+  const int64_t blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int rb = (int)(D * ESZ);  // bytes per row
+  const int cpr = rb / 16;
+  const int total = (int)bs * cpr;
+  const char *base = (const char *)x + (b * sb + h * sh) * ESZ;
+  uint4 v[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int c = tid + u * 256;
+    if (c < total) {
+      const int64_t row = min(blk * bs + c / cpr, T - 1);
+      v[u] = *(const uint4 *)(base + row * st * ESZ + (c % cpr) * 16);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int c = tid + u * 256;
+    if (c < total) *(uint4 *)(rows + (c / cpr) * rb + (c % cpr) * 16) = v[u];
+  }
+  __syncthreads();
+  for (int64_t d = tid; d < D; d += 256) {
+    double acc = 0.0;
+    for (int64_t i = 0; i < bs; ++i) {
+      const unsigned char *e = rows + i * rb + d * ESZ;
+      double xv;
+      if constexpr (ESZ == 4) {
+        xv = (double)*(const float *)e;
+      } else {
+        const uint32_t bits = *(const uint16_t *)e;
+        xv = dt == LA_BF16 ? (double)bf16_bits_to_f32(bits)
+                           : (double)__half2float(__ushort_as_half((uint16_t)bits));
+      }
+      acc = acc + xv;
+    }
+    out[((b * H + h) * nb + blk) * D + d] = acc / (double)bs;
+  }
+}
+
 constexpr int BS_TQ = 64, BS_TK = 64, BS_DC = 32, BS_NT = 256;
 
 // scores[(b*Hq+h)*nqb + i][j] = sum_d fl(qbar[b,h,i,d] * kbar[b,h/G,j,d]) for
@@ -140,11 +189,26 @@ extern "C" int la_block_select(const la_block_select_args *a, void *stream) {
   double *qbar = (double *)(ws + L.qbar_off);
   double *kbar = (double *)(ws + L.kbar_off);
   double *sc = (double *)(ws + L.sc_off);
-  mean_pool_kernel<<<dim3((unsigned)L.nqb, (unsigned)a->Hq, (unsigned)a->B), 128, 0, st>>>(
-      a->q, a->in_dtype, a->T, a->D, a->q_sb, a->q_sh, a->q_st, a->block, a->Hq, L.nqb, qbar);
+  const int64_t esz = a->in_dtype == LA_F32 ? 4 : 2;
+  auto pool = [&](const void *x, int64_t sb, int64_t sh, int64_t s_t, int64_t H, int64_t nb,
+                  double *out) {
+    const dim3 grid((unsigned)nb, (unsigned)H, (unsigned)a->B);
+    const bool vec = a->block <= 64 && (a->D * esz) % 16 == 0 && a->D * esz <= 512 &&
+                     (uintptr_t)x % 16 == 0 && (sb * esz) % 16 == 0 && (sh * esz) % 16 == 0 &&
+                     (s_t * esz) % 16 == 0;
+    if (vec && esz == 4)
+      mean_pool_vec_kernel<4><<<grid, 256, 0, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
+                                                    a->block, H, nb, out);
+    else if (vec)
+      mean_pool_vec_kernel<2><<<grid, 256, 0, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
+                                                    a->block, H, nb, out);
+    else
+      mean_pool_kernel<<<grid, 128, 0, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t, a->block, H,
+                                             nb, out);
+  };
+  pool(a->q, a->q_sb, a->q_sh, a->q_st, a->Hq, L.nqb, qbar);
   LA_LAUNCHED();
-  mean_pool_kernel<<<dim3((unsigned)L.nkb, (unsigned)a->Hkv, (unsigned)a->B), 128, 0, st>>>(
-      a->k, a->in_dtype, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block, a->Hkv, L.nkb, kbar);
+  pool(a->k, a->k_sb, a->k_sh, a->k_st, a->Hkv, L.nkb, kbar);
   LA_LAUNCHED();
   block_score_kernel<<<dim3((unsigned)ceil_div(L.nkb, BS_TK), (unsigned)ceil_div(L.nqb, BS_TQ),
                             (unsigned)(a->B * a->Hq)),

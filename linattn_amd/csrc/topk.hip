@@ -170,15 +170,15 @@ struct TkRow {
   bool force;
 };
 
-__device__ __forceinline__ TkRow tk_row(const TopkKParams &p) {
+__device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
   TkRow r;
-  // Segmented mode: workgroup gi handles segment gi % nseg of row gi / nseg.
-  r.br = p.seg_len > 0 ? (int64_t)blockIdx.x / p.nseg : (int64_t)blockIdx.x;
-  const int64_t seg = p.seg_len > 0 ? (int64_t)blockIdx.x % p.nseg : 0;
+  // Segmented mode: group gi handles segment gi % nseg of row gi / nseg.
+  r.br = p.seg_len > 0 ? gi / p.nseg : gi;
+  const int64_t seg = p.seg_len > 0 ? gi % p.nseg : 0;
   r.seg0 = seg * p.seg_len;
   r.tl = r.br % p.Tq;
   r.t = r.tl + p.t_base;
-  r.orow = p.seg_len > 0 ? (int64_t)blockIdx.x : (r.br / p.Tq) * p.out_tq + r.t;
+  r.orow = p.seg_len > 0 ? gi : (r.br / p.Tq) * p.out_tq + r.t;
   int64_t n_v = p.n;
   int64_t own = -1;
   if (p.pos_unit > 0) {
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ TkShared sh;
   const int tid = threadIdx.x;
-  const TkRow rw = tk_row(p);
+  const TkRow rw = tk_row(p, blockIdx.x);
   const int64_t seg0 = rw.seg0, tl = rw.tl, orow = rw.orow, n_v = rw.n_v, own = rw.own, K = rw.K;
   const int64_t br = rw.br;
   const bool force = rw.force;
@@ -438,7 +438,7 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const uint64_t lt = lanemask_lt(lane);
-  const TkRow rw = tk_row(p);
+  const TkRow rw = tk_row(p, blockIdx.x);
   const int32_t n_v = (int32_t)rw.n_v;  // n_v <= 256*KPT
   const int32_t own = (int32_t)rw.own;
   uint32_t *bm = nullptr;
@@ -625,6 +625,83 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
     __syncthreads();
     if (p.out_count && tid == 0) p.out_count[rw.orow] = (int32_t)s_first_pad;
   }
+}
+
+// Short rows in the bitmap form (unions, sink, window): one wave per output
+// row, four rows per workgroup, no workgroup barrier.  The wave holds the
+// keys of units lane + 64*j (j < KPL, rows of at most 64*KPL units), selects
+// each source row with tk_wave_select, ORs the ballots of kept units into its
+// own bitmap words, adds sink and window, and writes the kept units in
+// ascending order.
+template <int KPL>
+__global__ __launch_bounds__(TK_NT) void topk_wave_kernel(TopkKParams p) {
+  constexpr int WORDS = 2 * KPL;  // 32-bit bitmap words per row
+  __shared__ uint32_t hist[TK_NW][256];
+  __shared__ uint32_t bms[TK_NW][WORDS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t gi = (int64_t)blockIdx.x * TK_NW + w;
+  if (gi >= p.NG) return;  // whole wave: no barrier follows
+  const TkRow rw = tk_row(p, gi);
+  const int32_t n_v = (int32_t)rw.n_v;
+  const int32_t own = (int32_t)rw.own;
+  uint32_t *bm = bms[w];
+  for (int i = lane; i < WORDS; i += 64) bm[i] = 0u;
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t K = (uint32_t)rw.K;
+  for (int64_t g = 0; g < p.G; ++g) {
+    const int64_t row = ((rw.br / p.Tq) * p.G + g) * p.Tq + rw.tl;
+    const uint64_t *rb = (const uint64_t *)(p.scores + row * p.row_stride + rw.seg0);
+    uint64_t u[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) u[j] = lane + 64 * j < n_v ? rb[lane + 64 * j] : 0ull;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int32_t i = lane + 64 * j;
+      uint64_t x = (u[j] << 1) == 0 ? 0ull : u[j];  // ord_key of the raw bits
+      x = (x >> 63) ? ~x : (x | 0x8000000000000000ull);
+      u[j] = (rw.force && i == own) ? KEY_FORCED : x;
+    }
+    tk_wave_select<KPL>(u, n_v, K, hist[w], [&](int j, int32_t i, bool take) {
+      const uint64_t b = __ballot(take);
+      if (lane == 0) {
+        bm[2 * j] |= (uint32_t)b;
+        bm[2 * j + 1] |= (uint32_t)(b >> 32);
+      }
+    });
+    __builtin_amdgcn_wave_barrier();
+  }
+  // sink and window units
+  if (n_v > 0) {
+    const int64_t s_end = min(p.sink, (int64_t)n_v);
+    for (int64_t i = lane; i < s_end; i += 64) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    if (p.window > 0 && own >= 0) {
+      const int64_t w0 = max((int64_t)0, (int64_t)own - p.window + 1);
+      const int64_t w1 = min((int64_t)own, (int64_t)n_v - 1);
+      for (int64_t i = w0 + lane; i <= w1; i += 64) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  // ascending emission: lane x < WORDS owns word x (units past n_v are never set)
+  const uint32_t word = lane < WORDS ? bm[lane] : 0u;
+  const uint32_t cnt = (uint32_t)__popc(word);
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  const uint32_t total = __shfl(incl, 63, 64);
+  uint32_t pos = incl - cnt;
+  int32_t *oi = p.out_idx + rw.orow * p.width;
+  uint32_t bits = word;
+  while (bits) {
+    const int bb = __ffs(bits) - 1;
+    if (pos < (uint32_t)p.width) oi[pos] = (int32_t)(lane * 32 + bb);
+    ++pos;
+    bits &= bits - 1;
+  }
+  for (int64_t jj = (int64_t)total + lane; jj < p.width; jj += 64) oi[jj] = -1;
+  if (p.out_count && lane == 0) p.out_count[rw.orow] = (int32_t)min((int64_t)total, p.width);
 }
 
 static int64_t align16(int64_t x) { return (x + 15) / 16 * 16; }
@@ -839,6 +916,21 @@ int topk_launch(TopkKParams p, hipStream_t st) {
   int64_t p2 = 1;
   while (p2 < p.k) p2 <<= 1;
   p.p2k = p2;
+  // short bitmap rows: one wave per row
+  if (p.use_bitmap && p.seg_len == 0 && p.n_lds <= 1024) {
+    int kpl = 1;
+    while (kpl * 64 < p.n_lds) kpl <<= 1;
+    const dim3 grid((unsigned)((p.NG + TK_NW - 1) / TK_NW));
+    switch (kpl) {
+      case 1: topk_wave_kernel<1><<<grid, TK_NT, 0, st>>>(p); break;
+      case 2: topk_wave_kernel<2><<<grid, TK_NT, 0, st>>>(p); break;
+      case 4: topk_wave_kernel<4><<<grid, TK_NT, 0, st>>>(p); break;
+      case 8: topk_wave_kernel<8><<<grid, TK_NT, 0, st>>>(p); break;
+      default: topk_wave_kernel<16><<<grid, TK_NT, 0, st>>>(p); break;
+    }
+    LA_LAUNCHED();
+    return LA_OK;
+  }
   // register-resident rows: up to 8192 keys (16384 for the bitmap form)
   if ((p.use_bitmap && p.n_lds <= 64 * TK_NT) ||
       (p.n_lds <= 32 * TK_NT && p.G == 1 && std::min(p.k, p.n_lds) <= 16 * TK_NT))

@@ -58,3 +58,34 @@ def test_topk_sorted_keys_differing_in_low_bits(dev):
     ri, rv = oracle.topk_rows(sc[0, 0].numpy(), 700)
     assert np.array_equal(ids[0, 0].cpu().numpy(), ri)
     assert np.array_equal(vals[0, 0].cpu().numpy(), rv.astype(np.float32))
+
+
+@pytest.mark.parametrize("n,group", [(60, 1), (500, 2), (1024, 4), (3000, 2)])
+def test_topk_union_sink_window(dev, n, group):
+    """Bitmap form (one wave per row for short rows, register form for long):
+    per-head top-k with the own unit forced, union over the group, sink and
+    window units added, ascending order, -1 padded, counts."""
+    g = torch.Generator().manual_seed(n + group)
+    Tq, k, sink, window, unit = 5, 7, 2, 3, 16
+    sc = torch.randint(-4, 5, (1, 2 * group, Tq, n), generator=g).double()
+    pos_offset = n * unit - Tq - 40  # queries see all but the last few units
+    width = group * k + sink + window
+    ids, counts, _ = _topk(sc.to(dev), k=k, width=width, group=group, order=1,
+                           pos_offset=pos_offset, pos_unit=unit, force_own=True, sink=sink,
+                           window=window)
+    for hg in range(2):
+        for t in range(Tq):
+            pos = pos_offset + t
+            own = min(pos // unit, n - 1)
+            n_v = min(n, pos // unit + 1)
+            keep = set()
+            for j in range(group):
+                row = sc[0, hg * group + j, t].numpy()
+                ri, _ = oracle.topk_rows(row, min(k, n_v), n_valid=n_v, own=own, force_own=True)
+                keep.update(int(x) for x in ri if x >= 0)
+            keep.update(range(min(sink, n_v)))
+            keep.update(range(max(0, own - window + 1), own + 1))
+            want = sorted(keep)[:width]
+            got = ids[0, hg, t].cpu().numpy()
+            assert list(got[:len(want)]) == want and (got[len(want):] == -1).all(), (hg, t)
+            assert int(counts[0, hg, t]) == len(want)
