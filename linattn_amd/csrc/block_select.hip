@@ -39,34 +39,33 @@ __global__ __launch_bounds__(128) void mean_pool_kernel(const void *x, int dt, i
 // row of the block in flight at once; thread d then adds the rows in order.
 // Needs bs <= 64, D * element size a multiple of 16 bytes and <= 512 bytes,
 // 16-byte aligned rows.
-template <int ESZ>
-__global__ __launch_bounds__(256) void mean_pool_vec_kernel(const void *x, int dt, int64_t T,
+template <int ESZ, int NT>
+__global__ __launch_bounds__(NT) void mean_pool_vec_kernel(const void *x, int dt, int64_t T,
                                                             int64_t D, int64_t sb, int64_t sh,
                                                             int64_t st, int64_t bs, int64_t H,
                                                             int64_t nb, double *out) {
-  __shared__ __align__(16) unsigned char rows[64 * 512];
+  extern __shared__ __align__(16) unsigned char rows[];  // bs rows of D * ESZ bytes
+  constexpr int CH = 64 * 512 / 16 / NT;                  // chunks per thread (max)
   const int64_t blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int rb = (int)(D * ESZ);  // bytes per row
   const int cpr = rb / 16;
   const int total = (int)bs * cpr;
   const char *base = (const char *)x + (b * sb + h * sh) * ESZ;
-  uint4 v[8];
+  uint4 v[CH];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int c = tid + u * 256;
-    if (c < total) {
-      const int64_t row = min(blk * bs + c / cpr, T - 1);
-      v[u] = *(const uint4 *)(base + row * st * ESZ + (c % cpr) * 16);
-    }
+  for (int u = 0; u < CH; ++u) {
+    const int c = tid + u * NT;
+    const int64_t row = min(blk * bs + c / cpr, T - 1);
+    v[u] = c < total ? *(const uint4 *)(base + row * st * ESZ + (c % cpr) * 16) : uint4{0, 0, 0, 0};
   }
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int c = tid + u * 256;
+  for (int u = 0; u < CH; ++u) {
+    const int c = tid + u * NT;
     if (c < total) *(uint4 *)(rows + (c / cpr) * rb + (c % cpr) * 16) = v[u];
   }
   __syncthreads();
-  for (int64_t d = tid; d < D; d += 256) {
+  for (int64_t d = tid; d < D; d += NT) {
     double acc = 0.0;
     for (int64_t i = 0; i < bs; ++i) {
       const unsigned char *e = rows + i * rb + d * ESZ;
@@ -196,12 +195,21 @@ extern "C" int la_block_select(const la_block_select_args *a, void *stream) {
     const bool vec = a->block <= 64 && (a->D * esz) % 16 == 0 && a->D * esz <= 512 &&
                      (uintptr_t)x % 16 == 0 && (sb * esz) % 16 == 0 && (sh * esz) % 16 == 0 &&
                      (s_t * esz) % 16 == 0;
-    if (vec && esz == 4)
-      mean_pool_vec_kernel<4><<<grid, 256, 0, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
-                                                    a->block, H, nb, out);
+    const size_t lds = (size_t)(a->block * a->D * esz);
+    // 128 threads when one thread per d covers the row (the block stays in LDS
+    // only while it is summed, so several blocks per CU overlap)
+    if (vec && esz == 4 && a->D <= 128)
+      mean_pool_vec_kernel<4, 128><<<grid, 128, lds, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
+                                                           a->block, H, nb, out);
+    else if (vec && esz == 4)
+      mean_pool_vec_kernel<4, 256><<<grid, 256, lds, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
+                                                           a->block, H, nb, out);
+    else if (vec && a->D <= 128)
+      mean_pool_vec_kernel<2, 128><<<grid, 128, lds, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
+                                                           a->block, H, nb, out);
     else if (vec)
-      mean_pool_vec_kernel<2><<<grid, 256, 0, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
-                                                    a->block, H, nb, out);
+      mean_pool_vec_kernel<2, 256><<<grid, 256, lds, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
+                                                           a->block, H, nb, out);
     else
       mean_pool_kernel<<<grid, 128, 0, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t, a->block, H,
                                              nb, out);
