@@ -91,14 +91,27 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   struct Stage {
     uint4 k[4], v[4];
   };
+  // thread chunk i: key (tid/16) + 16 i of the block, 8 dims at (tid%16)*8;
+  // element offsets within a block are loop invariant
+  const int64_t koff = (int64_t)(tid >> 4) * p.k_st + (tid & 15) * 8, kstep = 16 * p.k_st;
+  const int64_t voff = (int64_t)(tid >> 4) * p.v_st + (tid & 15) * 8, vstep = 16 * p.v_st;
   auto gload = [&](int kb, Stage &r) {
+    if (kb >= 0 && (int64_t)kb * PF_BS + PF_BS <= p.T) {  // a whole block: plain loads
+      const uint16_t *kp = kbh + (int64_t)kb * PF_BS * p.k_st + koff;
+      const uint16_t *vp = vbh + (int64_t)kb * PF_BS * p.v_st + voff;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        r.k[i] = *(const uint4 *)(kp + i * kstep);
+        r.v[i] = *(const uint4 *)(vp + i * vstep);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ch = tid + i * PF_NT;  // K chunk: key ch/16, 8 dims at (ch%16)*8
-      const int64_t key = (int64_t)kb * PF_BS + (ch >> 4);
+      const int64_t key = (int64_t)kb * PF_BS + (tid >> 4) + 16 * i;
       const bool kok = kb >= 0 && key < p.T;  // -1 list entries read nothing
-      r.k[i] = kok ? *(const uint4 *)(kbh + key * p.k_st + (ch & 15) * 8) : uint4{0, 0, 0, 0};
-      r.v[i] = kok ? *(const uint4 *)(vbh + key * p.v_st + (ch & 15) * 8) : uint4{0, 0, 0, 0};
+      r.k[i] = kok ? *(const uint4 *)(kbh + key * p.k_st + (tid & 15) * 8) : uint4{0, 0, 0, 0};
+      r.v[i] = kok ? *(const uint4 *)(vbh + key * p.v_st + (tid & 15) * 8) : uint4{0, 0, 0, 0};
     }
   };
   auto lstore = [&](int buf, const Stage &r) {
@@ -193,16 +206,17 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) l[qg] += pv[e];
+      // packed words: hw = bf16x2(P) (round to nearest), its exact fp32
+      // value from the halves, lw = bf16x2(P - hi)
+      uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const bf16x2 h2 = __builtin_convertvector((f32x2{pv[e], pv[e + 1]}), bf16x2);
-        const f32x2 hf = __builtin_convertvector(h2, f32x2);
-        const bf16x2 l2 = __builtin_convertvector((f32x2{pv[e] - hf[0], pv[e + 1] - hf[1]}), bf16x2);
-        ph[qg][e] = h2[0];
-        ph[qg][e + 1] = h2[1];
-        pl[qg][e] = l2[0];
-        pl[qg][e + 1] = l2[1];
+      for (int e = 0; e < 4; ++e) {
+        hw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{pv[2 * e], pv[2 * e + 1]}), bf16x2));
+        const float h0 = __uint_as_float(hw[e] << 16), h1 = __uint_as_float(hw[e] & 0xffff0000u);
+        lw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{pv[2 * e] - h0, pv[2 * e + 1] - h1}), bf16x2));
       }
+      ph[qg] = __builtin_bit_cast(bf16x8, uint4{hw[0], hw[1], hw[2], hw[3]});
+      pl[qg] = __builtin_bit_cast(bf16x8, uint4{lw[0], lw[1], lw[2], lw[3]});
     }
     // O^T += V^T P^T over this wave's keys; each V^T operand serves both groups
 #pragma unroll
