@@ -127,7 +127,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     }
   };
 
-  // m: running max of the raw (unscaled) scores of this lane's query, per group
+  // m: reference maximum of the raw (unscaled) scores of this lane's query, per group
   float m[2] = {__int_as_float(0xff800000), __int_as_float(0xff800000)}, l[2] = {0.f, 0.f};
   f32x4 acc[2][8];
 #pragma unroll
@@ -184,9 +184,12 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
                        fmaxf(fmaxf(st[qg][1][0], st[qg][1][1]), fmaxf(st[qg][1][2], st[qg][1][3])));
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // m is a reference maximum: it is raised (and acc, l rescaled) only when
+      // a row's maximum exceeds it by more than 2^8 in the exponent, so the
+      // weights stay below 256 and the rescale is rare; the final division
+      // by l is unchanged by the choice of reference.
       const float mn = fmaxf(m[qg], mx);
-      // rescale only when some lane's maximum grew (rare after the first blocks)
-      if (__ballot(mn > m[qg]) != 0) {
+      if (__ballot((mn - m[qg]) * p.qscale > 8.f) != 0) {
         const float alpha = mn > m[qg] ? fast_exp2((m[qg] - mn) * p.qscale) : 1.f;
         l[qg] *= alpha;
 #pragma unroll

@@ -538,9 +538,12 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
     for (int e = 0; e < 4; ++e) {
       sv[e] = cur_ok ? sacc[e] * p.qscale : __int_as_float(0xff800000);
       mn[e] = fmaxf(ms[e], row_max16(sv[e]));
-      grow = grow || (slot < NRG && mn[e] > ms[e]);
+      grow = grow || (slot < NRG && mn[e] - ms[e] > 8.f);
     }
-    // the G heads' maxima are wave-uniform (DPP row 0: heads 0-3, row 1: 4-7)
+    // the G heads' reference maxima are wave-uniform (DPP row 0: heads 0-3,
+    // row 1: 4-7); a reference is raised (acc, l rescaled) only when a round
+    // maximum exceeds it by more than 8 in the log2 domain, so the weights
+    // stay below 256 and most rounds skip the rescale
     if (__ballot(grow) != 0) {
       float al[4];
 #pragma unroll
