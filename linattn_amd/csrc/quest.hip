@@ -159,6 +159,7 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
     const V *pl = (const V *)((const char *)mn + (mbase + p0) * (MT == LA_BF16 ? 2 : 4));
     const V *ph = (const V *)((const char *)mx + (mbase + p0) * (MT == LA_BF16 ? 2 : 4));
     const int64_t sd = m_sd / PPT;  // vectors per d step
+    const int Dn = (int)D;
     auto widen = [](const V &v, double (&x)[PPT]) {
       if constexpr (MT == LA_BF16) {
         x[0] = bf16lo(v.x); x[1] = bf16hi(v.x); x[2] = bf16lo(v.y); x[3] = bf16hi(v.y);
@@ -167,18 +168,21 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
       }
     };
     V a[2][QD], c[2][QD];
-    auto fetch = [&](int64_t d0, int buf) {
+    // loads are unconditional (channels past D re-read channel D-1 and are
+    // not consumed): a conditional load block would make the compiler wait
+    // for every outstanding load before each consume
+    auto fetch = [&](int d0, int buf) {
 #pragma unroll
       for (int j = 0; j < QD; ++j) {
-        const bool ok = d0 + j < D;
-        a[buf][j] = ok ? pl[(d0 + j) * sd] : V{};
-        c[buf][j] = ok ? ph[(d0 + j) * sd] : V{};
+        const int64_t d = min(d0 + j, Dn - 1);
+        a[buf][j] = pl[d * sd];
+        c[buf][j] = ph[d * sd];
       }
     };
-    auto consume = [&](int64_t d0, int buf) {
+    auto consume = [&](int d0, int buf) {
 #pragma unroll
       for (int j = 0; j < QD; ++j) {
-        if (d0 + j >= D) break;
+        if (d0 + j >= Dn) break;
         double lo[PPT], hi[PPT];
         widen(a[buf][j], lo);
         widen(c[buf][j], hi);
@@ -186,11 +190,10 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
       }
     };
     fetch(0, 0);
-    for (int64_t d0 = 0; d0 < D; d0 += 2 * QD) {
-      if (d0 + QD < D) fetch(d0 + QD, 1);
+    for (int d0 = 0; d0 < Dn; d0 += 2 * QD) {
+      fetch(d0 + QD, 1);
       consume(d0, 0);
-      if (d0 + QD >= D) break;
-      if (d0 + 2 * QD < D) fetch(d0 + 2 * QD, 0);
+      fetch(d0 + 2 * QD, 0);
       consume(d0 + QD, 1);
     }
   } else {
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
   constexpr int PPT = 4, QD = 8;
   extern __shared__ __align__(16) uint64_t keys[];  // [G][NP]
   __shared__ double qd[G * 256];
-  __shared__ TkRegShared<KPT> sr;
+  __shared__ uint32_t wtmp[TK_NW];
   __shared__ uint32_t bm[NP / 32];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;  // (b, kvh, t)
@@ -258,7 +261,8 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
   using V = typename std::conditional<MT == LA_BF16, uint2, float4>::type;
   constexpr int ESZ = MT == LA_BF16 ? 2 : 4;
   const int64_t mbase = b * a.m_sb + kvh * a.m_sh;
-  const int64_t sd = a.m_sd / PPT;  // vectors per d step
+  const int Dn = (int)D;
+  const int sd = (int)(a.m_sd / PPT);  // vectors per d step
   for (int c = 0; c < KPT / 4; ++c) {
     const int p0 = c * TK_NT * PPT + tid * PPT;
     double acc[G][PPT];
@@ -270,12 +274,13 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
       const V *pl = (const V *)((const char *)a.mn + (mbase + p0) * ESZ);
       const V *ph = (const V *)((const char *)a.mx + (mbase + p0) * ESZ);
       V lo_v[2][QD], hi_v[2][QD];
-      auto fetch = [&](int64_t d0, int buf) {
+      // channels past D re-read channel D-1 (in bounds) and are not consumed
+      auto fetch = [&](int d0, int buf) {
 #pragma unroll
         for (int j = 0; j < QD; ++j) {
-          const bool ok = d0 + j < D;
-          lo_v[buf][j] = ok ? pl[(d0 + j) * sd] : V{};
-          hi_v[buf][j] = ok ? ph[(d0 + j) * sd] : V{};
+          const int d = min(d0 + j, Dn - 1);
+          lo_v[buf][j] = pl[d * sd];
+          hi_v[buf][j] = ph[d * sd];
         }
       };
       auto widen = [](const V &v, double (&x)[PPT]) {
@@ -285,28 +290,29 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
           x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
         }
       };
-      auto consume = [&](int64_t d0, int buf) {
+      auto consume = [&](int d0, int buf) {
 #pragma unroll
         for (int j = 0; j < QD; ++j) {
-          if (d0 + j >= D) break;
+          if (d0 + j >= Dn) break;
           double lo[PPT], hi[PPT];
           widen(lo_v[buf][j], lo);
           widen(hi_v[buf][j], hi);
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-            const double qv = qd[g * D + d0 + j];
-            const bool pos_q = qv >= 0.0;
+            const double qv = qd[g * Dn + d0 + j];
+            const bool neg = qv < 0.0;
 #pragma unroll
-            for (int i = 0; i < PPT; ++i) acc[g][i] = __builtin_fma(qv, pos_q ? hi[i] : lo[i], acc[g][i]);
+            for (int i = 0; i < PPT; ++i) acc[g][i] = __builtin_fma(qv, neg ? lo[i] : hi[i], acc[g][i]);
           }
         }
       };
+      // fetches are unconditional (a conditional load block would make the
+      // compiler wait for every outstanding load before each consume)
       fetch(0, 0);
-      for (int64_t d0 = 0; d0 < D; d0 += 2 * QD) {
-        if (d0 + QD < D) fetch(d0 + QD, 1);
+      for (int d0 = 0; d0 < Dn; d0 += 2 * QD) {
+        fetch(d0 + QD, 1);
         consume(d0, 0);
-        if (d0 + QD >= D) break;
-        if (d0 + 2 * QD < D) fetch(d0 + 2 * QD, 0);
+        fetch(d0 + 2 * QD, 0);
         consume(d0 + QD, 1);
       }
     }
@@ -327,13 +333,13 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
     uint64_t u[KPL];
 #pragma unroll
     for (int j = 0; j < KPL; ++j) u[j] = keys[g * NP + lane + 64 * j];
-    tk_wave_select<KPL>(u, n_v, K, sr.hist[w], [&](int j, int32_t i, bool take) {
+    tk_wave_select_bits<KPL>(u, n_v, K, [&](int j, int32_t i, bool take) {
       if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
     });
   }
   __syncthreads();
   tk_emit_bitmap_row(bm, n_v, own, 0, 0, a.width, a.out_idx + row * a.width,
-                     a.out_count ? a.out_count + row : nullptr, sr.wtmp[1]);
+                     a.out_count ? a.out_count + row : nullptr, wtmp);
 }
 
 template <int MT, int G>

@@ -630,13 +630,12 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
 // Short rows in the bitmap form (unions, sink, window): one wave per output
 // row, four rows per workgroup, no workgroup barrier.  The wave holds the
 // keys of units lane + 64*j (j < KPL, rows of at most 64*KPL units), selects
-// each source row with tk_wave_select, ORs the ballots of kept units into its
+// each source row with tk_wave_select_bits, ORs the ballots of kept units into its
 // own bitmap words, adds sink and window, and writes the kept units in
 // ascending order.
 template <int KPL>
 __global__ __launch_bounds__(TK_NT) void topk_wave_kernel(TopkKParams p) {
   constexpr int WORDS = 2 * KPL;  // 32-bit bitmap words per row
-  __shared__ uint32_t hist[TK_NW][256];
   __shared__ uint32_t bms[TK_NW][WORDS];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t gi = (int64_t)blockIdx.x * TK_NW + w;
@@ -661,7 +660,7 @@ __global__ __launch_bounds__(TK_NT) void topk_wave_kernel(TopkKParams p) {
       x = (x >> 63) ? ~x : (x | 0x8000000000000000ull);
       u[j] = (rw.force && i == own) ? KEY_FORCED : x;
     }
-    tk_wave_select<KPL>(u, n_v, K, hist[w], [&](int j, int32_t i, bool take) {
+    tk_wave_select_bits<KPL>(u, n_v, K, [&](int j, int32_t i, bool take) {
       const uint64_t b = __ballot(take);
       if (lane == 0) {
         bm[2 * j] |= (uint32_t)b;

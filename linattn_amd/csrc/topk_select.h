@@ -161,101 +161,60 @@ __device__ __forceinline__ void tk_reg_select(const uint64_t (&u)[KPT], int32_t 
 }
 
 // One wave's top K of the keys u[j] of units lane + 64*j, j < KPL, among the
-// first n_v units: the same selection as tk_reg_select (common leading bits
-// skipped, 8-bit digits, ties to the lowest index) with no workgroup barrier,
-// so the waves of a workgroup can select different rows at once.  hist is
-// this wave's 256-bin LDS histogram.  emit(j, i, take) is called by every
-// lane for every slot j in increasing j.
+// first n_v units, by a bitwise search for the K-th largest key: T keeps the
+// bits found so far and each step counts the keys >= T | bit with one vector
+// compare per slot (the compare writes the wave's lane mask, counted on the
+// scalar unit).  It stops as soon as exactly K keys reach the candidate; else
+// T ends as the K-th largest key and its ties go to the lowest index.  No
+// LDS and no barrier.  Same selection as tk_reg_select.  emit(j, i, take) is
+// called by every lane for every slot j in increasing j.
 template <int KPL, class Emit>
-__device__ __forceinline__ void tk_wave_select(const uint64_t (&u)[KPL], int32_t n_v, uint32_t K,
-                                               uint32_t *hist, Emit emit) {
+__device__ __forceinline__ void tk_wave_select_bits(const uint64_t (&u_in)[KPL], int32_t n_v,
+                                                    uint32_t K, Emit emit) {
   const int lane = threadIdx.x & 63;
-  const uint64_t lt = lanemask_lt(lane);
-  uint64_t prefix = 0, mask = 0;
-  uint32_t need = K;
-  bool all_in = (int32_t)K >= n_v;
-  if (!all_in) {
-    uint64_t o = 0, a = ~0ull;
+  uint64_t u[KPL];  // units past n_v count as key 0, which no candidate reaches
 #pragma unroll
-    for (int j = 0; j < KPL; ++j) {
-      if (lane + 64 * j < n_v) {
-        o |= u[j];
-        a &= u[j];
-      }
-    }
+  for (int j = 0; j < KPL; ++j) u[j] = lane + 64 * j < n_v ? u_in[j] : 0ull;
+  if ((int32_t)K >= n_v) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      o |= __shfl_xor(o, off, 64);
-      a &= __shfl_xor(a, off, 64);
-    }
-    const uint64_t diff = o ^ a;
-    int top = diff ? 63 - __clzll((long long)diff) : -1;
-    mask = top >= 0 ? ~((2ull << top) - 1ull) : ~0ull;
-    prefix = a & mask;
-    while (top >= 0) {
-      const int shift = top >= 7 ? top - 7 : 0;
-      const uint32_t dm = (2u << (top - shift)) - 1u;
+    for (int j = 0; j < KPL; ++j) emit(j, lane + 64 * j, lane + 64 * j < n_v);
+    return;
+  }
+  uint64_t T = 0;  // count(u >= T) >= K throughout
+  bool exact = false;
+  for (int bit = 63; bit >= 0; --bit) {
+    const uint64_t T2 = T | (1ull << bit);
+    uint32_t c = 0;
 #pragma unroll
-      for (int x = 0; x < 4; ++x) hist[lane * 4 + x] = 0u;
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int j = 0; j < KPL; ++j) {
-        if (lane + 64 * j < n_v && (u[j] & mask) == prefix)
-          atomicAdd(&hist[(uint32_t)(u[j] >> shift) & dm], 1u);
-      }
-      __builtin_amdgcn_wave_barrier();
-      // lane l holds bins 255-4l-x (x = 0..3), i.e. descending bin order
-      uint32_t c[4], c4 = 0;
-#pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        c[x] = hist[255 - 4 * lane - x];
-        c4 += c[x];
-      }
-      uint32_t incl = c4;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += y;
-      }
-      const uint64_t hit = __ballot(incl >= need && incl - c4 < need);
-      const int src = __ffsll((unsigned long long)hit) - 1;
-      uint32_t above = __shfl(incl - c4, src, 64);
-      uint32_t bin = 0, cnt = 0;
-#pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        const uint32_t cx = __shfl(c[x], src, 64);
-        if (cnt == 0 && above + cx >= need) {
-          bin = 255 - 4 * src - x;
-          cnt = cx;
-        } else if (cnt == 0) {
-          above += cx;
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
-      need -= above;
-      prefix |= (uint64_t)bin << shift;
-      mask |= (uint64_t)dm << shift;
-      if (cnt == need) {
-        all_in = true;
+    for (int j = 0; j < KPL; ++j) c += (uint32_t)__popcll(__ballot(u[j] >= T2));
+    if (c >= K) {
+      T = T2;
+      if (c == K) {
+        exact = true;
         break;
       }
-      top = shift - 1;
     }
   }
+  if (exact) {
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) emit(j, lane + 64 * j, lane + 64 * j < n_v && u[j] >= T);
+    return;
+  }
+  // T is the K-th largest key: every key above it, then its ties by index
+  uint32_t gt = 0;
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) gt += (uint32_t)__popcll(__ballot(u[j] > T));
+  const uint32_t need = K - gt;
+  const uint64_t lt = lanemask_lt(lane);
   uint32_t eq_before = 0;
 #pragma unroll
   for (int j = 0; j < KPL; ++j) {
     const int32_t i = lane + 64 * j;
     const bool valid = i < n_v;
-    const uint64_t um = u[j] & mask;
-    const bool gt = valid && um > prefix;
-    const bool eq = valid && um == prefix;
-    bool take = gt || (eq && all_in);
-    if (!all_in) {
-      const uint64_t b = __ballot(eq);
-      take = gt || (eq && eq_before + (uint32_t)__popcll(b & lt) < need);
-      eq_before += (uint32_t)__popcll(b);
-    }
+    const bool eq = valid && u[j] == T;
+    const uint64_t b = __ballot(eq);
+    const bool take = (valid && u[j] > T) || (eq && eq_before + (uint32_t)__popcll(b & lt) < need);
+    eq_before += (uint32_t)__popcll(b);
     emit(j, i, take);
   }
 }
