@@ -15,6 +15,8 @@ namespace la {
 // ---------------------------------------------------------------- errors ----
 void set_error(const char *fmt, ...);
 int fail(int code, const char *fmt, ...);
+// compute units of the current device (cached per thread and device)
+int num_cus();
 
 #define LA_REQUIRE(cond, ...)                               \
   do {                                                      \
@@ -42,6 +44,35 @@ inline int ilog2(int64_t x) {
   int r = 0;
   while ((int64_t(1) << r) < x) ++r;
   return r;
+}
+
+// ----------------------------------------------------- LDS and barriers ----
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16 bytes per lane from global memory straight into LDS (gfx950
+// global_load_lds_dwordx4): lane i writes dst + 16 i, dst wave-uniform (M0).
+// Issued as inline assembly so that the compiler neither waits for it (it
+// treated the address registers as pending results) nor reorders it across
+// the barriers; it counts in vmcnt, and the caller waits (wait_vmcnt) and
+// synchronises the workgroup before reading the data.
+__device__ __forceinline__ void dma16(const void *src, void *dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t *)dst);
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+// Wait until at most N vector memory operations of this wave are
+// outstanding (N < 64; the other counters are not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier for LDS traffic only: this wave's LDS operations are
+// complete, then s_barrier.  Unlike __syncthreads it does not wait for global
+// memory operations (so loads issued earlier stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // --------------------------------------------------------- element loads ----

@@ -22,6 +22,20 @@ int fail(int code, const char *fmt, ...) {
   return code;
 }
 
+int num_cus() {
+  static thread_local int cached_dev = -1, cached = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev != cached_dev) {
+    int v = 0;
+    cached = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+                 ? v
+                 : 256;
+    cached_dev = dev;
+  }
+  return cached;
+}
+
 }  // namespace la
 
 extern "C" int la_abi_version(void) { return LA_ABI_VERSION; }

@@ -186,92 +186,207 @@ __global__ __launch_bounds__(256) void indexer_decode_kernel(IdxKP p) {
 }
 
 // Few queries over a long key axis with 2-byte keys whose (head, dim) block
-// is contiguous and 16-byte aligned (the decode shape of config C5).  64 keys
-// per workgroup, HI threads per key: the key rows are staged with coalesced
-// 16-byte loads (all in flight at once) into LDS rows padded to 528 bytes;
-// thread (key, head) computes that head's dot for every query of the chunk,
-// d in order, and thread (query, key) then adds the heads in order.
-constexpr int IDF_KEYS = 64, IDF_ROWB = 528;
+// is contiguous and 16-byte aligned (the decode shape of config C5).  Every
+// wave works on its own: a wave tile is 64/HI keys, lane (key, head) owns
+// that key's head segment of d values.  The tile is loaded with coalesced
+// 16-byte loads (lane l takes chunk l of each 1 KiB step), two tiles ahead
+// for HI >= 4 (one otherwise), written to the wave's LDS rows (head segments
+// of 2d + 16 bytes, which puts the 64 lanes' segments on different banks)
+// and read back per lane.  Lane (key, head) computes that head's dot for
+// every query of the chunk, d in order; the head lanes of a key are adjacent,
+// and the first adds the heads in order and writes the score.  No workgroup
+// barrier inside the loop.  The loads are issued as inline assembly and
+// waited for explicitly (the compiler's waits at the loop head were for
+// every outstanding load).
+constexpr int IDF_KEYS = 64;  // keys per workgroup step (one wave tile per wave)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float half_bits_to_f32(uint32_t bits16, int dt) {
-  return dt == LA_BF16 ? bf16_bits_to_f32(bits16) : __half2float(__ushort_as_half((uint16_t)bits16));
+__device__ __forceinline__ u32x4 load16_async(const void *ptr) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr));
+  return v;
 }
 
+// Wait until at most N loads are outstanding; the chunks are operands so
+// that no use of them is moved above the wait.
+template <int N, int CH>
+__device__ __forceinline__ void wait_chunks(u32x4 (&v)[CH]) {
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    if (i == 0)
+      asm volatile("s_waitcnt vmcnt(%1)" : "+v"(v[i]) : "n"(N));
+    else
+      asm volatile("" : "+v"(v[i]));
+  }
+}
+
+static size_t decode16_lds(int64_t tn, int64_t HI, int64_t d) {
+  return (size_t)(4 * 64 * (2 * d + 16) + tn * HI * d * 8 + tn * HI * 8);
+}
+
+// waves per SIMD the registers are sized for (two tiles of 16-byte chunks in
+// flight for HI >= 4; HI < 4 lanes hold more chunks per tile)
 template <int HI>
-__global__ __launch_bounds__(IDF_KEYS * HI) void indexer_decode16_kernel(IdxKP p) {
-  constexpr int NT = IDF_KEYS * HI;
-  constexpr int CPT = (IDF_KEYS * ID_MAXHD / 8 + NT - 1) / NT;  // 16-byte chunks per thread (max)
-  __shared__ __align__(16) unsigned char sk[IDF_KEYS * IDF_ROWB];
-  __shared__ double sqd[ID_MAXQ][ID_MAXHD];
-  __shared__ double sdot[ID_MAXQ][IDF_KEYS][HI];
-  const int tid = threadIdx.x;
+constexpr int idf_waves_per_eu() { return HI >= 4 ? 3 : HI == 2 ? 2 : 1; }
+
+// TN1: the chunk has one query (the decode step), so one dot per lane; BF:
+// bf16 keys (else fp16)
+template <int HI, bool TN1, bool BF>
+__global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_kernel(IdxKP p, int tiles) {
+  constexpr int NQ = TN1 ? 1 : ID_MAXQ;
+  constexpr int KW = 64 / HI;            // keys per wave tile
+  constexpr int CH = ID_MAXHD / 8 / HI;  // 16-byte chunks per lane (most)
+  constexpr bool TWO = HI >= 4;          // two tiles in flight
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t b = blockIdx.y;
-  const int64_t k0 = (int64_t)blockIdx.x * IDF_KEYS;
   const int d = (int)p.d;
   const int hd = HI * d;
-  const int cpr = hd / 8;  // 16-byte chunks per key row
+  const int ch = d / 8;       // chunks per lane in use (<= CH)
+  const int cpr = hd / 8;     // chunks per key row
+  const int hs = 2 * d + 16;  // LDS head segment
+  const int tn = (int)p.tn;
+  unsigned char *rows = smem + w * 64 * hs;              // this wave's KW rows of HI segments
+  double *sqd = (double *)(smem + 4 * 64 * hs);          // [tn][hd]
+  double *sw = sqd + tn * hd;                            // head weights [tn][HI]
   const uint16_t *kb = (const uint16_t *)p.k + b * p.k_sb;
-  {
-    uint4 v[CPT];
-#pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-      const int c = tid + u * NT;
-      const int r = c / cpr, col = c % cpr;
-      const int64_t s = k0 + r;
-      v[u] = (r < IDF_KEYS && s < p.Tk) ? *(const uint4 *)(kb + s * p.k_st + col * 8) : uint4{0, 0, 0, 0};
-    }
-    for (int i = tid; i < p.tn * hd; i += NT) {
-      const int tl = i / hd, c = i % hd;
-      const int h = c / d, dd = c % d;
-      sqd[tl][c] = load_as_f64(p.q, b * p.q_sb + (p.t0 + tl) * p.q_st + h * p.q_sh + dd, p.dt);
-    }
-#pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-      const int c = tid + u * NT;
-      if (c < IDF_KEYS * cpr) *(uint4 *)(sk + (c / cpr) * IDF_ROWB + (c % cpr) * 16) = v[u];
-    }
+  // wave tiles of this workgroup: [wt0, wt0 + 4 * tiles * HI / ... ) interleaved over waves
+  const int64_t n_wt = (p.Tk + KW - 1) / KW;
+  const int64_t wt0 = (int64_t)blockIdx.x * tiles * HI;  // `tiles` 64-key steps = tiles*HI wave tiles
+  const int64_t wt_end = min(n_wt, wt0 + (int64_t)tiles * HI);
+  const int nw = wt0 + w < wt_end ? (int)((wt_end - wt0 - w + 3) / 4) : 0;  // this wave's tiles
+  for (int i = tid; i < tn * hd; i += 256) {
+    const int tl = i / hd, c = i % hd;
+    const int h = c / d, dd = c % d;
+    sqd[tl * hd + c] = load_as_f64(p.q, b * p.q_sb + (p.t0 + tl) * p.q_st + h * p.q_sh + dd, p.dt);
   }
+  for (int i = tid; i < tn * HI; i += 256)
+    sw[i] = (double)p.w[b * p.w_sb + (p.t0 + i / HI) * p.w_st + (i % HI) * p.w_sh];
   __syncthreads();
-  {
-    const int h = tid % HI, r = tid / HI;
-    const unsigned char *row = sk + r * IDF_ROWB + h * d * 2;
-    double dot[ID_MAXQ] = {0.0, 0.0, 0.0, 0.0};
+  if (nw == 0) return;  // whole wave; no barrier follows
+  // chunk i of lane l in the coalesced load of a wave tile: c = i*64 + l of
+  // the tile's KW x cpr chunks (past the end: the tile's last chunk again)
+  auto fetch = [&](u32x4 (&v)[CH], int k) {  // k-th tile of this wave (clamped)
+    const int64_t key0 = (wt0 + w + 4 * (int64_t)min(k, nw - 1)) * KW;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = min(i * 64 + lane, KW * cpr - 1);
+      const int64_t s = min(key0 + c / cpr, p.Tk - 1);
+      v[i] = load16_async(kb + s * p.k_st + (c % cpr) * 8);
+    }
+  };
+  auto stage = [&](const u32x4 (&v)[CH]) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = i * 64 + lane;
+      if (i < ch) {
+        const int r = c / cpr, col = c % cpr;
+        *(u32x4 *)(rows + r * HI * hs + (col / ch) * hs + (col % ch) * 16) = v[i];
+      }
+    }
+  };
+  auto compute = [&](int k) {
+    const int64_t key0 = (wt0 + w + 4 * (int64_t)k) * KW;
+    const int kr = lane / HI, h = lane % HI;
+    const unsigned char *seg = rows + kr * HI * hs + h * hs;
+    double dot[NQ];
+#pragma unroll
+    for (int tl = 0; tl < NQ; ++tl) dot[tl] = 0.0;
     for (int dd = 0; dd < d; dd += 8) {
-      const uint4 kv = *(const uint4 *)(row + dd * 2);
-      const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+      const u32x4 kv = *(const u32x4 *)(seg + dd * 2);
       double kf[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        kf[2 * e] = (double)half_bits_to_f32(w4[e] & 0xffffu, p.dt);
-        kf[2 * e + 1] = (double)half_bits_to_f32(w4[e] >> 16, p.dt);
+        if constexpr (BF) {
+          kf[2 * e] = (double)bf16lo(kv[e]);
+          kf[2 * e + 1] = (double)bf16hi(kv[e]);
+        } else {
+          kf[2 * e] = (double)__half2float(__ushort_as_half((uint16_t)(kv[e] & 0xffffu)));
+          kf[2 * e + 1] = (double)__half2float(__ushort_as_half((uint16_t)(kv[e] >> 16)));
+        }
       }
 #pragma unroll
-      for (int tl = 0; tl < ID_MAXQ; ++tl) {
-        if (tl >= p.tn) break;
-        const double *qv = &sqd[tl][h * d + dd];
+      for (int tl = 0; tl < NQ; ++tl) {
+        if (tl >= tn) break;
+        const double *qv = &sqd[tl * hd + h * d + dd];
 #pragma unroll
         for (int e = 0; e < 8; ++e) dot[tl] = __builtin_fma(qv[e], kf[e], dot[tl]);
       }
     }
+    // heads of a key are lanes kr*HI + 0..HI-1: the first adds them in order
+    const int64_t s = key0 + kr;
 #pragma unroll
-    for (int tl = 0; tl < ID_MAXQ; ++tl)
-      if (tl < p.tn) sdot[tl][r][h] = dot[tl];
-  }
-  __syncthreads();
-  for (int i = tid; i < IDF_KEYS * p.tn; i += NT) {
-    const int r = i % IDF_KEYS, tl = i / IDF_KEYS;
-    const int64_t s = k0 + r;
-    if (s >= p.Tk) continue;
-    const int64_t t = p.t0 + tl;
-    double acc = 0.0;
+    for (int tl = 0; tl < NQ; ++tl) {
+      if (tl >= tn) break;
+      double acc = 0.0;
 #pragma unroll
-    for (int h = 0; h < HI; ++h) {
-      const double dv = sdot[tl][r][h];
-      const double rl = dv > 0.0 ? dv : 0.0;
-      acc = add_product(acc, (double)p.w[b * p.w_sb + t * p.w_st + h * p.w_sh], rl);
+      for (int hh = 0; hh < HI; ++hh) {
+        const double dv = __shfl(dot[tl], kr * HI + hh, 64);
+        const double rl = dv > 0.0 ? dv : 0.0;
+        acc = add_product(acc, sw[tl * HI + hh], rl);
+      }
+      if (h == 0 && s < p.Tk) p.scores[(b * p.tn + tl) * p.Tk + s] = acc;
     }
-    p.scores[(b * p.tn + tl) * p.Tk + s] = acc;
+  };
+  u32x4 va[CH];
+  if constexpr (TWO) {
+    u32x4 vb[CH];
+    fetch(va, 0);
+    fetch(vb, 1);
+    for (int k = 0; k < nw; k += 2) {
+      wait_chunks<CH, CH>(va);  // vb's loads (and at most a store) may still be in flight
+      stage(va);
+      fetch(va, k + 2);
+      compute(k);
+      if (k + 1 >= nw) break;
+      wait_chunks<CH, CH>(vb);
+      stage(vb);
+      fetch(vb, k + 3);
+      compute(k + 1);
+    }
+  } else {
+    fetch(va, 0);
+    for (int k = 0; k < nw; ++k) {
+      wait_chunks<0, CH>(va);
+      stage(va);
+      fetch(va, k + 1);
+      compute(k);
+    }
   }
+  wait_vmcnt<0>();  // drain the last (repeated) loads before the wave ends
+}
+
+template <int HI, bool TN1, bool BF>
+static int launch_decode16(const IdxKP &p, size_t lds, dim3 grid, int tiles, hipStream_t st) {
+  if (lds > 65536) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      LA_HIP(hipFuncSetAttribute((const void *)indexer_decode16_kernel<HI, TN1, BF>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      attr_set = true;
+    }
+  }
+  indexer_decode16_kernel<HI, TN1, BF><<<grid, 256, lds, st>>>(p, tiles);
+  LA_LAUNCHED();
+  return LA_OK;
+}
+
+template <int HI>
+static int dispatch_decode16(const IdxKP &p, hipStream_t st) {
+  const size_t lds = decode16_lds(p.tn, HI, p.d);
+  // a few workgroups per CU (by LDS, at most 4), each walking consecutive
+  // 64-key steps of one batch row
+  const int64_t per_cu = std::max<int64_t>(
+      1, std::min<int64_t>(idf_waves_per_eu<HI>(), (int64_t)(160 * 1024) / (int64_t)lds));
+  const int64_t n_tiles = ceil_div(p.Tk, IDF_KEYS);
+  const int64_t want = std::max<int64_t>(1, (int64_t)num_cus() * per_cu / p.B);
+  const int tiles = (int)std::max<int64_t>(1, ceil_div(n_tiles, want));
+  const dim3 grid((unsigned)ceil_div(n_tiles, tiles), (unsigned)p.B);
+  if (p.dt == LA_BF16)
+    return p.tn == 1 ? launch_decode16<HI, true, true>(p, lds, grid, tiles, st)
+                     : launch_decode16<HI, false, true>(p, lds, grid, tiles, st);
+  return p.tn == 1 ? launch_decode16<HI, true, false>(p, lds, grid, tiles, st)
+                   : launch_decode16<HI, false, false>(p, lds, grid, tiles, st);
 }
 
 static int64_t pick_chunk(const la_indexer_args *a) {
@@ -366,13 +481,14 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     p.causal = a->causal;
     p.unit = std::max<int64_t>(1, a->causal_unit);
     if (decode16) {
-      const dim3 grid((unsigned)ceil_div(a->Tk, IDF_KEYS), (unsigned)a->B);
+      int rc;
       switch (a->HI) {
-        case 1: indexer_decode16_kernel<1><<<grid, IDF_KEYS * 1, 0, st>>>(p); break;
-        case 2: indexer_decode16_kernel<2><<<grid, IDF_KEYS * 2, 0, st>>>(p); break;
-        case 4: indexer_decode16_kernel<4><<<grid, IDF_KEYS * 4, 0, st>>>(p); break;
-        default: indexer_decode16_kernel<8><<<grid, IDF_KEYS * 8, 0, st>>>(p); break;
+        case 1: rc = dispatch_decode16<1>(p, st); break;
+        case 2: rc = dispatch_decode16<2>(p, st); break;
+        case 4: rc = dispatch_decode16<4>(p, st); break;
+        default: rc = dispatch_decode16<8>(p, st); break;
       }
+      if (rc != LA_OK) return rc;
     } else if (decode) {
       indexer_decode_kernel<<<dim3((unsigned)ceil_div(a->Tk, ID_KEYS), (unsigned)a->B), 256, 0,
                               st>>>(p);

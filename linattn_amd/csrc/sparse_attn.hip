@@ -699,19 +699,6 @@ static int dispatch_d(const AttnKP &p, int64_t D, int64_t G, hipStream_t st) {
   }
 }
 
-static int num_cus() {
-  static int cached = 0;
-  if (cached <= 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cached = v;
-    else
-      cached = 256;
-  }
-  return cached;
-}
-
 struct Plan {
   int64_t G, R, splits, eps;
   size_t ws;
