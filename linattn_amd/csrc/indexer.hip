@@ -129,6 +129,160 @@ __global__ __launch_bounds__(IT_NT) void indexer_tile_kernel(IdxKP p) {
   }
 }
 
+// Tiled scores for 2-byte q/k whose (head, d) rows are 16-byte aligned, the
+// shape of config C2.  Same 64-query x 128-key tile and fp64 arithmetic as
+// indexer_tile_kernel, restaged for throughput:
+//  - a (head, 64-d) slice is loaded with coalesced 16-byte loads (8 lanes per
+//    row), the next slice's loads in flight while the current one is
+//    computed; q goes to LDS as fp64 and k as fp32, both row-major;
+//  - thread (tq, tk) owns queries 8 tq .. 8 tq + 7 and keys tk + 32 c
+//    (c < 4): each k read of a wave covers 32 consecutive rows (no bank
+//    conflicts), the q reads are broadcasts, and only k is converted in the
+//    inner loop (each k value feeds 8 FMAs);
+//  - the head weights of the tile's queries are staged once.
+constexpr int IT16_D = 64;  // d slice
+constexpr int IT16_QS = IT16_D + 2, IT16_KS = IT16_D + 4;  // LDS row strides (fp64, fp32)
+
+template <bool BF>
+__device__ __forceinline__ void widen8(const uint4 &v, float (&x)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (BF) {
+      x[2 * e] = bf16lo(w[e]);
+      x[2 * e + 1] = bf16hi(w[e]);
+    } else {
+      x[2 * e] = __half2float(__ushort_as_half((uint16_t)(w[e] & 0xffffu)));
+      x[2 * e + 1] = __half2float(__ushort_as_half((uint16_t)(w[e] >> 16)));
+    }
+  }
+}
+
+template <bool BF>
+__global__ __launch_bounds__(IT_NT, 2) void indexer_tile16_kernel(IdxKP p) {
+  __shared__ __align__(16) double sq[IT_Q][IT16_QS];
+  __shared__ __align__(16) float sk[IT_K][IT16_KS];
+  __shared__ float sw[IT_Q][8];
+  const int tid = threadIdx.x;
+  const int tq = tid >> 5, tk = tid & 31;
+  const int64_t b = blockIdx.z;
+  const int64_t q0 = (int64_t)blockIdx.y * IT_Q;  // within the chunk
+  const int64_t k0 = (int64_t)blockIdx.x * IT_K;
+  if (q0 >= p.tn) return;
+  if (p.causal) {
+    const int64_t last_q = p.offset + p.t0 + min(q0 + IT_Q, p.tn) - 1;
+    if (k0 * p.unit > last_q) return;
+  }
+  const int HI = (int)p.HI, d = (int)p.d;
+  for (int i = tid; i < IT_Q * HI; i += IT_NT) {
+    const int r = i / HI, h = i % HI;
+    const int64_t t = p.t0 + min(q0 + r, p.tn - 1);
+    sw[r][h] = p.w[b * p.w_sb + t * p.w_st + h * p.w_sh];
+  }
+  const uint16_t *qb = (const uint16_t *)p.q + b * p.q_sb;
+  const uint16_t *kb = (const uint16_t *)p.k + b * p.k_sb;
+  // slice loads: chunk c of q (c < 512) is row c/8, d-chunk c%8; k likewise
+  // (c < 1024).  Rows past the chunk / key range read a clamped row.
+  uint4 lq[2], lk[4];
+  auto fetch = [&](int h, int d0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + u * IT_NT, r = c >> 3, dc = c & 7;
+      const int64_t t = p.t0 + min(q0 + r, p.tn - 1);
+      const int dd = min(d0 + dc * 8, d - 8);
+      lq[u] = *(const uint4 *)(qb + t * p.q_st + h * p.q_sh + dd);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + u * IT_NT, r = c >> 3, dc = c & 7;
+      const int64_t s = min(k0 + r, p.Tk - 1);
+      const int dd = min(d0 + dc * 8, d - 8);
+      lk[u] = *(const uint4 *)(kb + s * p.k_st + h * p.k_sh + dd);
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + u * IT_NT, r = c >> 3, dc = c & 7;
+      float x[8];
+      widen8<BF>(lq[u], x);
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        *(double2 *)&sq[r][dc * 8 + e] = double2{(double)x[e], (double)x[e + 1]};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + u * IT_NT, r = c >> 3, dc = c & 7;
+      float x[8];
+      widen8<BF>(lk[u], x);
+      *(float4 *)&sk[r][dc * 8] = float4{x[0], x[1], x[2], x[3]};
+      *(float4 *)&sk[r][dc * 8 + 4] = float4{x[4], x[5], x[6], x[7]};
+    }
+  };
+  double score[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) score[i][c] = 0.0;
+  fetch(0, 0);
+  for (int h = 0; h < HI; ++h) {
+    double dot[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dot[i][c] = 0.0;
+    for (int d0 = 0; d0 < d; d0 += IT16_D) {
+      const int dn = min(IT16_D, d - d0);
+      __syncthreads();  // the previous slice is consumed
+      stage();
+      __syncthreads();
+      {  // next slice in flight during this one
+        const bool last_d = d0 + IT16_D >= d;
+        const int nh = last_d ? h + 1 : h, nd = last_d ? 0 : d0 + IT16_D;
+        fetch(min(nh, HI - 1), nd);
+      }
+      for (int dd = 0; dd < dn; dd += 4) {
+        float4 k4[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) k4[c] = *(const float4 *)&sk[tk + 32 * c][dd];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          double kv[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) kv[c] = (double)(e == 0 ? k4[c].x : e == 1 ? k4[c].y : e == 2 ? k4[c].z : k4[c].w);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const double qv = sq[8 * tq + i][dd + e];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) dot[i][c] = __builtin_fma(qv, kv[c], dot[i][c]);
+          }
+        }
+      }
+    }
+    // head epilogue: score += fl(w * relu(dot)), heads in increasing order
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const double wv = (double)sw[8 * tq + i][h];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const double r = dot[i][c] > 0.0 ? dot[i][c] : 0.0;
+        score[i][c] = add_product(score[i][c], wv, r);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t ql = q0 + 8 * tq + i;
+    if (ql >= p.tn) continue;
+    double *row = p.scores + (b * p.tn + ql) * p.Tk;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t s = k0 + tk + 32 * c;
+      if (s < p.Tk) row[s] = score[i][c];
+    }
+  }
+}
+
 // Few queries (decode): 32 keys per workgroup, rows staged in LDS (fp32,
 // padded); thread (key, head) computes the head's dot for every query of the
 // chunk, then thread (query, key) adds the heads in order.
@@ -460,6 +614,11 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
                         (a->HI == 1 || a->HI == 2 || a->HI == 4 || a->HI == 8) &&
                         a->k_sh == a->d && a->d % 8 == 0 && a->k_st % 8 == 0 &&
                         a->k_sb % 8 == 0 && (uintptr_t)a->kk % 16 == 0;
+  // 2-byte q and k, 16-byte aligned (head, d) rows with d a multiple of 8
+  const bool tile16 = (a->in_dtype == LA_BF16 || a->in_dtype == LA_F16) && a->d % 8 == 0 &&
+                      a->q_st % 8 == 0 && a->q_sh % 8 == 0 && a->q_sb % 8 == 0 &&
+                      a->k_st % 8 == 0 && a->k_sh % 8 == 0 && a->k_sb % 8 == 0 &&
+                      (uintptr_t)a->q % 16 == 0 && (uintptr_t)a->kk % 16 == 0;
   for (int64_t t0 = 0; t0 < a->Tq; t0 += chunk) {
     IdxKP p{};
     p.q = a->q;
@@ -493,9 +652,13 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
       indexer_decode_kernel<<<dim3((unsigned)ceil_div(a->Tk, ID_KEYS), (unsigned)a->B), 256, 0,
                               st>>>(p);
     } else {
-      indexer_tile_kernel<<<dim3((unsigned)ceil_div(a->Tk, IT_K), (unsigned)ceil_div(p.tn, IT_Q),
-                                 (unsigned)a->B),
-                            IT_NT, 0, st>>>(p);
+      const dim3 grid((unsigned)ceil_div(a->Tk, IT_K), (unsigned)ceil_div(p.tn, IT_Q), (unsigned)a->B);
+      if (tile16 && a->in_dtype == LA_BF16)
+        indexer_tile16_kernel<true><<<grid, IT_NT, 0, st>>>(p);
+      else if (tile16)
+        indexer_tile16_kernel<false><<<grid, IT_NT, 0, st>>>(p);
+      else
+        indexer_tile_kernel<<<grid, IT_NT, 0, st>>>(p);
     }
     LA_LAUNCHED();
     rc = topk_launch_ws(topk_params(a, p.scores, t0, p.tn), (char *)a->workspace + sc_bytes,
