@@ -347,9 +347,10 @@ __global__ __launch_bounds__(256) void indexer_decode_kernel(IdxKP p) {
 // for HI >= 4 (one otherwise), written to the wave's LDS rows (head segments
 // of 2d + 16 bytes, which puts the 64 lanes' segments on different banks)
 // and read back per lane.  Lane (key, head) computes that head's dot for
-// every query of the chunk, d in order; the head lanes of a key are adjacent,
-// and the first adds the heads in order and writes the score.  No workgroup
-// barrier inside the loop.  The loads are issued as inline assembly and
+// every query of the chunk, d in order (q read from LDS as fp32, exact for
+// 2-byte inputs, which halves the bytes of those reads); the head lanes of a
+// key are adjacent, and the first adds the heads in order and writes the
+// score.  No workgroup barrier inside the loop.  The loads are issued as inline assembly and
 // waited for explicitly (the compiler's waits at the loop head were for
 // every outstanding load).
 constexpr int IDF_KEYS = 64;  // keys per workgroup step (one wave tile per wave)
@@ -375,7 +376,7 @@ __device__ __forceinline__ void wait_chunks(u32x4 (&v)[CH]) {
 }
 
 static size_t decode16_lds(int64_t tn, int64_t HI, int64_t d) {
-  return (size_t)(4 * 64 * (2 * d + 16) + tn * HI * d * 8 + tn * HI * 8);
+  return (size_t)(4 * 64 * (2 * d + 16) + ((tn * HI * d + 3) & ~3) * 4 + tn * HI * 8);
 }
 
 // waves per SIMD the registers are sized for (two tiles of 16-byte chunks in
@@ -401,8 +402,8 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
   const int hs = 2 * d + 16;  // LDS head segment
   const int tn = (int)p.tn;
   unsigned char *rows = smem + w * 64 * hs;              // this wave's KW rows of HI segments
-  double *sqd = (double *)(smem + 4 * 64 * hs);          // [tn][hd]
-  double *sw = sqd + tn * hd;                            // head weights [tn][HI]
+  float *sqf = (float *)(smem + 4 * 64 * hs);            // q [tn][hd] (fp32: exact for 2-byte inputs)
+  double *sw = (double *)(sqf + ((tn * hd + 3) & ~3));   // head weights [tn][HI]
   const uint16_t *kb = (const uint16_t *)p.k + b * p.k_sb;
   // wave tiles of this workgroup: [wt0, wt0 + 4 * tiles * HI / ... ) interleaved over waves
   const int64_t n_wt = (p.Tk + KW - 1) / KW;
@@ -412,7 +413,7 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
   for (int i = tid; i < tn * hd; i += 256) {
     const int tl = i / hd, c = i % hd;
     const int h = c / d, dd = c % d;
-    sqd[tl * hd + c] = load_as_f64(p.q, b * p.q_sb + (p.t0 + tl) * p.q_st + h * p.q_sh + dd, p.dt);
+    sqf[tl * hd + c] = load_as_f32(p.q, b * p.q_sb + (p.t0 + tl) * p.q_st + h * p.q_sh + dd, p.dt);
   }
   for (int i = tid; i < tn * HI; i += 256)
     sw[i] = (double)p.w[b * p.w_sb + (p.t0 + i / HI) * p.w_st + (i % HI) * p.w_sh];
@@ -462,9 +463,11 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
 #pragma unroll
       for (int tl = 0; tl < NQ; ++tl) {
         if (tl >= tn) break;
-        const double *qv = &sqd[tl * hd + h * d + dd];
+        const float4 qa = *(const float4 *)&sqf[tl * hd + h * d + dd];
+        const float4 qb = *(const float4 *)&sqf[tl * hd + h * d + dd + 4];
+        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dot[tl] = __builtin_fma(qv[e], kf[e], dot[tl]);
+        for (int e = 0; e < 8; ++e) dot[tl] = __builtin_fma((double)qv[e], kf[e], dot[tl]);
       }
     }
     // heads of a key are lanes kr*HI + 0..HI-1: the first adds them in order
