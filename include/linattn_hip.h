@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 1
+#define LA_ABI_VERSION 2
 
 /* element types */
 enum {
@@ -249,8 +249,11 @@ int la_topk_rows(const la_topk_args *a, void *stream);
  * scores every key, fused_indexer.py:63-73).  With causal_unit = m > 1 the
  * keys are pooled groups of m tokens and group s is kept when s*m <= offset+t
  * (the compressed-indexing mask of selection.py:739-747); 0 or 1 = tokens.
- * out_idx int32 (B, Tq, k) sorted by (score desc, index asc), -1 padded;
- * out_val fp32 (B, Tq, k), -inf padded (optional).
+ * order 0: out_idx int32 (B, Tq, k) sorted by (score desc, index asc), -1
+ * padded; out_val fp32 (B, Tq, k), -inf padded (optional).
+ * order 1 (an addition): the same selected keys in ascending index order,
+ * -1 padded, out_val must be NULL (no sort is done; the selection is the set
+ * a token mask is built from, selection.py:752-761).
  * q_chunk bounds the queries scored per pass (workspace = q_chunk*Tk*8 bytes
  * plus the top-k scratch); 0 picks one.
  */
@@ -271,6 +274,8 @@ typedef struct {
   int64_t causal_unit;
   int32_t in_dtype;
   int32_t causal;
+  int32_t order; /* 0 = by score (sorted), 1 = ascending index */
+  int32_t reserved;
 } la_indexer_args;
 
 size_t la_indexer_topk_workspace(const la_indexer_args *a);

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -85,7 +85,8 @@ class LaIndexerArgs(ctypes.Structure):
                 ("HI", _i64), ("d", _i64), ("k", _i64), ("q_sb", _i64), ("q_st", _i64),
                 ("q_sh", _i64), ("k_sb", _i64), ("k_st", _i64), ("k_sh", _i64), ("w_sb", _i64),
                 ("w_st", _i64), ("w_sh", _i64), ("offset", _i64), ("q_chunk", _i64),
-                ("causal_unit", _i64), ("in_dtype", _i32), ("causal", _i32)]
+                ("causal_unit", _i64), ("in_dtype", _i32), ("causal", _i32), ("order", _i32),
+                ("reserved", _i32)]
 
 
 class LaBlockSelectArgs(ctypes.Structure):

@@ -563,6 +563,8 @@ static int validate(const la_indexer_args *a) {
              "la_indexer_topk: q/k must be fp32, bf16 or fp16");
   LA_REQUIRE(a->HI <= 8, "la_indexer_topk: at most 8 indexer heads");
   LA_REQUIRE(a->Tk < ((int64_t)1 << 31), "la_indexer_topk: Tk >= 2^31");
+  LA_REQUIRE(a->order == 0 || a->order == 1, "la_indexer_topk: order must be 0 or 1");
+  LA_REQUIRE(a->order == 0 || !a->out_val, "la_indexer_topk: index order returns no values");
   return LA_OK;
 }
 
@@ -585,7 +587,7 @@ static TopkKParams topk_params(const la_indexer_args *a, double *scores, int64_t
   tp.width = a->k;
   tp.pos_off = a->causal ? a->offset : 0;
   tp.pos_unit = a->causal ? std::max<int64_t>(1, a->causal_unit) : 0;
-  tp.order = 0;
+  tp.order = a->order;
   tp.out_idx = a->out_idx;
   tp.out_val = a->out_val;
   return tp;

@@ -197,10 +197,16 @@ __device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
   return r;
 }
 
+// the candidate row of a segmented top-k's final level (G = 1), or null
+__device__ __forceinline__ const int32_t *tk_cand_row(const TopkKParams &p, const TkRow &rw) {
+  return p.cand_idx ? p.cand_idx + ((rw.br / p.Tq) * p.G * p.Tq + rw.tl) * p.row_stride + rw.seg0
+                    : nullptr;
+}
+
 __device__ __forceinline__ void tk_emit_bitmap(const TopkKParams &p, uint32_t *bm, const TkRow &rw,
                                                uint32_t *wtmp) {
   tk_emit_bitmap_row(bm, rw.n_v, rw.own, p.sink, p.window, p.width, p.out_idx + rw.orow * p.width,
-                     p.out_count ? p.out_count + rw.orow : nullptr, wtmp);
+                     p.out_count ? p.out_count + rw.orow : nullptr, wtmp, tk_cand_row(p, rw));
 }
 
 __global__ __launch_bounds__(TK_NT) void topk_rows_kernel(TopkKParams p) {
@@ -680,8 +686,18 @@ __global__ __launch_bounds__(TK_NT) void topk_wave_kernel(TopkKParams p) {
     }
   }
   __builtin_amdgcn_wave_barrier();
-  // ascending emission: lane x < WORDS owns word x (units past n_v are never set)
-  const uint32_t word = lane < WORDS ? bm[lane] : 0u;
+  // ascending emission: lane x < WORDS owns word x (units past n_v are never
+  // set); candidate rows drop slots without a candidate and write cand[i]
+  const int32_t *cand = tk_cand_row(p, rw);
+  uint32_t word = lane < WORDS ? bm[lane] : 0u;
+  if (cand) {
+    uint32_t bits = word;
+    while (bits) {
+      const int bb = __ffs(bits) - 1;
+      if (cand[lane * 32 + bb] < 0) word &= ~(1u << bb);
+      bits &= bits - 1;
+    }
+  }
   const uint32_t cnt = (uint32_t)__popc(word);
   uint32_t incl = cnt;
 #pragma unroll
@@ -695,7 +711,7 @@ __global__ __launch_bounds__(TK_NT) void topk_wave_kernel(TopkKParams p) {
   uint32_t bits = word;
   while (bits) {
     const int bb = __ffs(bits) - 1;
-    if (pos < (uint32_t)p.width) oi[pos] = (int32_t)(lane * 32 + bb);
+    if (pos < (uint32_t)p.width) oi[pos] = cand ? cand[lane * 32 + bb] : (int32_t)(lane * 32 + bb);
     ++pos;
     bits &= bits - 1;
   }
@@ -766,12 +782,14 @@ struct LongPlan {
 
 static int64_t lds_limit() { return (int64_t)max_dynamic_lds() - (int64_t)sizeof(TkShared) - 256; }
 
-// Long rows (keys + sort buffer beyond LDS) of a plain sorted top-k are
-// reduced in segments that fit the LDS; each level keeps k per segment.
+// Long rows (keys + sort buffer beyond LDS) of a plain top-k are reduced in
+// segments that fit the LDS; each level keeps k per segment, in index order,
+// so the candidate rows of the final level are in ascending unit order.
 static LongPlan long_plan(const TopkKParams &p) {
   LongPlan L;
-  const bool plain = p.G == 1 && p.sink == 0 && p.window == 0 && p.order == 0 && !p.force_own &&
-                     !p.cand_idx && p.seg_len == 0;
+  // sorted (order 0) or index-order (order 1) rows of one head, no extras
+  const bool plain = p.G == 1 && p.sink == 0 && p.window == 0 && (p.order == 0 || p.order == 1) &&
+                     !p.force_own && !p.cand_idx && p.seg_len == 0;
   int64_t p2 = 1;
   while (p2 < p.k) p2 <<= 1;
   const int64_t limit = lds_limit();

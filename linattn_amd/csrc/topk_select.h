@@ -221,10 +221,13 @@ __device__ __forceinline__ void tk_wave_select_bits(const uint64_t (&u_in)[KPL],
 
 // Sink units [0, sink) and the window (own - window, own] are OR'd into the
 // bitmap of kept units, which is then written in ascending index order to
-// out[0, width), -1 padded; *count (if given) gets the number kept.
+// out[0, width), -1 padded; *count (if given) gets the number kept.  With
+// cand (a candidate row of a segmented top-k), slot i stands for unit
+// cand[i]: slots whose candidate is -1 are dropped and cand[i] is written.
 __device__ __forceinline__ void tk_emit_bitmap_row(uint32_t *bm, int64_t n_v, int64_t own,
                                                    int64_t sink, int64_t window, int64_t width,
-                                                   int32_t *out, int32_t *count, uint32_t *wtmp) {
+                                                   int32_t *out, int32_t *count, uint32_t *wtmp,
+                                                   const int32_t *cand = nullptr) {
   const int tid = threadIdx.x;
   if (n_v > 0) {
     const int64_t s_end = min(sink, n_v);
@@ -241,7 +244,18 @@ __device__ __forceinline__ void tk_emit_bitmap_row(uint32_t *bm, int64_t n_v, in
   const int64_t wpt = (words + TK_NT - 1) / TK_NT;
   const int64_t w_beg = min(words, (int64_t)tid * wpt), w_end = min(words, w_beg + wpt);
   uint32_t cnt = 0;
-  for (int64_t x = w_beg; x < w_end; ++x) cnt += __popc(bm[x]);
+  for (int64_t x = w_beg; x < w_end; ++x) {
+    if (cand) {  // candidate rows: slots without a candidate (-1) are dropped
+      uint32_t bits = bm[x], keep = bits;
+      while (bits) {
+        const int b = __ffs(bits) - 1;
+        if (cand[x * 32 + b] < 0) keep &= ~(1u << b);
+        bits &= bits - 1;
+      }
+      bm[x] = keep;
+    }
+    cnt += __popc(bm[x]);
+  }
   uint32_t total;
   const uint32_t incl = tk_block_incl_scan(cnt, wtmp, total);
   uint32_t pos = incl - cnt;
@@ -249,7 +263,7 @@ __device__ __forceinline__ void tk_emit_bitmap_row(uint32_t *bm, int64_t n_v, in
     uint32_t bits = bm[x];
     while (bits) {
       const int b = __ffs(bits) - 1;
-      if (pos < (uint32_t)width) out[pos] = (int32_t)(x * 32 + b);
+      if (pos < (uint32_t)width) out[pos] = cand ? cand[x * 32 + b] : (int32_t)(x * 32 + b);
       ++pos;
       bits &= bits - 1;
     }

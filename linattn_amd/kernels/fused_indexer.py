@@ -15,7 +15,7 @@ scan-order cap) is replaced by an exact radix select.
 from __future__ import annotations
 
 import ctypes
-from typing import Tuple
+from typing import Optional, Tuple
 
 import torch
 
@@ -26,13 +26,17 @@ __all__ = ["indexer_topk", "indexer_topk_hip", "indexer_topk_triton"]
 
 def indexer_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, head_weights: torch.Tensor, k: int, *,
                  backend: str = "auto", causal: bool = False, offset: int = 0,
-                 causal_unit: int = 1, q_chunk: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+                 causal_unit: int = 1, q_chunk: int = 0, sorted: bool = True
+                 ) -> Tuple[Optional[torch.Tensor], torch.Tensor]:
     """Top-k indexer scores: ``(values fp32 (B,Tq,k), indices int32 (B,Tq,k))``.
 
     q_idx: (B, Tq, H_I, d), k_idx: (B, Tk, H_I, d) in fp32/bf16/fp16;
     head_weights: (B, Tq, H_I).  ``k`` is clipped to Tk as in the reference.
     With ``causal_unit`` = m > 1 the keys are pooled groups of m tokens and
-    group s is visible to query t when s*m <= offset + t."""
+    group s is visible to query t when s*m <= offset + t.  ``sorted=False``
+    (an addition) returns ``(None, indices)`` with the same selected keys in
+    ascending index order, -1 padded: the token set a selection mask is built
+    from (selection.py:752-761), without the sort."""
     if backend not in ("auto", "hip", "triton"):
         raise ValueError(f"backend {backend!r} is not provided by linattn_amd (only 'hip')")
     dev = N.require_gpu(q_idx, k_idx, head_weights, what="indexer_topk")
@@ -53,10 +57,11 @@ def indexer_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, head_weights: torch.T
     if kk < 1:
         raise ValueError("k must be >= 1")
     idx = torch.empty(B, Tq, kk, dtype=torch.int32, device=dev)
-    val = torch.empty(B, Tq, kk, dtype=torch.float32, device=dev)
+    val = torch.empty(B, Tq, kk, dtype=torch.float32, device=dev) if sorted else None
     a = N.LaIndexerArgs()
     a.q, a.kk, a.w = q_idx.data_ptr(), k_idx.data_ptr(), w.data_ptr()
-    a.out_idx, a.out_val = idx.data_ptr(), val.data_ptr()
+    a.out_idx, a.out_val = idx.data_ptr(), (val.data_ptr() if sorted else None)
+    a.order = 0 if sorted else 1
     a.B, a.Tq, a.Tk, a.HI, a.d, a.k = B, Tq, Tk, HI, d, kk
     a.q_sb, a.q_st, a.q_sh = q_idx.stride(0), q_idx.stride(1), q_idx.stride(2)
     a.k_sb, a.k_st, a.k_sh = k_idx.stride(0), k_idx.stride(1), k_idx.stride(2)

@@ -42,9 +42,12 @@ def indexer_decode_step(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Ten
     ``topk`` tokens per sequence (causal, one list shared by every head,
     fused_indexer.py:52-73), then every query head attends those tokens of the
     paged (optionally fp8) cache.  q (B, Hq, 1, D); q_idx (B, 1, H_I, d);
-    k_idx (B, T, H_I, d); head_weights (B, 1, H_I).  Returns (out, token ids)."""
+    k_idx (B, T, H_I, d); head_weights (B, 1, H_I).  Returns (out, token ids):
+    the selected set in ascending order, -1 padded (the attention reads a set,
+    as the reference's token mask does, selection.py:752-761, so the ids are
+    not sorted by score)."""
     B, Hkv = q.shape[0], k_pool.shape[1]
-    _, idx = indexer_topk(q_idx, k_idx, head_weights, topk, causal=True, offset=pos)
+    _, idx = indexer_topk(q_idx, k_idx, head_weights, topk, causal=True, offset=pos, sorted=False)
     ids = idx.view(B, 1, 1, -1).expand(B, Hkv, 1, idx.shape[-1])
     out = sparse_attention(q, k_pool, v_pool, ids, unit=1, causal=True, offset=pos,
                            page_table=page_table, page_size=page_size, k_scale=k_scale,

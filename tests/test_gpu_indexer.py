@@ -59,6 +59,31 @@ def test_indexer_causal_with_offset(dev):
     check(q, k, w, 128, dev, causal=True, offset=517 - 70)
 
 
+def index_order(ri):
+    """The oracle's (score desc) lists as ascending sets, -1 padded."""
+    out = np.full_like(ri, -1)
+    for r in np.ndindex(ri.shape[:-1]):
+        v = np.sort(ri[r][ri[r] >= 0])
+        out[r][:v.size] = v
+    return out
+
+
+@pytest.mark.parametrize("tq,tk,kk,offset", [
+    (5, 600, 64, 400),      # short rows: one wave per row
+    (3, 9000, 700, 8000),   # register rows
+    (2, 70000, 4096, 69000),  # long rows: segmented levels, candidate rows
+    (1, 70000, 4096, 3000),   # fewer visible keys than k: -1 padded
+])
+def test_indexer_index_order(dev, tq, tk, kk, offset):
+    """sorted=False: the same selection as ascending sets, no values."""
+    q, k, w = inputs(1, tq, tk, 4, 64, seed=11 + tq, dtype=torch.bfloat16)
+    val, idx = indexer_topk(q.to(dev), k.to(dev), w.to(dev), kk, causal=True, offset=offset,
+                            sorted=False)
+    assert val is None
+    _, ri = oracle.indexer_topk(q, k, w, kk, causal=True, offset=offset)
+    assert np.array_equal(idx.cpu().numpy(), index_order(ri))
+
+
 @pytest.mark.parametrize("tq", [1, 3])
 @pytest.mark.parametrize("hi,d,dtype", [(4, 64, torch.bfloat16), (1, 256, torch.bfloat16),
                                         (2, 128, torch.float16), (8, 32, torch.bfloat16)])
