@@ -481,12 +481,15 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
       u[j] = (rw.force && i == own) ? KEY_FORCED : x;
     }
     const uint32_t K = (uint32_t)rw.K;
+    // bitmap rows (segments and unions, few rows in flight) keep the radix
+    // select, which takes fewer barrier steps; sorted rows (many in flight)
+    // use the bitwise search, which issues fewer instructions
     if constexpr (BITMAP) {
       tk_reg_select<KPT>(u, n_v, K, sr, [&](int j, int32_t i, bool take) {
         if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
       });
     } else {
-      tk_reg_select<KPT>(u, n_v, K, sr, [&](int j, int32_t i, bool take) {
+      tk_reg_select_bits<KPT>(u, n_v, K, sr, [&](int j, int32_t i, bool take) {
         const uint64_t tm = __ballot(take);
         uint32_t base = 0;
         if (lane == 0 && tm) base = atomicAdd(&s_fill, (uint32_t)__popcll(tm));

@@ -160,6 +160,121 @@ __device__ __forceinline__ void tk_reg_select(const uint64_t (&u)[KPT], int32_t 
   __syncthreads();
 }
 
+// Top K of the keys u[j] of units t + 256*j (t = thread), j < KPT, among the
+// first n_v units: the selection of tk_reg_select by a bitwise search for the
+// K-th largest key.  T starts as the leading bits all valid keys share and
+// keeps the bits found so far; each step counts the keys >= T | bit (one
+// vector compare per slot, counted from the lane mask on the scalar unit),
+// adds the four waves' counts through LDS (one barrier per step, alternating
+// slots) and keeps the bit when at least K keys reach it.
+// It stops when exactly K do; else T is the K-th largest key and its ties
+// are taken lowest index first.  emit(j, i, take) as in tk_reg_select.
+// The keys of units past n_v are set to 0 in u (no candidate reaches 0).
+template <int KPT, class Emit>
+__device__ __forceinline__ void tk_reg_select_bits(uint64_t (&u)[KPT], int32_t n_v, uint32_t K,
+                                                   TkRegShared<KPT> &sh, Emit emit) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  uint32_t *cnt = sh.wtmp[0];  // [2][TK_NW] counts, alternating steps
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) u[j] = tid + TK_NT * j < n_v ? u[j] : 0ull;
+  if ((int32_t)K >= n_v) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) emit(j, tid + TK_NT * j, tid + TK_NT * j < n_v);
+    __syncthreads();
+    return;
+  }
+  // the bits every valid key shares need no step: start below them
+  uint64_t o = 0, a = ~0ull;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if (tid + TK_NT * j < n_v) {
+      o |= u[j];
+      a &= u[j];
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    o |= __shfl_xor(o, off, 64);
+    a &= __shfl_xor(a, off, 64);
+  }
+  if (lane == 0) {
+    sh.red[0][w] = o;
+    sh.red[1][w] = a;
+  }
+  __syncthreads();
+  o = 0;
+  a = ~0ull;
+#pragma unroll
+  for (int x = 0; x < TK_NW; ++x) {
+    o |= sh.red[0][x];
+    a &= sh.red[1][x];
+  }
+  const uint64_t diff = o ^ a;
+  const int top = diff ? 63 - __clzll((long long)diff) : -1;
+  uint64_t T = top >= 0 ? a & ~((2ull << top) - 1ull) : a;  // 2ull << 63 wraps to 0
+  bool exact = false;
+  int step = 0;
+  for (int bit = top; bit >= 0; --bit, ++step) {
+    const uint64_t T2 = T | (1ull << bit);
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) c += (uint32_t)__popcll(__ballot(u[j] >= T2));
+    uint32_t *slot = cnt + (step & 1) * TK_NW;
+    if (lane == 0) slot[w] = c;
+    __syncthreads();
+    uint32_t tot = 0;
+#pragma unroll
+    for (int x = 0; x < TK_NW; ++x) tot += slot[x];
+    if (tot >= K) {
+      T = T2;
+      if (tot == K) {
+        exact = true;
+        break;
+      }
+    }
+  }
+  if (exact) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) emit(j, tid + TK_NT * j, tid + TK_NT * j < n_v && u[j] >= T);
+    __syncthreads();
+    return;
+  }
+  // T is the K-th largest key: every key above it, then its ties by index
+  // (slot j before slot j + 1, lower waves and lanes first within a slot)
+  uint32_t gt = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) gt += (uint32_t)__popcll(__ballot(u[j] > T));
+  __syncthreads();  // sh.red is read above
+  if (lane == 0) sh.red[0][w] = gt;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const bool eq = tid + TK_NT * j < n_v && u[j] == T;
+    const uint64_t b = __ballot(eq);
+    if (lane == 0) sh.eqc[j][w] = (uint32_t)__popcll(b);
+  }
+  __syncthreads();
+  uint32_t need = K;
+#pragma unroll
+  for (int x = 0; x < TK_NW; ++x) need -= (uint32_t)sh.red[0][x];
+  const uint64_t lt = lanemask_lt(lane);
+  uint32_t eq_before = 0;  // threshold keys in earlier slots
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int32_t i = tid + TK_NT * j;
+    const bool valid = i < n_v;
+    const bool eq = valid && u[j] == T;
+    const uint64_t b = __ballot(eq);
+    uint32_t rank = eq_before + (uint32_t)__popcll(b & lt);
+#pragma unroll
+    for (int x = 0; x < TK_NW; ++x) rank += x < w ? sh.eqc[j][x] : 0u;
+    const bool take = (valid && u[j] > T) || (eq && rank < need);
+#pragma unroll
+    for (int x = 0; x < TK_NW; ++x) eq_before += sh.eqc[j][x];
+    emit(j, i, take);
+  }
+  __syncthreads();
+}
+
 // One wave's top K of the keys u[j] of units lane + 64*j, j < KPL, among the
 // first n_v units, by a bitwise search for the K-th largest key: T keeps the
 // bits found so far and each step counts the keys >= T | bit with one vector
