@@ -165,17 +165,37 @@ __device__ __forceinline__ float dpp_f32(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
 
+// The values of lane l and its partner l ^ 16 (pair16) or l ^ 32 (pair32), in
+// lane order: .x from the lower lane, .y from the upper one, the same pair on
+// both partners.  gfx950 v_permlane16_swap / v_permlane32_swap are VALU lane
+// swaps, so these cost no LDS round trip (unlike __shfl_xor's ds_bpermute).
+__device__ __forceinline__ float2 pair16(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 pair32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair16_sum(float x) { const float2 p = pair16(x); return p.x + p.y; }
+__device__ __forceinline__ float pair32_sum(float x) { const float2 p = pair32(x); return p.x + p.y; }
+__device__ __forceinline__ float pair16_max(float x) { const float2 p = pair16(x); return fmaxf(p.x, p.y); }
+__device__ __forceinline__ float pair32_max(float x) { const float2 p = pair32(x); return fmaxf(p.x, p.y); }
+
 // Sum over aligned groups of N lanes; every lane of a group gets the same sum
 // (each step adds a value to its partner's, and fp addition is commutative).
-// quad_perm [1,0,3,2] and [2,3,0,1], then row_half_mirror and row_mirror.
+// quad_perm [1,0,3,2] and [2,3,0,1], then row_half_mirror and row_mirror, then
+// the 16- and 32-lane swaps.
 template <int N>
 __device__ __forceinline__ float group_sum(float x) {
   if constexpr (N >= 2) x += dpp_f32<0xB1>(x);
   if constexpr (N >= 4) x += dpp_f32<0x4E>(x);
   if constexpr (N >= 8) x += dpp_f32<0x141>(x);
   if constexpr (N >= 16) x += dpp_f32<0x140>(x);
-  if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
-  if constexpr (N >= 64) x += __shfl_xor(x, 32, 64);
+  if constexpr (N >= 32) x = pair16_sum(x);
+  if constexpr (N >= 64) x = pair32_sum(x);
   return x;
 }
 

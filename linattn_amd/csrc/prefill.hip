@@ -182,8 +182,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       }
       float mx = fmaxf(fmaxf(fmaxf(st[qg][0][0], st[qg][0][1]), fmaxf(st[qg][0][2], st[qg][0][3])),
                        fmaxf(fmaxf(st[qg][1][0], st[qg][1][1]), fmaxf(st[qg][1][2], st[qg][1][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = pair32_max(pair16_max(mx));
       // m is a reference maximum: it is raised (and acc, l rescaled) only when
       // a row's maximum exceeds it by more than 2^8 in the exponent, so the
       // weights stay below 256 and the rescale is rare; the final division
@@ -248,8 +247,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // l is a per-lane partial over this lane's keys; sum the 4 lane groups.
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg) {
-    l[qg] += __shfl_xor(l[qg], 16, 64);
-    l[qg] += __shfl_xor(l[qg], 32, 64);
+    l[qg] = pair32_sum(pair16_sum(l[qg]));
   }
   // Merge the two key halves: the kh = 1 wave of each query half hands its
   // state to the kh = 0 wave through LDS (the K buffers are free now).

@@ -595,8 +595,7 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      acc[g][e] += __shfl_xor(acc[g][e], 16, 64);
-      acc[g][e] += __shfl_xor(acc[g][e], 32, 64);
+      acc[g][e] = pair32_sum(pair16_sum(acc[g][e]));
     }
 #pragma unroll
   for (int e = 0; e < 4; ++e) ls[e] = group_sum<16>(ls[e]);
