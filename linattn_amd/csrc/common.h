@@ -75,6 +75,26 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// An empty use of a register value: the compiler waits here for a load of it
+// still in flight.  Placed after the waits of inline-asm loads, it stops the
+// compiler from waiting for its own earlier loads later (by then its counts
+// would also cover the asm loads issued after them).
+template <class T>
+__device__ __forceinline__ void settle(const T &x) {
+  asm volatile("" ::"v"(x));
+}
+
+// Wave-uniform 32-bit read through the scalar cache, waited for at once
+// (lgkmcnt(0): LDS operations in flight are waited for as well).  For reads
+// the compiler would otherwise issue as vector loads: after inline assembly
+// that may write memory it no longer proves a pointer unclobbered, and a
+// vector load's wait also waits for every load issued before it.
+__device__ __forceinline__ int32_t sload_i32(const int32_t *p) {
+  int32_t v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+
 // --------------------------------------------------------- element loads ----
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
