@@ -219,6 +219,41 @@ def bench_c5(dev, steps, warmup):
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def bench_serving(dev, q, pool_k, pool_v, pt, mins, maxs, cfg, steps, warmup):
+    """C4 shapes as a ragged serving step: every sequence at its own position
+    (uniform in [T/2, T-1)) appends one token (K/V into the paged pool, Quest
+    page bounds updated in the same kernel), then a ragged Quest decode step
+    attends.  Runs after the headline (it writes into the pool)."""
+    import torch
+
+    from linattn_amd.kernels.kv_cache import paged_kv_append
+    from linattn_amd.kernels.paged_decode import quest_decode_step
+
+    B, Hkv, T, D, ps = cfg["B"], cfg["Hkv"], cfg["T"], cfg["D"], cfg["page"]
+    g = torch.Generator(device=dev).manual_seed(1)
+    positions = torch.randint(T // 2, T - 1, (B,), generator=g, device=dev).to(torch.int32)
+    k_new = torch.randn(B, Hkv, 1, D, generator=g, device=dev).to(torch.bfloat16)
+    v_new = torch.randn(B, Hkv, 1, D, generator=g, device=dev).to(torch.bfloat16)
+
+    def append():
+        paged_kv_append(k_new, v_new, pool_k, pool_v, pt, positions, page_min=mins,
+                        page_max=maxs, page_size=ps)
+
+    def step():
+        append()
+        quest_decode_step(q, pool_k, pool_v, pt, mins, maxs, page_size=ps, topk=cfg["topk"],
+                          positions=positions)
+
+    ms_append = time_cuda(append, steps, warmup)
+    ms_step = time_cuda(step, steps, warmup)
+    # K, V rows read and written, bounds of the touched page read and written
+    append_bytes = B * Hkv * D * 2 * (2 + 2) + B * Hkv * D * 2 * 2 * 2
+    return {"workload": "ragged serving step on C4 shapes: append 1 token + page bounds, "
+                        "ragged Quest select + attend (positions uniform in [T/2, T-1))",
+            "ms_append": round(ms_append, 4), "append_bytes": append_bytes,
+            "ms_step": round(ms_step, 4), "tok_per_s": round(B / (ms_step * 1e-3), 1)}
+
+
 def _counter_rows(d):
     import csv
     import glob
@@ -377,6 +412,8 @@ def main() -> int:
     result["indexer"] = bench_c2(dev, max(3, args.steps // 4), 2)
     result["prefill"] = bench_c3(dev, max(3, args.steps // 4), 2)
     result["fp8_decode"] = bench_c5(dev, max(3, args.steps // 4), 2)
+    result["serving"] = bench_serving(dev, q, pool_k, pool_v, pt, mins, maxs, cfg,
+                                      max(3, args.steps // 4), 2)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg,
                                               args.cpu_sample, union)

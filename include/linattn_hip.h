@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 2
+#define LA_ABI_VERSION 3
 
 /* element types */
 enum {
@@ -185,9 +185,54 @@ typedef struct {
   int64_t n_pages, m_sb, m_sh, m_sp, m_sd;
   int64_t page_size, pos_offset, k;
   int32_t q_dtype, meta_dtype;
+  /* Optional per-sequence positions (ragged decode): row (b, kvh, t) uses
+   * positions[b] + t in place of pos_offset + t.  NULL: pos_offset. */
+  const int32_t *positions;
 } la_quest_select_args;
 
 int la_quest_select(const la_quest_select_args *a, void *stream);
+
+/*
+ * Paged KV append with Quest page bounds maintained in the same pass.
+ * Fuses the KV concatenation of AttentionVariant.push_kv (core.py:219-220)
+ * with the incremental refresh of QuestAttention._refresh_pages
+ * (variants/selection.py:181-201), and for an fp8 pool the per-token codec of
+ * kv/quant.py:76-93 (group = head_dim: scale = max(absmax, 1e-8)/448, codes =
+ * e4m3fn(x / scale)).
+ * The Tn new tokens of sequence b (k_new / v_new at element strides
+ * n_sb/n_sh/n_st: (B, Hkv, Tn, D)) go to logical positions positions[b] ..
+ * positions[b] + Tn - 1, i.e. slot t % pool_page of physical page
+ * page_table[b*pt_sb + t/pool_page] of the pools (n_phys, Hkv, pool_page, D),
+ * contiguous; tokens whose table entry lies outside [0, n_phys) are dropped
+ * (neither stored nor counted in the bounds).  With
+ * page_min / page_max ((B, Hkv, n_pages, D) at element strides
+ * m_sb/m_sh/m_sp/m_sd, in the key dtype), every Quest page of meta_page tokens
+ * that the new tokens touch gets its channel-wise bounds updated: a page that
+ * starts at or after positions[b] is set to the new tokens' bounds, any other
+ * takes min / max with its stored bounds.  For an append at the end of the
+ * sequence (positions[b] = its length) this equals la_quest_page_bounds over
+ * the grown sequence, bit for bit.  fp8 pools take no bounds.
+ */
+typedef struct {
+  const void *k_new;
+  const void *v_new;
+  void *k_pool;
+  void *v_pool;
+  float *k_scale; /* fp8 pool: (n_phys, Hkv, pool_page) per-token scales */
+  float *v_scale;
+  const int32_t *page_table;
+  const int32_t *positions;
+  void *page_min;
+  void *page_max;
+  int64_t B, Hkv, Tn, D;
+  int64_t n_sb, n_sh, n_st;
+  int64_t n_phys, pool_page, pt_sb, pt_pages;
+  int64_t meta_page, n_pages, m_sb, m_sh, m_sp, m_sd;
+  int32_t in_dtype;   /* LA_F32 or LA_BF16 */
+  int32_t pool_dtype; /* in_dtype, or LA_FP8_E4M3 */
+} la_kv_append_args;
+
+int la_paged_kv_append(const la_kv_append_args *a, void *stream);
 
 /*
  * Row-wise top-k with ties broken by lowest index.

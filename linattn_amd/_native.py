@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -36,6 +36,7 @@ EXPORTED = (
     "la_block_select_workspace",
     "la_block_select",
     "la_block_sparse_prefill",
+    "la_paged_kv_append",
 )
 
 _vp = ctypes.c_void_p
@@ -76,7 +77,17 @@ class LaQuestSelectArgs(ctypes.Structure):
                 ("D", _i64), ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64), ("n_pages", _i64),
                 ("m_sb", _i64), ("m_sh", _i64), ("m_sp", _i64), ("m_sd", _i64),
                 ("page_size", _i64), ("pos_offset", _i64), ("k", _i64), ("q_dtype", _i32),
-                ("meta_dtype", _i32)]
+                ("meta_dtype", _i32), ("positions", _vp)]
+
+
+class LaKvAppendArgs(ctypes.Structure):
+    _fields_ = [("k_new", _vp), ("v_new", _vp), ("k_pool", _vp), ("v_pool", _vp),
+                ("k_scale", _vp), ("v_scale", _vp), ("page_table", _vp), ("positions", _vp),
+                ("page_min", _vp), ("page_max", _vp), ("B", _i64), ("Hkv", _i64), ("Tn", _i64),
+                ("D", _i64), ("n_sb", _i64), ("n_sh", _i64), ("n_st", _i64), ("n_phys", _i64),
+                ("pool_page", _i64), ("pt_sb", _i64), ("pt_pages", _i64), ("meta_page", _i64),
+                ("n_pages", _i64), ("m_sb", _i64), ("m_sh", _i64), ("m_sp", _i64), ("m_sd", _i64),
+                ("in_dtype", _i32), ("pool_dtype", _i32)]
 
 
 class LaIndexerArgs(ctypes.Structure):
@@ -145,6 +156,7 @@ def load() -> ctypes.CDLL:
     L.la_block_select_workspace.restype = ctypes.c_size_t
     L.la_block_select.argtypes = [P(LaBlockSelectArgs), _vp]
     L.la_block_sparse_prefill.argtypes = [P(LaPrefillArgs), _vp]
+    L.la_paged_kv_append.argtypes = [P(LaKvAppendArgs), _vp]
     for name in EXPORTED:
         fn = getattr(L, name)
         if fn.restype is None or fn.restype is ctypes.c_int:

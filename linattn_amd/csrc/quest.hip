@@ -229,6 +229,7 @@ struct QsKP {
   int32_t *out_idx, *out_count;
   int64_t Hq, Hkv, Tq, D, q_sb, q_sh, q_st, n_pages, m_sb, m_sh, m_sd;
   int64_t page_size, pos_offset, k, width;
+  const int32_t *positions;
   int32_t q_dt;
 };
 
@@ -251,7 +252,7 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
     qd[g * D + d] = load_as_f64(a.q, b * a.q_sb + (kvh * G + g) * a.q_sh + t * a.q_st + d, a.q_dt);
   }
   for (int i = tid; i < NP / 32; i += TK_NT) bm[i] = 0u;
-  const int64_t pos = a.pos_offset + t;
+  const int64_t pos = (a.positions ? (int64_t)a.positions[b] : a.pos_offset) + t;
   const int64_t u_own = pos >= 0 ? pos / a.page_size : -1;
   const int32_t n_v = (int32_t)min(a.n_pages, u_own + 1);
   const int32_t own = (int32_t)min(u_own, a.n_pages - 1);
@@ -507,6 +508,7 @@ extern "C" int la_quest_select(const la_quest_select_args *a, void *stream) {
   k.m_sd = a->m_sd;
   k.page_size = a->page_size;
   k.pos_offset = a->pos_offset;
+  k.positions = a->positions;
   k.k = std::max<int64_t>(1, std::min(a->k, a->n_pages));
   k.width = G * k.k;
   k.q_dt = a->q_dtype;

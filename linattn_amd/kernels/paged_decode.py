@@ -83,16 +83,34 @@ def paged_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, page_ids: to
 
 def quest_decode_step(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                       page_table: torch.Tensor, page_min: torch.Tensor, page_max: torch.Tensor, *,
-                      page_size: int, topk: int, pos: int, gqa_union: bool = True,
+                      page_size: int, topk: int, pos: Optional[int] = None,
+                      positions: Optional[torch.Tensor] = None, gqa_union: bool = True,
                       kv_len: Optional[torch.Tensor] = None, scale: Optional[float] = None,
                       out_dtype: Optional[torch.dtype] = None, num_splits: int = 0
                       ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """One Quest decode step for a batch of sequences sharing position ``pos``.
+    """One Quest decode step: every sequence at position ``pos``, or (ragged
+    batches) sequence b at ``positions[b]`` (int32 (B,)).
 
     q: (B, Hq, 1, D); k/v pools (n_phys, Hkv, page_size, D); page_table int32
     (B, pages); page_min/max (B, Hkv, pages, D).  Selects ``topk`` pages per
-    query head (own page forced, GQA union by default) and attends them.
+    query head (own page forced, GQA union by default) and attends them; with
+    ``positions`` the keys of sequence b are those before positions[b] + 1.
     Returns (out (B, Hq, 1, D), ids, counts)."""
+    if (pos is None) == (positions is None):
+        raise ValueError("pass exactly one of pos and positions")
+    if positions is not None:
+        if q.shape[2] != 1:
+            raise ValueError("positions: one query per sequence (decode)")
+        ids, counts = quest_select_hip(q, page_min, page_max, page_size=page_size, topk=topk,
+                                       gqa_union=gqa_union, positions=positions)
+        lens = positions + 1
+        if kv_len is not None:
+            lens = torch.minimum(lens, kv_len)
+        out = sparse_attention(q, k_pool, v_pool, ids, unit=page_size, counts=counts,
+                               causal=False, page_table=page_table, page_size=page_size,
+                               kv_len=lens.to(torch.int32), scale=scale, out_dtype=out_dtype,
+                               num_splits=num_splits)
+        return out, ids, counts
     ids, counts = quest_select_hip(q, page_min, page_max, page_size=page_size, topk=topk,
                                    offset=pos, gqa_union=gqa_union)
     out = sparse_attention(q, k_pool, v_pool, ids, unit=page_size, counts=counts, causal=True,

@@ -136,7 +136,8 @@ def _topk(scores: torch.Tensor, *, k: int, width: int, group: int, order: int,
 
 
 def quest_select_hip(q: torch.Tensor, mins: torch.Tensor, maxs: torch.Tensor, *, page_size: int,
-                     topk: int, offset: int = 0, gqa_union: bool = True
+                     topk: int, offset: int = 0, gqa_union: bool = True,
+                     positions: Optional[torch.Tensor] = None
                      ) -> Tuple[torch.Tensor, torch.Tensor]:
     """QuestAttention.page_selection (selection.py:214-237) as page lists.
 
@@ -145,14 +146,19 @@ def quest_select_hip(q: torch.Tensor, mins: torch.Tensor, maxs: torch.Tensor, *,
     ``gqa_union`` (the reference default) the G query heads of a KV head read
     the union of their pages: ids (B, Hkv, Tq, G*k) ascending, -1 padded.
     Otherwise each query head keeps its own list: ids (B, Hq, Tq, k) by
-    (score desc, index asc).  Also returns counts (valid entries per list)."""
-    dev = N.require_gpu(q, mins, maxs, what="quest_select_hip")
+    (score desc, index asc).  Also returns counts (valid entries per list).
+    ``positions`` (int32 (B,), ragged batches) replaces ``offset`` per
+    sequence: query t of sequence b sits at positions[b] + t."""
+    dev = N.require_gpu(q, mins, maxs, positions, what="quest_select_hip")
     B, Hq, Tq, D = q.shape
     Hkv, P = mins.shape[1], mins.shape[2]
     G = Hq // Hkv
     k = max(1, min(int(topk), P))
     if mins.shape != (B, Hkv, P, D) or maxs.shape != mins.shape or Hq % Hkv:
         raise ValueError("mins/maxs must be (B, Hkv, P, D) with Hq a multiple of Hkv")
+    if positions is not None and (positions.dtype != torch.int32 or positions.shape != (B,)
+                                  or not positions.is_contiguous()):
+        raise ValueError("positions must be contiguous int32 (B,)")
     if gqa_union and G > 1 and mins.stride() == maxs.stride() and mins.dtype == maxs.dtype:
         # one pass: scores, per-head top-k and the union (la_quest_select)
         ids = torch.empty(B, Hkv, Tq, G * k, dtype=torch.int32, device=dev)
@@ -166,10 +172,18 @@ def quest_select_hip(q: torch.Tensor, mins: torch.Tensor, maxs: torch.Tensor, *,
         a.m_sb, a.m_sh, a.m_sp, a.m_sd = mins.stride()
         a.page_size, a.pos_offset, a.k = page_size, offset, k
         a.q_dtype, a.meta_dtype = N.dtype_code(q.dtype), N.dtype_code(mins.dtype)
+        a.positions = N.ptr(positions)
         rc = N.load().la_quest_select(ctypes.byref(a), N.stream_handle(dev))
         if rc != N.LA_ERR_UNSUPPORTED:
             N.check(rc, "quest_select_hip")
             return ids, counts
+    if positions is not None:
+        # two-pass path: one selection per sequence at its own position
+        # (reads the positions on the host)
+        parts = [quest_select_hip(q[b:b + 1], mins[b:b + 1], maxs[b:b + 1], page_size=page_size,
+                                  topk=topk, offset=int(pb), gqa_union=gqa_union)
+                 for b, pb in enumerate(positions.tolist())]
+        return torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])
     scores = page_scores_hip(q, mins, maxs)
     if gqa_union and G > 1:
         ids, counts, _ = _topk(scores, k=k, width=G * k, group=G, order=1, pos_offset=offset,

@@ -24,6 +24,7 @@ STRUCTS = {
     "la_indexer_args": N.LaIndexerArgs,
     "la_block_select_args": N.LaBlockSelectArgs,
     "la_prefill_args": N.LaPrefillArgs,
+    "la_kv_append_args": N.LaKvAppendArgs,
 }
 
 
