@@ -254,6 +254,42 @@ def bench_serving(dev, q, pool_k, pool_v, pt, mins, maxs, cfg, steps, warmup):
             "ms_step": round(ms_step, 4), "tok_per_s": round(B / (ms_step * 1e-3), 1)}
 
 
+def bench_moba(dev, steps, warmup):
+    """MoBA decode (selection.py:610-640; the same routing is NSA's selection
+    branch): B=16, 32/8 heads, D=128, T=16384 bf16, 64-token blocks, top-16
+    blocks + own block per query head.  The routing pools K every step, as
+    the reference does (no cached block means)."""
+    import torch
+
+    from linattn_amd.kernels.block_sparse import sparse_attention
+    from linattn_amd.kernels.routing import gate_select_hip
+
+    B, Hq, Hkv, T, D, bs, topk = 16, 32, 8, 16384, 128, 64, 16
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn(B, Hq, 1, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, T, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, T, D, generator=g, device=dev).to(torch.bfloat16)
+
+    def route():
+        return gate_select_hip(q, k, block=bs, topk=topk, offset=T - 1)
+
+    ids, counts = route()
+
+    def step():
+        i, c = route()
+        sparse_attention(q, k, v, i, unit=bs, counts=c, causal=True, offset=T - 1)
+
+    ms_route = time_cuda(route, steps, warmup)
+    ms_step = time_cuda(step, steps, warmup)
+    pool_bytes = B * Hkv * T * D * 2
+    att_bytes = int(counts.sum()) * bs * D * 2 * 2
+    return {"workload": "MoBA decode, B=16, T=16384, 32/8 heads, D=128, bf16, block 64, top-16",
+            "ms_route": round(ms_route, 4), "ms_step": round(ms_step, 4),
+            "tok_per_s": round(B / (ms_step * 1e-3), 1),
+            "route_GBps": round(pool_bytes / (ms_route * 1e-3) / 1e9, 1),
+            "attend_bytes": att_bytes}
+
+
 def _counter_rows(d):
     import csv
     import glob
@@ -412,6 +448,7 @@ def main() -> int:
     result["indexer"] = bench_c2(dev, max(3, args.steps // 4), 2)
     result["prefill"] = bench_c3(dev, max(3, args.steps // 4), 2)
     result["fp8_decode"] = bench_c5(dev, max(3, args.steps // 4), 2)
+    result["moba_decode"] = bench_moba(dev, max(3, args.steps // 4), 2)
     result["serving"] = bench_serving(dev, q, pool_k, pool_v, pt, mins, maxs, cfg,
                                       max(3, args.steps // 4), 2)
     if not args.no_cpu_baseline:

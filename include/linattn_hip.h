@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 3
+#define LA_ABI_VERSION 4
 
 /* element types */
 enum {
@@ -355,6 +355,42 @@ typedef struct {
 
 size_t la_block_select_workspace(const la_block_select_args *a);
 int la_block_select(const la_block_select_args *a, void *stream);
+
+/*
+ * Per-query block routing: the gate of MoBAAttention.select
+ * (variants/selection.py:624-634) and the blockwise selection of
+ * NSAAttention.selection_mask (variants/native_sparse.py:78-93), which compute
+ * the same lists.  For query t of (b, h) at position pos = offset + t, key
+ * block j (tokens [j*block, (j+1)*block), the tail block padded by repeating
+ * the last row as block_reduce does, core.py:115-117) is visible when
+ * j*block <= pos; the gate is q_t . mean(K block j) in fp64 (products added
+ * over d in order; the positive 1/sqrt(D) of the reference is left out, it
+ * does not change the ranking); the top min(topk, visible) visible blocks are
+ * kept (ties to the lowest block) and the query's own block pos/block is OR'd
+ * in (selection.py:632-633).
+ * q: (B, Hq, Tq, D), k: (B, Hkv, T, D) at element strides; query head h reads
+ * KV head h / (Hq/Hkv).  Output: out_idx[((b*Hq + h)*Tq + t)*width + i]
+ * ascending, -1 padded (width >= min(topk, blocks) + 1), out_count the number
+ * kept.  Workspace: la_gate_select_workspace bytes (fp64 q, pooled keys and
+ * the gate rows).
+ */
+typedef struct {
+  const void *q;
+  const void *k;
+  int32_t *out_idx;
+  int32_t *out_count;
+  void *workspace;
+  int64_t ws_bytes;
+  int64_t B, Hq, Hkv, Tq, T, D;
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  int64_t block, topk, offset, width;
+  int32_t in_dtype;
+  int32_t reserved;
+} la_gate_select_args;
+
+size_t la_gate_select_workspace(const la_gate_select_args *a);
+int la_gate_select(const la_gate_select_args *a, void *stream);
 
 /*
  * Block-sparse causal prefill on the matrix cores (MFMA bf16, fp32 accumulate).

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -37,6 +37,8 @@ EXPORTED = (
     "la_block_select",
     "la_block_sparse_prefill",
     "la_paged_kv_append",
+    "la_gate_select_workspace",
+    "la_gate_select",
 )
 
 _vp = ctypes.c_void_p
@@ -109,6 +111,14 @@ class LaBlockSelectArgs(ctypes.Structure):
                 ("in_dtype", _i32), ("reserved", _i32)]
 
 
+class LaGateSelectArgs(ctypes.Structure):
+    _fields_ = [("q", _vp), ("k", _vp), ("out_idx", _vp), ("out_count", _vp), ("workspace", _vp),
+                ("ws_bytes", _i64), ("B", _i64), ("Hq", _i64), ("Hkv", _i64), ("Tq", _i64),
+                ("T", _i64), ("D", _i64), ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64),
+                ("k_sb", _i64), ("k_sh", _i64), ("k_st", _i64), ("block", _i64), ("topk", _i64),
+                ("offset", _i64), ("width", _i64), ("in_dtype", _i32), ("reserved", _i32)]
+
+
 class LaPrefillArgs(ctypes.Structure):
     _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp), ("ids", _vp), ("counts", _vp),
                 ("B", _i64), ("Hq", _i64), ("Hkv", _i64), ("T", _i64), ("D", _i64),
@@ -157,6 +167,9 @@ def load() -> ctypes.CDLL:
     L.la_block_select.argtypes = [P(LaBlockSelectArgs), _vp]
     L.la_block_sparse_prefill.argtypes = [P(LaPrefillArgs), _vp]
     L.la_paged_kv_append.argtypes = [P(LaKvAppendArgs), _vp]
+    L.la_gate_select_workspace.argtypes = [P(LaGateSelectArgs)]
+    L.la_gate_select_workspace.restype = ctypes.c_size_t
+    L.la_gate_select.argtypes = [P(LaGateSelectArgs), _vp]
     for name in EXPORTED:
         fn = getattr(L, name)
         if fn.restype is None or fn.restype is ctypes.c_int:

@@ -86,10 +86,14 @@ __global__ __launch_bounds__(NT) void mean_pool_vec_kernel(const void *x, int dt
 constexpr int BS_TQ = 64, BS_TK = 64, BS_DC = 32, BS_NT = 256;
 
 // scores[(b*Hq+h)*nqb + i][j] = sum_d fl(qbar[b,h,i,d] * kbar[b,h/G,j,d]) for
-// the 64x64 tile (i, j), j <= i (tiles above the diagonal are skipped).
+// the 64x64 tile (i, j).  Row i sits at position pos0 + i*qunit and column j
+// starts at j*kunit; tiles whose every column starts past every row's
+// position are skipped (causal: their scores are never read).
 __global__ __launch_bounds__(BS_NT) void block_score_kernel(const double *qbar, const double *kbar,
                                                             int64_t Hq, int64_t Hkv, int64_t nqb,
-                                                            int64_t nkb, int64_t D, double *scores) {
+                                                            int64_t nkb, int64_t D, int64_t pos0,
+                                                            int64_t qunit, int64_t kunit,
+                                                            double *scores) {
   __shared__ double sq[BS_DC][BS_TQ + 2];
   __shared__ double sk[BS_DC][BS_TK + 2];
   const int tid = threadIdx.x;
@@ -97,7 +101,7 @@ __global__ __launch_bounds__(BS_NT) void block_score_kernel(const double *qbar, 
   const int64_t i0 = (int64_t)blockIdx.y * BS_TQ, j0 = (int64_t)blockIdx.x * BS_TK;
   const int64_t bh = blockIdx.z;
   const int64_t b = bh / Hq, h = bh % Hq;
-  if (j0 > min(i0 + BS_TQ - 1, nqb - 1)) return;  // entirely above the diagonal
+  if (j0 * kunit > pos0 + min(i0 + BS_TQ - 1, nqb - 1) * qunit) return;  // all in the future
   const double *qb = qbar + bh * nqb * D;
   const double *kb = kbar + (b * Hkv + h / (Hq / Hkv)) * nkb * D;
   double acc[4][4];
@@ -137,6 +141,30 @@ __global__ __launch_bounds__(BS_NT) void block_score_kernel(const double *qbar, 
       if (j < nkb) scores[(bh * nqb + i) * nkb + j] = acc[a][c];
     }
   }
+}
+
+// Mean of every `bs` rows of x[b][h] (rows past T repeat row T-1) into
+// out[b][h][blk][d] in fp64; bs = 1 is the exact widening to fp64.
+static void pool_rows(const void *x, int dt, int64_t B, int64_t H, int64_t T, int64_t D, int64_t sb,
+                      int64_t sh, int64_t s_t, int64_t bs, int64_t nb, double *out,
+                      hipStream_t st) {
+  const int64_t esz = dt == LA_F32 ? 4 : 2;
+  const dim3 grid((unsigned)nb, (unsigned)H, (unsigned)B);
+  const bool vec = bs <= 64 && (D * esz) % 16 == 0 && D * esz <= 512 && (uintptr_t)x % 16 == 0 &&
+                   (sb * esz) % 16 == 0 && (sh * esz) % 16 == 0 && (s_t * esz) % 16 == 0;
+  const size_t lds = (size_t)(bs * D * esz);
+  // 128 threads when one thread per d covers the row (the block stays in LDS
+  // only while it is summed, so several blocks per CU overlap)
+  if (vec && esz == 4 && D <= 128)
+    mean_pool_vec_kernel<4, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+  else if (vec && esz == 4)
+    mean_pool_vec_kernel<4, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+  else if (vec && D <= 128)
+    mean_pool_vec_kernel<2, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+  else if (vec)
+    mean_pool_vec_kernel<2, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+  else
+    mean_pool_kernel<<<grid, 128, 0, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
 }
 
 struct BsLayout {
@@ -188,39 +216,15 @@ extern "C" int la_block_select(const la_block_select_args *a, void *stream) {
   double *qbar = (double *)(ws + L.qbar_off);
   double *kbar = (double *)(ws + L.kbar_off);
   double *sc = (double *)(ws + L.sc_off);
-  const int64_t esz = a->in_dtype == LA_F32 ? 4 : 2;
-  auto pool = [&](const void *x, int64_t sb, int64_t sh, int64_t s_t, int64_t H, int64_t nb,
-                  double *out) {
-    const dim3 grid((unsigned)nb, (unsigned)H, (unsigned)a->B);
-    const bool vec = a->block <= 64 && (a->D * esz) % 16 == 0 && a->D * esz <= 512 &&
-                     (uintptr_t)x % 16 == 0 && (sb * esz) % 16 == 0 && (sh * esz) % 16 == 0 &&
-                     (s_t * esz) % 16 == 0;
-    const size_t lds = (size_t)(a->block * a->D * esz);
-    // 128 threads when one thread per d covers the row (the block stays in LDS
-    // only while it is summed, so several blocks per CU overlap)
-    if (vec && esz == 4 && a->D <= 128)
-      mean_pool_vec_kernel<4, 128><<<grid, 128, lds, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
-                                                           a->block, H, nb, out);
-    else if (vec && esz == 4)
-      mean_pool_vec_kernel<4, 256><<<grid, 256, lds, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
-                                                           a->block, H, nb, out);
-    else if (vec && a->D <= 128)
-      mean_pool_vec_kernel<2, 128><<<grid, 128, lds, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
-                                                           a->block, H, nb, out);
-    else if (vec)
-      mean_pool_vec_kernel<2, 256><<<grid, 256, lds, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t,
-                                                           a->block, H, nb, out);
-    else
-      mean_pool_kernel<<<grid, 128, 0, st>>>(x, a->in_dtype, a->T, a->D, sb, sh, s_t, a->block, H,
-                                             nb, out);
-  };
-  pool(a->q, a->q_sb, a->q_sh, a->q_st, a->Hq, L.nqb, qbar);
+  pool_rows(a->q, a->in_dtype, a->B, a->Hq, a->T, a->D, a->q_sb, a->q_sh, a->q_st, a->block, L.nqb,
+            qbar, st);
   LA_LAUNCHED();
-  pool(a->k, a->k_sb, a->k_sh, a->k_st, a->Hkv, L.nkb, kbar);
+  pool_rows(a->k, a->in_dtype, a->B, a->Hkv, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block, L.nkb,
+            kbar, st);
   LA_LAUNCHED();
   block_score_kernel<<<dim3((unsigned)ceil_div(L.nkb, BS_TK), (unsigned)ceil_div(L.nqb, BS_TQ),
                             (unsigned)(a->B * a->Hq)),
-                       BS_NT, 0, st>>>(qbar, kbar, a->Hq, a->Hkv, L.nqb, L.nkb, a->D, sc);
+                       BS_NT, 0, st>>>(qbar, kbar, a->Hq, a->Hkv, L.nqb, L.nkb, a->D, 0, 1, 1, sc);
   LA_LAUNCHED();
   TopkKParams tp{};
   tp.scores = sc;
@@ -237,6 +241,92 @@ extern "C" int la_block_select(const la_block_select_args *a, void *stream) {
   tp.pos_unit = 1;
   tp.sink = a->sink_blocks;
   tp.window = a->window_blocks;
+  tp.order = 1;
+  tp.out_idx = a->out_idx;
+  tp.out_count = a->out_count;
+  return topk_launch(tp, st);
+}
+
+// ------------------------------------------------------------ gate select --
+// Per-query block routing: MoBA's gate (variants/selection.py:624-634) and
+// the blockwise selection of NSA (variants/native_sparse.py:78-93), which
+// compute the same thing: g[j] = q_t . mean(K block j) over the visible
+// blocks (start <= pos_t = offset + t), the top-k blocks by gate, and the
+// query's own block OR'd in.  The gates are fp64, fl(q_d * kbar_d) added
+// over d in order, without the positive 1/sqrt(D) factor (it does not change
+// the ranking); ties go to the lowest block.
+namespace la {
+struct GsLayout {
+  int64_t nkb, qbar_off, kbar_off, sc_off, bytes;
+};
+static GsLayout gs_layout(const la_gate_select_args *a) {
+  GsLayout L{};
+  L.nkb = ceil_div(a->T, a->block);
+  L.qbar_off = 0;
+  L.kbar_off = L.qbar_off + a->B * a->Hq * a->Tq * a->D * 8;
+  L.sc_off = L.kbar_off + a->B * a->Hkv * L.nkb * a->D * 8;
+  L.bytes = L.sc_off + a->B * a->Hq * a->Tq * L.nkb * 8;
+  return L;
+}
+static int gs_validate(const la_gate_select_args *a) {
+  LA_REQUIRE(a && a->q && a->k && a->out_idx, "la_gate_select: null pointer");
+  LA_REQUIRE(a->B > 0 && a->Hq > 0 && a->Hkv > 0 && a->Tq > 0 && a->T > 0 && a->D > 0 &&
+                 a->block > 0,
+             "la_gate_select: bad shape");
+  LA_REQUIRE(a->Hq % a->Hkv == 0, "n_heads must be a multiple of n_kv_heads");
+  LA_REQUIRE(a->topk >= 1, "la_gate_select: topk");
+  LA_REQUIRE(a->offset >= 0, "la_gate_select: offset");
+  LA_REQUIRE(a->width >= std::min(a->topk, ceil_div(a->T, a->block)) + 1,
+             "la_gate_select: width < min(topk, blocks) + 1");
+  LA_REQUIRE(a->in_dtype == LA_F32 || a->in_dtype == LA_BF16 || a->in_dtype == LA_F16,
+             "la_gate_select: q/k dtype");
+  return LA_OK;
+}
+}  // namespace la
+
+extern "C" size_t la_gate_select_workspace(const la_gate_select_args *a) {
+  if (gs_validate(a) != LA_OK) return 0;
+  return (size_t)gs_layout(a).bytes;
+}
+
+extern "C" int la_gate_select(const la_gate_select_args *a, void *stream) {
+  int rc = gs_validate(a);
+  if (rc != LA_OK) return rc;
+  const GsLayout L = gs_layout(a);
+  if (!a->workspace || a->ws_bytes < L.bytes)
+    return fail(LA_ERR_WORKSPACE, "la_gate_select: workspace %lld < %lld bytes",
+                (long long)a->ws_bytes, (long long)L.bytes);
+  hipStream_t st = (hipStream_t)stream;
+  char *ws = (char *)a->workspace;
+  double *qbar = (double *)(ws + L.qbar_off);
+  double *kbar = (double *)(ws + L.kbar_off);
+  double *sc = (double *)(ws + L.sc_off);
+  pool_rows(a->q, a->in_dtype, a->B, a->Hq, a->Tq, a->D, a->q_sb, a->q_sh, a->q_st, 1, a->Tq, qbar,
+            st);  // q widened to fp64
+  LA_LAUNCHED();
+  pool_rows(a->k, a->in_dtype, a->B, a->Hkv, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block,
+            L.nkb, kbar, st);
+  LA_LAUNCHED();
+  block_score_kernel<<<dim3((unsigned)ceil_div(L.nkb, BS_TK), (unsigned)ceil_div(a->Tq, BS_TQ),
+                            (unsigned)(a->B * a->Hq)),
+                       BS_NT, 0, st>>>(qbar, kbar, a->Hq, a->Hkv, a->Tq, L.nkb, a->D, a->offset, 1,
+                                       a->block, sc);
+  LA_LAUNCHED();
+  TopkKParams tp{};
+  tp.scores = sc;
+  tp.row_stride = L.nkb;
+  tp.G = 1;
+  tp.Tq = a->Tq;
+  tp.NG = a->B * a->Hq * a->Tq;
+  tp.t_base = 0;
+  tp.out_tq = a->Tq;
+  tp.n = L.nkb;
+  tp.k = a->topk;
+  tp.width = a->width;
+  tp.pos_off = a->offset;  // visible: block start <= offset + t; own = (offset + t) / block
+  tp.pos_unit = a->block;
+  tp.sink = 0;
+  tp.window = 1;  // the own block, OR'd after the top-k (selection.py:632-633)
   tp.order = 1;
   tp.out_idx = a->out_idx;
   tp.out_count = a->out_count;

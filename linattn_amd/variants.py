@@ -10,6 +10,8 @@ selection kernels and runs the HIP executor, while ``stats``/``read_budget``/
 * ``hip_quest``          QuestAttention (variants/selection.py:139-248)
 * ``hip_dsa``            DSAAttention (selection.py:659-789), token or pooled-group
                          indexing, sink + window OR'd in
+* ``hip_moba``           MoBAAttention (selection.py:610-640): per-query routing by
+                         q . mean(K block), own block added
 * ``hip_sliding_window`` SlidingWindowAttention (variants/local.py:22-61)
 * ``hip_streaming_sink`` StreamingSinkAttention (local.py:64-80)
 
@@ -28,9 +30,10 @@ from linattn_amd.core import AttnConfig, AttentionVariant
 from linattn_amd.kernels.block_sparse import sparse_attention
 from linattn_amd.kernels.fused_indexer import indexer_topk
 from linattn_amd.kernels.quest_pages import alloc_page_meta, page_update_hip, quest_select_hip
+from linattn_amd.kernels.routing import gate_select_hip
 
-__all__ = ["HipAttention", "HipQuest", "HipDSA", "HipSlidingWindow", "HipStreamingSink",
-           "SUPPORTED"]
+__all__ = ["HipAttention", "HipQuest", "HipDSA", "HipMoBA", "HipSlidingWindow",
+           "HipStreamingSink", "SUPPORTED"]
 
 
 def _reads_per_query(ids: torch.Tensor, unit: int, offset: int, t_k: int) -> float:
@@ -290,9 +293,39 @@ class HipDSA(HipAttention):
         return super().flops(seq_len, batch) + int(sel)
 
 
+class HipMoBA(HipAttention):
+    """MoBAAttention (selection.py:610-640) on the GPU: every query routes to
+    the ``topk_blocks`` visible key blocks of highest gate q . mean(K block)
+    (``gate_select_hip``, fp64 gates, ties to the lowest block) plus its own
+    block, then the executor reads those blocks intersected with causality
+    (the effective mask of selection.py:86-108)."""
+
+    reference = "moba"
+
+    def attend(self, q, state, offset: int = 0):
+        k, v = state["k"], state["v"]
+        bs = self.cfg.block_size
+        ids, counts = gate_select_hip(q, k, block=bs, topk=self.cfg.topk_blocks, offset=offset)
+        out = sparse_attention(q, k, v, ids, unit=bs, counts=counts, causal=True, offset=offset,
+                               out_dtype=q.dtype)
+        self._extra = {"blocks_per_query": float(counts.to(torch.float64).mean()),
+                       "reads_per_query": _reads_per_query(ids, bs, offset, k.shape[-2])}
+        return out
+
+    def read_budget(self, seq_len, batch=1):
+        c = self.cfg
+        return float(min(seq_len, c.topk_blocks * c.block_size + c.window_size))
+
+    def flops(self, seq_len, batch=1):
+        n_kb = (seq_len + self.cfg.block_size - 1) // self.cfg.block_size
+        sel = 2 * batch * self.cfg.n_heads * seq_len * n_kb * self.cfg.head_dim
+        return super().flops(seq_len, batch) + int(sel)
+
+
 SUPPORTED = {
     "quest": HipQuest,
     "dsa": HipDSA,
+    "moba": HipMoBA,
     "sliding_window": HipSlidingWindow,
     "streaming_sink": HipStreamingSink,
 }

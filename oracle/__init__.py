@@ -504,6 +504,51 @@ def block_select(q, k, *, block: int, topk: int, sink_blocks: int = 1,
     return out
 
 
+# ------------------------------------------------------ per-query routing --
+def gate_select(q, k, *, block: int, topk: int, offset: int = 0) -> np.ndarray:
+    """MoBA's gate routing (selection.py:610-640), also NSA's blockwise
+    selection (native_sparse.py:78-93): for query t at position offset + t,
+    blocks whose start is <= the position are visible; gate = q_t .
+    mean(K block) (block_reduce with the tail repeating the last row,
+    core.py:102-120; the positive 1/sqrt(D) left out), fp64 with products
+    added over d in order (la_oracle.c); the top min(topk, n_blocks) visible
+    blocks (ties to the lowest) plus the own block.  Returns (B, Hq, Tq,
+    min(topk, n_blocks) + 1) ascending, -1 padded."""
+    q, k = to_f64(q), to_f64(k)
+    B, Hq, Tq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    nkb = (T + block - 1) // block
+    L = lib()
+    kp = np.zeros((B, Hkv, nkb, D))
+    for b in range(B):
+        for h in range(Hkv):
+            x = np.ascontiguousarray(k[b, h])
+            o = np.zeros((nkb, D))
+            L.or_mean_pool(_p(x, _D), T, D, block, _p(o, _D))
+            kp[b, h] = o
+    gates = np.zeros((B, Hq, Tq, nkb))
+    for b in range(B):
+        for h in range(Hq):
+            a = np.ascontiguousarray(q[b, h])
+            c = np.ascontiguousarray(kp[b, h // G])
+            o = np.zeros((Tq, nkb))
+            L.or_dot_rows(_p(a, _D), _p(c, _D), Tq, nkb, D, _p(o, _D))
+            gates[b, h] = o
+    pos = np.arange(Tq) + offset
+    n_valid = np.minimum(nkb, pos // block + 1)
+    own = np.minimum(pos // block, nkb - 1)
+    kk = max(1, min(topk, nkb))
+    idx, _ = topk_rows(gates, kk, n_valid=n_valid)
+    out = np.full((B, Hq, Tq, kk + 1), -1, dtype=np.int32)
+    for b in range(B):
+        for h in range(Hq):
+            for t in range(Tq):
+                u = sorted(set(int(x) for x in idx[b, h, t] if x >= 0) | {int(own[t])})
+                out[b, h, t, :len(u)] = u
+    return out
+
+
 # ------------------------------------------------------------------ local --
 def window_mask(t_q: int, t_k: int, offset: int, window: int, sink: int) -> np.ndarray:
     """j <= i and (i - j < window or j < sink); local.py:47-53."""

@@ -25,6 +25,7 @@ STRUCTS = {
     "la_block_select_args": N.LaBlockSelectArgs,
     "la_prefill_args": N.LaPrefillArgs,
     "la_kv_append_args": N.LaKvAppendArgs,
+    "la_gate_select_args": N.LaGateSelectArgs,
 }
 
 

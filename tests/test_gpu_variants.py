@@ -134,3 +134,56 @@ def test_hip_dsa_matches_oracle(dev, ratio):
                     mask[0, h, t, j] = True
     ref = oracle.dense_attention(q, k, v, mask=mask)
     assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
+
+
+# ---------------------------------------------------------------- MoBA ----
+def moba_oracle(q, k, v, c, chunk):
+    """MoBAAttention.forward (selection.py:610-640) chunk by chunk: routing
+    over every key pushed so far at the chunk's offset, causal attention."""
+    T = q.shape[2]
+    outs = []
+    for s in range(0, T, chunk):
+        e = min(T, s + chunk)
+        ids = oracle.gate_select(q[:, :, s:e], k[:, :, :e], block=c.block_size,
+                                 topk=c.topk_blocks, offset=s)
+        outs.append(oracle.attend_lists(q[:, :, s:e], k[:, :, :e], v[:, :, :e], ids,
+                                        unit=c.block_size, causal=True, offset=s))
+    return np.concatenate(outs, axis=2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("hq,hkv,T", [(4, 2, 150), (8, 8, 97)])
+def test_gate_select_bit_exact(dev, dtype, hq, hkv, T):
+    """Routing lists equal the oracle's bit for bit, for a prefill (every
+    query, T not a multiple of the block) and for one decode query."""
+    from linattn_amd.kernels.routing import gate_select_hip
+
+    q, k, _ = inputs(2, hq, hkv, T, 64, seed=6)
+    q, k = q.to(dtype), k.to(dtype)
+    ids, counts = gate_select_hip(q.to(dev), k.to(dev), block=16, topk=3, offset=0)
+    ref = oracle.gate_select(q, k, block=16, topk=3, offset=0)
+    assert np.array_equal(ids.cpu().numpy(), ref)
+    assert np.array_equal(counts.cpu().numpy(), (ref >= 0).sum(-1))
+    ids1, _ = gate_select_hip(q[:, :, -1:].to(dev), k.to(dev), block=16, topk=4, offset=T - 1)
+    ref1 = oracle.gate_select(q[:, :, -1:], k, block=16, topk=4, offset=T - 1)
+    assert np.array_equal(ids1.cpu().numpy(), ref1)
+
+
+@pytest.mark.parametrize("chunk", [160, 48])
+def test_hip_moba_matches_oracle(dev, chunk):
+    c = cfg()
+    q, k, v = inputs(2, 4, 2, 160, 64, seed=7)
+    out, _, stats = build("hip_moba", c).forward(q.to(dev), k.to(dev), v.to(dev), chunk=chunk,
+                                                 collect_stats=True)
+    ref = moba_oracle(q, k, v, c, chunk)
+    assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
+    assert all(s["blocks_per_query"] <= c.topk_blocks + 1 for s in stats)
+
+
+def test_hip_moba_full_budget_recovers_dense(dev):
+    """test_budgets.py:64-81 for MoBA, float64 in and out."""
+    q, k, v = inputs(1, 4, 2, 160, 64, seed=8)
+    c = cfg(topk_blocks=160 // 16 + 2)
+    out, _ = build("hip_moba", c).forward(q.double().to(dev), k.double().to(dev),
+                                          v.double().to(dev), chunk=160)
+    assert np.abs(out.cpu().numpy() - oracle.dense_attention(q, k, v)).max() < 1e-5

@@ -16,8 +16,9 @@ from linattn_amd.registry import KERNEL_VARIANTS, build, describe_kernel
 
 def test_registry_names_and_errors():
     """registry.py:225-236: <backend>_<variant> names, KeyError otherwise."""
-    assert set(KERNEL_VARIANTS) == {"hip_quest", "hip_dsa", "hip_sliding_window",
+    assert set(KERNEL_VARIANTS) == {"hip_quest", "hip_dsa", "hip_moba", "hip_sliding_window",
                                     "hip_streaming_sink"}
+    assert describe_kernel("hip_moba")["reference"] == "moba"
     assert describe_kernel("hip_quest")["reference"] == "quest"
     assert build("hip_quest").name == "hip_quest"
     with pytest.raises(KeyError):

@@ -332,6 +332,48 @@ def test_block_select_structure_and_ranking():
             assert len(s) == len(set(top) | {0} | set(range(max(0, i - 1), i + 1)))
 
 
+# ------------------------------------------------- per-query routing ----
+def test_gate_select_ranking_bruteforce():
+    """MoBA gate routing (selection.py:610-640): lists hold only visible
+    blocks, always the own block, and otherwise exactly the top-k of an
+    independent gate computed by einsum over numpy block means (tail block
+    padded with the last row, core.py:115-117)."""
+    r = rng(13)
+    B, Hq, Hkv, T, D, bs, kk = 1, 4, 2, 90, 8, 16, 3  # T not a multiple of bs
+    q = r.standard_normal((B, Hq, T, D)).astype(np.float32)
+    k = r.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    ids = oracle.gate_select(q, k, block=bs, topk=kk, offset=0)
+    nkb = (T + bs - 1) // bs
+    kpad = np.concatenate([k, np.repeat(k[:, :, -1:], nkb * bs - T, axis=2)], axis=2)
+    kbar = kpad.astype(np.float64).reshape(B, Hkv, nkb, bs, D).mean(3)
+    gates = np.einsum("bhtd,bhjd->bhtj", q.astype(np.float64), np.repeat(kbar, Hq // Hkv, axis=1))
+    assert ids.shape == (B, Hq, T, kk + 1)
+    for h in range(Hq):
+        for t in range(T):
+            s = [x for x in ids[0, h, t].tolist() if x >= 0]
+            own = t // bs
+            assert s == sorted(set(s)) and max(s) == own and own in s
+            top = sorted(range(own + 1), key=lambda j: (-gates[0, h, t, j], j))[:kk]
+            assert set(s) == set(top) | {own}
+
+
+def test_gate_select_full_budget_recovers_dense():
+    """test_budgets.py:64-81 for MoBA: with every block routed the output is
+    dense causal attention; with an offset (decode) as well."""
+    r = rng(14)
+    B, Hq, Hkv, T, D, bs = 1, 4, 2, 40, 8, 8
+    q = torch.from_numpy(r.standard_normal((B, Hq, T, D)))
+    k = torch.from_numpy(r.standard_normal((B, Hkv, T, D))).float()
+    v = torch.from_numpy(r.standard_normal((B, Hkv, T, D))).float()
+    ids = oracle.gate_select(q, k, block=bs, topk=T // bs + 2, offset=0)
+    out = oracle.attend_lists(q, k, v, ids, unit=bs, causal=True, offset=0)
+    dense = oracle.dense_attention(q.numpy(), k.double().numpy(), v.double().numpy())
+    assert np.abs(out - dense).max() < 1e-12
+    ids1 = oracle.gate_select(q[:, :, -1:], k, block=bs, topk=T // bs + 2, offset=T - 1)
+    out1 = oracle.attend_lists(q[:, :, -1:], k, v, ids1, unit=bs, causal=True, offset=T - 1)
+    assert np.abs(out1 - dense[:, :, -1:]).max() < 1e-12
+
+
 # ----------------------------------------------------------------- fp8 ----
 def test_fp8_decode_matches_torch_for_all_codes():
     """The oracle's e4m3fn decoder (from the OCP spec) against torch's dtype,
