@@ -35,6 +35,49 @@ struct TopkKParams {
   const int32_t *cand_idx;
 };
 
+// The row (group) a workgroup selects for, its valid prefix and forced unit.
+struct TkRow {
+  int64_t br, seg0, tl, t, orow, n_v, own, K;
+  bool force;
+};
+
+__device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
+  TkRow r;
+  // Segmented mode: group gi handles segment gi % nseg of row gi / nseg.
+  r.br = p.seg_len > 0 ? gi / p.nseg : gi;
+  const int64_t seg = p.seg_len > 0 ? gi % p.nseg : 0;
+  r.seg0 = seg * p.seg_len;
+  r.tl = r.br % p.Tq;
+  r.t = r.tl + p.t_base;
+  r.orow = p.seg_len > 0 ? gi : (r.br / p.Tq) * p.out_tq + r.t;
+  int64_t n_v = p.n;
+  int64_t own = -1;
+  if (p.pos_unit > 0) {
+    const int64_t pos = p.pos_off + r.t;
+    const int64_t u = pos >= 0 ? pos / p.pos_unit : -1;
+    n_v = min(p.n, u + 1);
+    own = min(u, p.n - 1);
+  }
+  if (p.n_valid_tab) n_v = min(p.n, (int64_t)p.n_valid_tab[r.t]);
+  if (p.own_tab) own = (int64_t)p.own_tab[r.t];
+  if (p.seg_len > 0) n_v = min(n_v - r.seg0, min(p.seg_len, p.n - r.seg0));
+  r.n_v = max(n_v, (int64_t)0);
+  r.own = own;
+  r.force = p.force_own && own >= 0 && own < r.n_v;
+  r.K = min(p.k, r.n_v);
+  return r;
+}
+
+// Long plain rows split over several workgroups per row (topk_wide.hip):
+// C chunks per row, R rows per cooperative launch, workspace bytes (state of
+// one launch, then the candidate rows of a sorted selection).  C = 0 when the
+// device cannot hold one row's chunks at once.
+struct WidePlan {
+  int64_t C = 0, R = 0, state_bytes = 0, bytes = 0;
+};
+WidePlan wide_plan(const TopkKParams &p);
+int topk_wide_launch(const TopkKParams &p, const WidePlan &W, void *ws, hipStream_t st);
+
 // Workspace bytes topk_launch needs (rows longer than the LDS can hold are
 // selected in segments: candidates of each level are kept in the workspace).
 int64_t topk_workspace_bytes(const TopkKParams &p);

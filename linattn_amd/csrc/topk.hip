@@ -164,39 +164,6 @@ __device__ void tk_select(const RowKeys &key, int64_t n_v, int64_t K, TkShared &
   __syncthreads();
 }
 
-// The row (group) a workgroup selects for, its valid prefix and forced unit.
-struct TkRow {
-  int64_t br, seg0, tl, t, orow, n_v, own, K;
-  bool force;
-};
-
-__device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
-  TkRow r;
-  // Segmented mode: group gi handles segment gi % nseg of row gi / nseg.
-  r.br = p.seg_len > 0 ? gi / p.nseg : gi;
-  const int64_t seg = p.seg_len > 0 ? gi % p.nseg : 0;
-  r.seg0 = seg * p.seg_len;
-  r.tl = r.br % p.Tq;
-  r.t = r.tl + p.t_base;
-  r.orow = p.seg_len > 0 ? gi : (r.br / p.Tq) * p.out_tq + r.t;
-  int64_t n_v = p.n;
-  int64_t own = -1;
-  if (p.pos_unit > 0) {
-    const int64_t pos = p.pos_off + r.t;
-    const int64_t u = pos >= 0 ? pos / p.pos_unit : -1;
-    n_v = min(p.n, u + 1);
-    own = min(u, p.n - 1);
-  }
-  if (p.n_valid_tab) n_v = min(p.n, (int64_t)p.n_valid_tab[r.t]);
-  if (p.own_tab) own = (int64_t)p.own_tab[r.t];
-  if (p.seg_len > 0) n_v = min(n_v - r.seg0, min(p.seg_len, p.n - r.seg0));
-  r.n_v = max(n_v, (int64_t)0);
-  r.own = own;
-  r.force = p.force_own && own >= 0 && own < r.n_v;
-  r.K = min(p.k, r.n_v);
-  return r;
-}
-
 // the candidate row of a segmented top-k's final level (G = 1), or null
 __device__ __forceinline__ const int32_t *tk_cand_row(const TopkKParams &p, const TkRow &rw) {
   return p.cand_idx ? p.cand_idx + ((rw.br / p.Tq) * p.G * p.Tq + rw.tl) * p.row_stride + rw.seg0
@@ -788,15 +755,22 @@ static int64_t lds_limit() { return (int64_t)max_dynamic_lds() - (int64_t)sizeof
 // Long rows (keys + sort buffer beyond LDS) of a plain top-k are reduced in
 // segments that fit the LDS; each level keeps k per segment, in index order,
 // so the candidate rows of the final level are in ascending unit order.
-static LongPlan long_plan(const TopkKParams &p) {
-  LongPlan L;
-  // sorted (order 0) or index-order (order 1) rows of one head, no extras
+// Sorted (order 0) or index-order (order 1) rows of one head with no extras,
+// too long for one workgroup's LDS.
+static bool long_plain(const TopkKParams &p) {
   const bool plain = p.G == 1 && p.sink == 0 && p.window == 0 && (p.order == 0 || p.order == 1) &&
                      !p.force_own && !p.cand_idx && p.seg_len == 0;
   int64_t p2 = 1;
   while (p2 < p.k) p2 <<= 1;
+  return plain && p.n * 8 + p2 * 12 + 64 > lds_limit();
+}
+
+static LongPlan long_plan(const TopkKParams &p) {
+  LongPlan L;
+  int64_t p2 = 1;
+  while (p2 < p.k) p2 <<= 1;
   const int64_t limit = lds_limit();
-  if (!plain || p.n * 8 + p2 * 12 + 64 <= limit) return L;
+  if (!long_plain(p)) return L;
   int64_t seg = 1;
   while ((seg * 2) * 8 + (seg * 2) / 8 + 64 <= limit) seg *= 2;
   if (p.k * 2 > seg) return L;  // segments would not shrink the rows
@@ -817,11 +791,25 @@ static LongPlan long_plan(const TopkKParams &p) {
 }
 
 int64_t topk_workspace_bytes(const TopkKParams &p) {
+  if (long_plain(p)) {
+    const WidePlan W = wide_plan(p);
+    if (W.C > 0) return W.bytes;
+  }
   const LongPlan L = long_plan(p);
   return L.levels > 0 ? L.bytes : 0;
 }
 
 int topk_launch_ws(TopkKParams p, void *ws, int64_t ws_bytes, hipStream_t st) {
+  if (p.NG <= 0) return LA_OK;
+  if (long_plain(p)) {
+    const WidePlan W = wide_plan(p);
+    if (W.C > 0) {
+      if (!ws || ws_bytes < W.bytes)
+        return fail(LA_ERR_WORKSPACE, "topk: long rows need %lld workspace bytes",
+                    (long long)W.bytes);
+      return topk_wide_launch(p, W, ws, st);
+    }
+  }
   const LongPlan L = long_plan(p);
   if (L.levels <= 0) return topk_launch(p, st);
   if (!ws || ws_bytes < L.bytes)
