@@ -21,6 +21,8 @@
 // The waits need every workgroup of a row resident at once: the kernel is
 // launched cooperatively (the runtime refuses a grid that cannot be), rows
 // go in batches that fit, and every wait is bounded.
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "topk.h"
@@ -303,6 +305,10 @@ static int64_t wide_capacity() {
 
 WidePlan wide_plan(const TopkKParams &p) {
   WidePlan W;
+  // LA_TOPK_WIDE=0 keeps long rows on the segmented levels (kept for devices
+  // without cooperative launch, and tested against the same oracle)
+  const char *env = getenv("LA_TOPK_WIDE");
+  if (env && env[0] == '0') return W;
   const int64_t cap = wide_capacity();
   W.C = ceil_div(p.n, TW_CHUNK);
   if (cap <= 0 || W.C > cap || p.n >= ((int64_t)1 << 31)) {

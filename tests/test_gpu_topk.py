@@ -36,6 +36,24 @@ def test_topk_ties_and_prefixes(dev, n, k):
     assert np.array_equal(vals[0, 0].cpu().numpy(), rv.astype(np.float32))
 
 
+@pytest.mark.parametrize("order", [0, 1])
+def test_topk_long_rows_segmented_fallback(dev, monkeypatch, order):
+    """Long rows with the multi-workgroup kernel switched off (LA_TOPK_WIDE=0):
+    the segmented levels, the form used where a device cannot launch
+    cooperatively, give the same selection."""
+    n, k = 70000, 3000
+    g = torch.Generator().manual_seed(3)
+    sc = torch.randint(-3, 4, (1, 1, 2, n), generator=g).double()
+    sc[0, 0, 1] = torch.randn(n, generator=g, dtype=torch.float64)
+    ref_i, _ = oracle.topk_rows(sc[0, 0].numpy(), k)
+    monkeypatch.setenv("LA_TOPK_WIDE", "0")
+    ids, counts, _ = _topk(sc.to(dev), k=k, width=k, group=1, order=order, pos_offset=0,
+                           pos_unit=0, force_own=False, with_values=False)
+    got = ids[0, 0].cpu().numpy()
+    want = ref_i if order == 0 else np.sort(ref_i, axis=-1)
+    assert np.array_equal(got, want)
+
+
 def test_topk_short_rows_pad(dev):
     sc = torch.randn(1, 2, 5, 300, dtype=torch.float64)
     ids, vals = run(sc.to(dev), 64, pos_offset=0, pos_unit=8)  # t visible units: t//8 + 1
