@@ -15,6 +15,7 @@
 // Math: fp32 online softmax in the log2 domain (q is pre-scaled by
 // scale*log2(e)); exp2 is the hardware v_exp_f32.
 #include <algorithm>
+#include <cstdlib>
 
 #include "common.h"
 #include "kv_access.h"
@@ -377,6 +378,14 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Per-lane scales of the fp8 matrix-core kernel (empty for bf16 K/V).
+template <bool F8>
+struct Fp8Scales {
+  float k = 0.f, v[4] = {0.f, 0.f, 0.f, 0.f};
+};
+template <>
+struct Fp8Scales<false> {};
+
 // Maximum over the 16 lanes of a DPP row; every lane of the row gets it.
 __device__ __forceinline__ float row_max16(float x) {
   x = fmaxf(x, dpp_f32<0xB1>(x));
@@ -397,8 +406,20 @@ __device__ __forceinline__ float row_max16(float x) {
 // it and merge by plain sums.  Probabilities pass through LDS to the PV
 // lanes, which read V rows 16 contiguous bytes per lane (a token per 16
 // lanes) and accumulate O on the VALU in fp32.
-template <int G, bool PAGED, bool U16>
+//
+// fp8 e4m3 K/V with per-token scales (KT = LA_FP8_E4M3): the scores come from
+// v_mfma_f32_16x16x32_fp8_fp8 on the K codes as stored.  q is quantised in
+// the kernel to a two-term fp8 expansion, q ~ sq * (hi + lo), with one scale
+// sq = absmax/448 over the G heads and lo = fp8(q/sq - hi) (the residual, in
+// the same code units, down to the e4m3 subnormal step 2^-9), so
+// S = ks_t * sq * (hi + lo).K is eight fp8 MFMAs into one accumulator per
+// round and keeps q to ~2^-8 relative; the per-token K scale multiplies the
+// fp32 scores, and each V row is decoded in registers with its scale folded
+// into the token's weight.
+template <int KT, int G, bool PAGED, bool U16>
 __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel(AttnKP p) {
+  constexpr bool F8 = KT == LA_FP8_E4M3;
+  constexpr int ESZ = F8 ? 1 : 2;  // bytes per K/V element
   constexpr int D = 128;
   constexpr int RT = 16;            // tokens per wave round
   constexpr int NRG = (G + 3) / 4;  // DPP rows holding heads
@@ -409,6 +430,8 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
   __shared__ float s_acc[SA_NW][G][D];
   __shared__ float s_m[SA_NW][G], s_l[SA_NW][G];
   __shared__ __align__(16) float s_p[SA_NW][RT][4 * NRG];
+  __shared__ long s_q8[F8 ? 2 * 4 * 64 : 1];  // fp8: [term][s][lane] q codes
+  __shared__ float s_sq;                      // fp8: their scale
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = lane & 15;     // V: 8-dim chunk; K: token of the round
@@ -416,9 +439,11 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
   const RowCtx rc = stage_row<G, PAGED>(p, s_tok0, s_phys);
   const int32_t lim32 = (int32_t)min(rc.lim, (int64_t)0x7fffffff);
 
-  // A operand: q row c (head c < G), dims 32s + 8*slot .. +8, raw bf16 bits.
+  // A operand: q row c (head c < G), dims 32s + 8*slot .. +8, raw bf16 bits
+  // (fp8: dims 32*slot + 8s .. +8 of the hi and lo codes, the same dims as
+  // the K bytes the lane feeds to MFMA s).
   bf16x8 qa[4];
-  {
+  if constexpr (!F8) {
     const uint16_t *qp = (const uint16_t *)p.q;
     const int64_t qo = rc.b * p.q_sb + (rc.h0 + c) * p.q_sh + rc.t * p.q_st + 8 * slot;
 #pragma unroll
@@ -428,6 +453,43 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
       for (int e = 0; e < 8; ++e) x[e] = c < G ? qp[qo + 32 * s + e] : (uint16_t)0;
       qa[s] = __builtin_bit_cast(bf16x8, x);
     }
+  } else if (w == 0) {  // fp8: wave 0 writes the codes for the workgroup
+    const uint16_t *qp = (const uint16_t *)p.q;
+    const int64_t qo = rc.b * p.q_sb + (rc.h0 + c) * p.q_sh + rc.t * p.q_st + 32 * slot;
+    float x[32];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      x[i] = c < G ? bf16_bits_to_f32(qp[qo + i]) : 0.f;
+      amax = fmaxf(amax, fabsf(x[i]));
+    }
+    // absmax over the wave: the 4 lanes of a head, then the 16 heads
+    const float am = row_max16(pair32_max(pair16_max(amax)));
+    const float sq = am > 0.f ? am / 448.f : 1.f;
+    if (lane == 0) s_sq = sq;
+    const float inv = 1.f / sq;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) x[i] *= inv;
+    // codes of x by round to nearest; x keeps the residual
+    auto term = [&](int tm) {
+      uint32_t wd[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int wv = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * j], x[4 * j + 1], 0, false);
+        wv = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * j + 2], x[4 * j + 3], wv, true);
+        wd[j] = (uint32_t)wv;
+        const float2 a = fp8x2_to_f32<false>(wd[j]), b = fp8x2_to_f32<true>(wd[j]);
+        x[4 * j] -= a.x;
+        x[4 * j + 1] -= a.y;
+        x[4 * j + 2] -= b.x;
+        x[4 * j + 3] -= b.y;
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        s_q8[(tm * 4 + s) * 64 + lane] = (long)(((uint64_t)wd[2 * s + 1] << 32) | (uint64_t)wd[2 * s]);
+    };
+    term(0);
+    term(1);
   }
   float ms[4], ls[4];  // per DPP row: max and partial sums of heads 4*slot + e
   float acc[G][8];
@@ -449,7 +511,9 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
   // One set of K/V registers, refilled as it is consumed: the next round's K
   // loads are issued once the current K is in the matrix core, and each V
   // row of the next round once the current one has been accumulated.
-  uint4 kr[4], vr[4];
+  uint4 kr[F8 ? 2 : 4];
+  typename KvTraits<KT>::Vec vr[4];
+  Fp8Scales<F8> f8s;  // fp8: scales of this lane's K / V tokens
   bool kok = false;
   // U16 (units of 16k tokens lying inside one page): the 16 tokens of a round
   // are consecutive rows of one entry, so the entry lookup is wave-uniform and
@@ -488,34 +552,61 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
   // pool page, so every row address is valid; a round with nothing to attend
   // reads the first rows of the pool instead.  Tokens that are not attended
   // have their K columns masked and their V rows zeroed after the load.
-  const uint32_t koff = (uint32_t)((c * D + 8 * slot) * 2);
-  const uint32_t voff = (uint32_t)((slot * D + 8 * c) * 2);
+  // K: bf16, dims 32s + 8*slot (four 16-byte loads); fp8, dims 32*slot ..
+  // +32 (two).  V: dims 8c .. +8 of token slot (+4u) of the round.
+  const uint32_t koff = (uint32_t)((c * D + (F8 ? 32 : 8) * slot) * ESZ);
+  const uint32_t voff = (uint32_t)((slot * D + 8 * c) * ESZ);
+  using VVec = typename KvTraits<KT>::Vec;
+  uint32_t prow_k = 0xffffffffu;  // paged token lists: pool row of this lane's K token (~0: none)
   auto load_k = [&](int32_t base) {
     if constexpr (U16) {
       rd_next = round_of(base);
       kok = rd_next.tok >= 0 && rd_next.tok + c <= lim32;
-      const char *rp = rd_next.tok >= 0 ? kbase + rd_next.kb * 2 : kbase;  // wave-uniform
+      const char *rp = rd_next.tok >= 0 ? kbase + rd_next.kb * ESZ : kbase;  // wave-uniform
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kr[s] = *(const uint4 *)(rp + koff + 64 * s);
+      for (int s = 0; s < (F8 ? 2 : 4); ++s) kr[s] = *(const uint4 *)(rp + koff + 16 * (F8 ? 1 : 4) * s);
+      if constexpr (F8) f8s.k = p.kv.k_scale[(rd_next.tok >= 0 ? rd_next.kb / D : 0) + c];
     } else {
       int64_t ko = 0, vo = 0, so = 0;
       kok = token_rows<D, PAGED>(p, rc, s_tok0, s_phys, base + w * RT + c, F, lim32, ko, vo, so);
+      if constexpr (PAGED) prow_k = kok ? (uint32_t)so : 0xffffffffu;
+      if constexpr (F8) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        kr[s] = kok ? *(const uint4 *)(kbase + (ko + 32 * s + 8 * slot) * 2) : uint4{0, 0, 0, 0};
+        for (int s = 0; s < 2; ++s)
+          kr[s] = kok ? *(const uint4 *)(kbase + ko + 32 * slot + 16 * s) : uint4{0, 0, 0, 0};
+        f8s.k = kok ? p.kv.k_scale[so] : 0.f;
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          kr[s] = kok ? *(const uint4 *)(kbase + (ko + 32 * s + 8 * slot) * 2) : uint4{0, 0, 0, 0};
+      }
     }
   };
   auto load_v = [&](int32_t base, int u) {
     if constexpr (U16) {
       const bool ok = rd_next.tok >= 0 && rd_next.tok + 4 * u + slot <= lim32;
-      const char *rp = rd_next.tok >= 0 ? vbase + rd_next.vb * 2 : vbase;  // wave-uniform
-      const uint4 x = *(const uint4 *)(rp + voff + 4 * u * D * 2);
-      vr[u] = ok ? x : uint4{0, 0, 0, 0};
+      const char *rp = rd_next.tok >= 0 ? vbase + rd_next.vb * ESZ : vbase;  // wave-uniform
+      const VVec x = *(const VVec *)(rp + voff + 4 * u * D * ESZ);
+      if constexpr (F8) vr[u] = ok ? x : uint2{0, 0}; else vr[u] = ok ? x : uint4{0, 0, 0, 0};
+      if constexpr (F8) {
+        const float sv = p.kv.v_scale[(rd_next.tok >= 0 ? rd_next.vb / D : 0) + 4 * u + slot];
+        f8s.v[u] = ok ? sv : 0.f;
+      }
     } else {
       int64_t ko = 0, vo = 0, so = 0;
-      const bool ok =
-          token_rows<D, PAGED>(p, rc, s_tok0, s_phys, base + w * RT + 4 * u + slot, F, lim32, ko, vo, so);
-      vr[u] = ok ? *(const uint4 *)(vbase + (vo + 8 * c) * 2) : uint4{0, 0, 0, 0};
+      bool ok;
+      if constexpr (PAGED) {
+        // a paged K and V row share the pool row, which the round's K load
+        // (issued first) resolved on lane 4u + slot
+        const uint32_t pr = (uint32_t)__shfl((int)prow_k, 4 * u + slot, 64);
+        ok = pr != 0xffffffffu;
+        vo = (int64_t)pr * D;
+        so = pr;
+      } else {
+        ok = token_rows<D, PAGED>(p, rc, s_tok0, s_phys, base + w * RT + 4 * u + slot, F, lim32, ko, vo, so);
+      }
+      if constexpr (F8) vr[u] = ok ? *(const VVec *)(vbase + (vo + 8 * c) * ESZ) : uint2{0, 0}; else vr[u] = ok ? *(const VVec *)(vbase + (vo + 8 * c) * ESZ) : uint4{0, 0, 0, 0};
+      if constexpr (F8) f8s.v[u] = ok ? p.kv.v_scale[so] : 0.f;
     }
   };
   if (F > 0) {
@@ -526,9 +617,22 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
   for (int32_t base = 0; base < F; base += STEP) {
     const bool more = base + STEP < F;
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+    float kq = p.qscale;  // fp8: times the q scale and the K scale of this lane's token
+    if constexpr (F8) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], __builtin_bit_cast(bf16x8, kr[s]), sacc, 0, 0, 0);
+      for (int s = 0; s < 4; ++s) {
+        const uint4 &kk = kr[s >> 1];
+        const long kb8 = (s & 1) ? (long)(((uint64_t)kk.w << 32) | kk.z)
+                                 : (long)(((uint64_t)kk.y << 32) | kk.x);
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(s_q8[s * 64 + lane], kb8, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(s_q8[(4 + s) * 64 + lane], kb8, sacc, 0, 0, 0);
+      }
+      kq *= s_sq * f8s.k;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], __builtin_bit_cast(bf16x8, kr[s]), sacc, 0, 0, 0);
+    }
     const bool cur_ok = kok;
     if (U16 || more) load_k(base + STEP);
     __builtin_amdgcn_sched_barrier(0);
@@ -536,7 +640,8 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
     bool grow = false;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      sv[e] = cur_ok ? sacc[e] * p.qscale : __int_as_float(0xff800000);
+      const float raw = sacc[e];
+      sv[e] = cur_ok ? raw * kq : __int_as_float(0xff800000);
       mn[e] = fmaxf(ms[e], row_max16(sv[e]));
       grow = grow || (slot < NRG && mn[e] - ms[e] > 8.f);
     }
@@ -579,7 +684,11 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
         pg[4 * x + 3] = v4.w;
       }
       float vf[8];
-      unpack<LA_BF16, 8>(vr[u], vf);
+      unpack<KT, 8>(vr[u], vf);
+      if constexpr (F8) {
+#pragma unroll
+        for (int g = 0; g < 4 * NRG; ++g) pg[g] *= f8s.v[u];
+      }
       if (U16 || more) load_v(base + STEP, u);
       // keep each refill after the use of the registers it replaces
       __builtin_amdgcn_sched_barrier(0);
@@ -643,6 +752,17 @@ __global__ __launch_bounds__(256) void sparse_attn_combine(AttnKP p, int64_t G, 
   }
 }
 
+// bf16 or fp8 K/V with bf16 q and head dim 128 take the matrix-core kernel.
+// LA_FP8_MFMA=0 keeps fp8 K/V on the VALU kernel (fp32 dequantised scores).
+static bool mfma_path(int kt, int64_t d, int q_dt) {
+  static const bool fp8_mfma = [] {
+    const char *e = getenv("LA_FP8_MFMA");
+    return !(e && e[0] == '0');
+  }();
+  if (d != 128 || q_dt != LA_BF16) return false;
+  return kt == LA_BF16 || (kt == LA_FP8_E4M3 && fp8_mfma);
+}
+
 // Tokens per row slot per batch; two batches are in flight per wave.
 template <int KT>
 constexpr int unroll_for(int D) {
@@ -655,10 +775,10 @@ static int launch_attn(const AttnKP &p, hipStream_t st) {
   dim3 grid((unsigned)p.splits, (unsigned)(p.B * p.ids_heads * p.Tq));
   // U16: paged, and every 16-row round lies inside one entry of one page
   const bool u16 = PAGED && p.staged && p.unit % 16 == 0;
-  if (KT == LA_BF16 && D == 128 && p.q_dt == LA_BF16 && u16)
-    sparse_attn_mfma_kernel<G, PAGED, true><<<grid, SA_NT, 0, st>>>(p);
-  else if (KT == LA_BF16 && D == 128 && p.q_dt == LA_BF16)
-    sparse_attn_mfma_kernel<G, PAGED, false><<<grid, SA_NT, 0, st>>>(p);
+  if (mfma_path(KT, D, p.q_dt) && u16)
+    sparse_attn_mfma_kernel<KT == LA_F32 ? LA_BF16 : KT, G, PAGED, true><<<grid, SA_NT, 0, st>>>(p);
+  else if (mfma_path(KT, D, p.q_dt))
+    sparse_attn_mfma_kernel<KT == LA_F32 ? LA_BF16 : KT, G, PAGED, false><<<grid, SA_NT, 0, st>>>(p);
   else
     sparse_attn_kernel<KT, D, G, UNR, PAGED><<<grid, SA_NT, 0, st>>>(p);
   LA_LAUNCHED();
@@ -737,7 +857,7 @@ static int plan_attn(const la_sparse_attn_args *a, const la_kv *kv, Plan &pl) {
   if (splits <= 0) {
     // workgroups to aim for: the matrix-core kernel keeps 4 resident per CU
     // (so one full wave of workgroups), the VALU kernel 8 per CU
-    const bool mfma = kv->dtype == LA_BF16 && a->q_dtype == LA_BF16 && a->D == 128;
+    const bool mfma = mfma_path(kv->dtype, a->D, a->q_dtype);
     const int64_t target = (int64_t)num_cus() * (mfma ? 4 : 8);
     const int64_t tokens = a->N * a->unit;
     const int64_t by_tokens = std::max<int64_t>(1, tokens / 256);

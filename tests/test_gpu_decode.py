@@ -252,6 +252,33 @@ def test_sparse_attention_fp8(dev, paged):
     assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-2
 
 
+@pytest.mark.parametrize("unit,causal", [(16, False), (64, True)])
+def test_sparse_attention_fp8_page_lists(dev, unit, causal):
+    """fp8 page lists on the paged pool (the matrix-core kernel's rounds of 16
+    rows inside one page), GQA groups of 4 and of 1, causal cut mid-page."""
+    q, k, v = make_inputs(2, 8, 2, 1, 1024, 128, seed=15)
+    kc, ks = oracle.fp8_quantize(k)
+    vc, vs = oracle.fp8_quantize(v)
+    ks, vs = ks.squeeze(-1), vs.squeeze(-1)
+    n_units = 1024 // unit
+    pk, pv, pt = to_pool(kc.view(torch.uint8), vc.view(torch.uint8), 64)
+    psk, psv, _ = to_pool(ks.unsqueeze(-1), vs.unsqueeze(-1), 64)
+    kw = dict(unit=unit, page_table=pt.to(dev), page_size=64,
+              k_scale=psk.squeeze(-1).contiguous().to(dev),
+              v_scale=psv.squeeze(-1).contiguous().to(dev), out_dtype=torch.float32)
+    off = 1000 if causal else 0
+    qb = q.bfloat16()
+    for heads in (2, 8):  # one list per KV head (G = 4) or per query head (G = 1)
+        ids = _lists(2, heads, 1, n_units // 3, n_units, seed=16 + heads)
+        out = sparse_attention(qb.to(dev), pk.view(torch.float8_e4m3fn).to(dev),
+                               pv.view(torch.float8_e4m3fn).to(dev), ids.to(dev), causal=causal,
+                               offset=off, **kw)
+        ref = oracle.attend_lists(qb, kc, vc, ids.numpy(), unit=unit, causal=causal, offset=off,
+                                  k_scale=ks, v_scale=vs)
+        # fp8 MFMA scores with q as a two-term fp8 expansion (~2^-8 relative)
+        assert np.abs(out.cpu().double().numpy() - ref).max() < 2e-3, heads
+
+
 def test_paged_pool_equals_contiguous(dev):
     q, k, v = make_inputs(2, 32, 8, 1, 1024, 128, seed=15)
     q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
