@@ -290,6 +290,37 @@ def bench_moba(dev, steps, warmup):
             "attend_bytes": att_bytes}
 
 
+def bench_xattn(dev, steps, warmup):
+    """XAttention block selection (selection.py:528-595) at its defaults
+    (8-token blocks, antidiagonal stride 8, threshold 0.9): B=1, T=8192,
+    32/8 heads, D=128, bf16 prefill.  Every (query block, visible key block)
+    pair costs 8 antidiagonal dot products of D (fp64, exact)."""
+    import torch
+
+    from linattn_amd.kernels.routing import xattn_select_hip
+
+    B, Hq, Hkv, T, D, blk, r = 1, 32, 8, 8192, 128, 8, 8
+    g = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn(B, Hq, T, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, T, D, generator=g, device=dev).to(torch.bfloat16)
+
+    def sel():
+        return xattn_select_hip(q, k, block=blk, stride=r, threshold=0.9)
+
+    ids, counts = sel()
+    ms = time_cuda(sel, steps, warmup)
+    n_qb = T // blk
+    pairs = B * Hq * n_qb * (n_qb + 1) // 2
+    entries = sum(min(blk - 1, o) - max(0, o - blk + 1) + 1 for o in range(0, 2 * blk - 1, r))
+    tflops = pairs * entries * D * 2 / (ms * 1e-3) / 1e12
+    return {"workload": "XAttention selection, B=1, T=8192, 32/8 heads, D=128, bf16, "
+                        "block 8, stride 8, threshold 0.9",
+            "ms_select": round(ms, 4), "blocks_per_row": round(float(counts.float().mean()), 2),
+            "frac_causal_blocks_kept": round(int(counts.sum()) / pairs, 4),
+            "score_tflops_fp64": round(tflops, 2),
+            "frac_fp64_valu_peak": round(tflops / FP64_VALU_PEAK_TFLOPS, 4)}
+
+
 def _counter_rows(d):
     import csv
     import glob
@@ -462,6 +493,7 @@ def main() -> int:
     result["prefill"] = bench_c3(dev, max(3, args.steps // 4), 2)
     result["fp8_decode"] = bench_c5(dev, max(3, args.steps // 4), 2)
     result["moba_decode"] = bench_moba(dev, max(3, args.steps // 4), 2)
+    result["xattn_select"] = bench_xattn(dev, max(3, args.steps // 10), 2)
     result["serving"] = bench_serving(dev, q, pool_k, pool_v, pt, mins, maxs, cfg,
                                       max(3, args.steps // 4), 2)
     if not args.no_cpu_baseline:

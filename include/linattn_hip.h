@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 4
+#define LA_ABI_VERSION 5
 
 /* element types */
 enum {
@@ -391,6 +391,49 @@ typedef struct {
 
 size_t la_gate_select_workspace(const la_gate_select_args *a);
 int la_gate_select(const la_gate_select_args *a, void *stream);
+
+/*
+ * XAttention block selection: XAttention.antidiagonal_scores / select
+ * (variants/selection.py:528-595).  Replaces the torch selection path of that
+ * variant (no kernel backend exists for it in the reference).  Blocks of
+ * `block` tokens; query block qb of (b, h) (rows past Tq are zero rows, F.pad
+ * at :544) against key block kb of KV head h / (Hq/Hkv) (rows past T zero);
+ * visible when kb*block <= qb*block + offset (:573-575).  Slot s, for
+ * antidiagonal offset o = s*stride <= 2*block - 2 (:554), is the sum over
+ * i = max(0, o-block+1) .. min(block-1, o), increasing, of the fp64 dot
+ * product q[qb*block + i] . k[kb*block + o - i] (d increasing), times
+ * inv_sqrt_d (the caller's fl(1/fl(sqrt(D))), :566).  Per row: weights
+ * exp(slot - max) over the visible slots (a fixed fma sequence, bit-identical
+ * in the CPU oracle), as integers rint(w * 2^F), F = 52 - ceil(log2(n_kb *
+ * n_slots)); block mass = the sum over its slots (:576-579, unnormalised).
+ *   mode 0 (threshold, _cumulative_select :62-69 / per-head thresholds
+ *     :587-589): with blocks ordered by (mass desc, index asc), keep
+ *     1 + #{m : C_m < ceil(alpha[h] * Z)} blocks (C_m the sum of the first m
+ *     masses, Z the total; alpha[h] * Z > Z keeps all);
+ *   mode 1 (top-k, :581-582): the top min(topk, n_kb) blocks in that order.
+ * The own block (first token qb*block + offset) is OR'd in and blocks past
+ * causality are dropped (:591-592).  Output: out_idx[((b*Hq + h)*n_qb + qb)
+ * *width + i] ascending, -1 padded, width >= n_kb (mode 0) or
+ * min(topk, n_kb) + 1 (mode 1); out_count[(b*Hq + h)*n_qb + qb].  Limits:
+ * block <= 64, n_kb <= 4096, LDS block*D*4 + n_kb*n_slots*8 <= 120 KiB.
+ * No workspace.
+ */
+typedef struct {
+  const void *q;
+  const void *k;
+  int32_t *out_idx;
+  int32_t *out_count;
+  const double *alpha; /* device, Hq thresholds (mode 0) */
+  int64_t B, Hq, Hkv, Tq, T, D;
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  int64_t block, stride, offset, topk, width;
+  double inv_sqrt_d;
+  int32_t mode;
+  int32_t in_dtype;
+} la_xattn_select_args;
+
+int la_xattn_select(const la_xattn_select_args *a, void *stream);
 
 /*
  * Block-sparse causal prefill on the matrix cores (MFMA bf16, fp32 accumulate).

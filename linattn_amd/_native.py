@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -39,6 +39,7 @@ EXPORTED = (
     "la_paged_kv_append",
     "la_gate_select_workspace",
     "la_gate_select",
+    "la_xattn_select",
 )
 
 _vp = ctypes.c_void_p
@@ -119,6 +120,15 @@ class LaGateSelectArgs(ctypes.Structure):
                 ("offset", _i64), ("width", _i64), ("in_dtype", _i32), ("reserved", _i32)]
 
 
+class LaXattnSelectArgs(ctypes.Structure):
+    _fields_ = [("q", _vp), ("k", _vp), ("out_idx", _vp), ("out_count", _vp), ("alpha", _vp),
+                ("B", _i64), ("Hq", _i64), ("Hkv", _i64), ("Tq", _i64), ("T", _i64), ("D", _i64),
+                ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64), ("k_sb", _i64), ("k_sh", _i64),
+                ("k_st", _i64), ("block", _i64), ("stride", _i64), ("offset", _i64),
+                ("topk", _i64), ("width", _i64), ("inv_sqrt_d", ctypes.c_double),
+                ("mode", _i32), ("in_dtype", _i32)]
+
+
 class LaPrefillArgs(ctypes.Structure):
     _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp), ("ids", _vp), ("counts", _vp),
                 ("B", _i64), ("Hq", _i64), ("Hkv", _i64), ("T", _i64), ("D", _i64),
@@ -170,6 +180,8 @@ def load() -> ctypes.CDLL:
     L.la_gate_select_workspace.argtypes = [P(LaGateSelectArgs)]
     L.la_gate_select_workspace.restype = ctypes.c_size_t
     L.la_gate_select.argtypes = [P(LaGateSelectArgs), _vp]
+    L.la_xattn_select.argtypes = [P(LaXattnSelectArgs), _vp]
+    L.la_xattn_select.restype = ctypes.c_int
     for name in EXPORTED:
         fn = getattr(L, name)
         if fn.restype is None or fn.restype is ctypes.c_int:

@@ -1,0 +1,358 @@
+// XAttention block selection on gfx950 (variants/selection.py:500-595).
+//
+// One workgroup per (b, query head h, query block qb) row.  The row's query
+// block (blk rows, zero past Tq) is staged in LDS as fp32 (exact for the
+// input types); every visible key block kb (kb*blk <= qb*blk + offset) gets
+// the strided antidiagonal scores of selection.py:528-566: slot s (offset
+// o = s*r, o <= 2*blk - 2) sums the entries (i, o - i) of the (query block,
+// key block) gram matrix, key rows past T counting as zero rows (F.pad).
+// Arithmetic is fixed so that the CPU oracle reproduces every bit:
+//   entry  = sum_d q[i][d] * k[j][d] in fp64, d increasing (exact products);
+//   slot   = entries added in increasing i, then times inv_sqrt_d (a host
+//            constant, fl(1/fl(sqrt(D))));
+//   weight = exp_det(slot - row max) (below), as a fixed-point integer
+//            rint(weight * 2^F), F = 52 - ceil(log2(n_kb * n_slots)), so that
+//            block masses (the sum over a block's slots) and their totals are
+//            exact integer sums below 2^53 in any order;
+//   threshold mode (the paper's rule, _cumulative_select, selection.py:62-69):
+//            with blocks ordered by (mass desc, index asc) and C_m the sum of
+//            the first m masses, keep n = 1 + #{m : C_m < ceil(alpha * Z)}
+//            blocks (Z the row's total; alpha * Z > Z keeps every block);
+//            found without a sort by a bitwise search for the largest mass
+//            value v with sum(mass >= v) >= thr, then every block above v and
+//            the first 1 + (thr - 1 - sum(mass > v)) / v blocks equal to v;
+//   top-k mode: the top min(topk, n_kb) blocks by (mass desc, index asc).
+// The own block (first token at qb*blk + offset) is OR'd in and the blocks
+// past causality dropped (selection.py:591-592); the list is written in
+// ascending order.
+#include <algorithm>
+#include <cmath>
+
+#include "common.h"
+#include "topk_select.h"
+
+#pragma clang fp contract(off)
+
+namespace la {
+
+__host__ __device__ constexpr int64_t xa_align16(int64_t x) { return (x + 15) & ~(int64_t)15; }
+
+// exp(x) for x <= 0 with a fixed sequence of correctly rounded operations
+// (the CPU oracle runs the same sequence): 0 below -700; x = k*ln2 + r by a
+// two-part ln2 (the fdlibm split) with fused multiply-adds; e^r by its
+// degree-13 Taylor polynomial in Horner form (fma); times 2^k from exponent
+// bits (exact, 2^k is normal for x > -700).
+__device__ __forceinline__ double exp_det(double x) {
+  if (!(x > -700.0)) return 0.0;
+  const double kf = __builtin_rint(x * 1.4426950408889634);
+  double r = __builtin_fma(-kf, 6.93147180369123816490e-01, x);
+  r = __builtin_fma(-kf, 1.90821492927058770002e-10, r);
+  double p = 1.6059043836821613e-10;
+  p = __builtin_fma(p, r, 2.08767569878681e-09);
+  p = __builtin_fma(p, r, 2.505210838544172e-08);
+  p = __builtin_fma(p, r, 2.755731922398589e-07);
+  p = __builtin_fma(p, r, 2.7557319223985893e-06);
+  p = __builtin_fma(p, r, 2.48015873015873e-05);
+  p = __builtin_fma(p, r, 0.0001984126984126984);
+  p = __builtin_fma(p, r, 0.001388888888888889);
+  p = __builtin_fma(p, r, 0.008333333333333333);
+  p = __builtin_fma(p, r, 0.041666666666666664);
+  p = __builtin_fma(p, r, 0.16666666666666666);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const double two_k = __longlong_as_double((long long)((int64_t)kf + 1023) << 52);
+  return p * two_k;
+}
+
+struct XaKP {
+  const void *q, *k;
+  int32_t *out_idx, *out_count;
+  const double *alpha;  // per query head (threshold mode)
+  int64_t B, Hq, Hkv, Tq, T, D;
+  int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st;
+  int64_t blk, r, n_slots, offset, n_qb, n_kb, topk, width;
+  double inv_sqrt_d, two_f;
+  int32_t in_dt, mode;  // mode 0: threshold, 1: top-k
+};
+
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t *red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += (uint64_t)__shfl_xor((unsigned long long)v, off, 64);
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int x = 0; x < TK_NW; ++x) t += red[x];
+  __syncthreads();
+  return t;
+}
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t *red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = (uint64_t)__shfl_xor((unsigned long long)v, off, 64);
+    v = o > v ? o : v;
+  }
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int x = 0; x < TK_NW; ++x) t = red[x] > t ? red[x] : t;
+  __syncthreads();
+  return t;
+}
+
+template <int KPT>
+__global__ __launch_bounds__(TK_NT) void xattn_select_kernel(XaKP p) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ TkRegShared<KPT> sh;
+  __shared__ uint64_t red[TK_NW];
+  __shared__ double redd[TK_NW];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t row = blockIdx.x;  // (b, h, qb)
+  const int64_t qb = row % p.n_qb;
+  const int64_t h = (row / p.n_qb) % p.Hq;
+  const int64_t b = row / (p.n_qb * p.Hq);
+  const int64_t kvh = h / (p.Hq / p.Hkv);
+  const int64_t blk = p.blk, D = p.D, NS = p.n_slots, n_kb = p.n_kb;
+
+  float *sq = (float *)dyn;                       // [blk][D]
+  double *ss = (double *)(dyn + xa_align16(blk * D * 4));  // [n_kb][NS]
+  uint32_t *bm = (uint32_t *)(ss + n_kb * NS);    // bitmap of kept blocks
+
+  for (int64_t x = tid; x < blk * D; x += TK_NT) {
+    const int64_t i = x / D, d = x % D, t = qb * blk + i;
+    sq[x] = t < p.Tq ? load_as_f32(p.q, b * p.q_sb + h * p.q_sh + t * p.q_st + d, p.in_dt) : 0.f;
+  }
+  for (int64_t x = tid; x < (n_kb + 31) / 32; x += TK_NT) bm[x] = 0u;
+  __syncthreads();
+
+  // visible key blocks: kb*blk <= qb*blk + offset
+  const int64_t pos0 = qb * blk + p.offset;
+  const int64_t lim = min(pos0 / blk, n_kb - 1);
+  const int64_t n_vis = lim + 1;
+  const int64_t kbase = b * p.k_sb + kvh * p.k_sh;
+
+  // slot scores of the visible blocks, one block per thread
+  for (int64_t kb = tid; kb < n_vis; kb += TK_NT) {
+    for (int64_t s = 0; s < NS; ++s) {
+      const int64_t o = s * p.r;
+      double acc = 0.0;
+      for (int64_t i = max((int64_t)0, o - blk + 1); i <= min(blk - 1, o); ++i) {
+        const int64_t j = o - i, kr = kb * blk + j;
+        const float *qi = sq + i * D;
+        double e = 0.0;
+        if (kr < p.T) {
+          const int64_t ko = kbase + kr * p.k_st;
+          if (p.in_dt == LA_BF16) {
+            const uint16_t *kp = (const uint16_t *)p.k + ko;
+            for (int64_t d = 0; d < D; d += 8) {
+              const uint4 v = *(const uint4 *)(kp + d);
+              const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                e = __builtin_fma((double)qi[d + 2 * u], (double)bf16lo(wv[u]), e);
+                e = __builtin_fma((double)qi[d + 2 * u + 1], (double)bf16hi(wv[u]), e);
+              }
+            }
+          } else {
+            for (int64_t d = 0; d < D; ++d)
+              e = __builtin_fma((double)qi[d], (double)load_as_f32(p.k, ko + d, p.in_dt), e);
+          }
+        } else {
+          // a zero key row (F.pad): the same operations on zeros
+          for (int64_t d = 0; d < D; ++d) e = __builtin_fma((double)qi[d], 0.0, e);
+        }
+        acc = acc + e;
+      }
+      ss[kb * NS + s] = acc * p.inv_sqrt_d;
+    }
+  }
+  __syncthreads();
+
+  // row maximum over the visible slots (exact, any order)
+  double mx = __int_as_float(0xff800000);
+  for (int64_t x = tid; x < n_vis * NS; x += TK_NT) mx = fmax(mx, ss[x]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmax(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) redd[w] = mx;
+  __syncthreads();
+  mx = redd[0];
+#pragma unroll
+  for (int x = 1; x < TK_NW; ++x) mx = fmax(mx, redd[x]);
+
+  // fixed-point block masses, kept in registers (block tid + 256 j)
+  uint64_t u[KPT];
+  uint64_t zpart = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int64_t kb = tid + TK_NT * j;
+    uint64_t m = 0;
+    if (kb < n_vis) {
+      for (int64_t s = 0; s < NS; ++s) {
+        const double e = exp_det(ss[kb * NS + s] - mx);
+        m += (uint64_t)__builtin_rint(e * p.two_f);
+      }
+    }
+    u[j] = m;
+    zpart += m;
+  }
+  const uint64_t Z = block_sum_u64(zpart, red);
+
+  const uint64_t lt = lanemask_lt(lane);
+  auto keep = [&](int64_t kb) {
+    if (kb <= lim) atomicOr(&bm[kb >> 5], 1u << (kb & 31));
+  };
+  bool by_count = p.mode == 1;
+  uint32_t K = (uint32_t)min(p.topk, n_kb);
+  if (p.mode == 0) {
+    const double thr_d = p.alpha[h] * (double)Z;
+    if (thr_d > (double)Z) {  // every block
+      for (int64_t kb = tid; kb < n_kb; kb += TK_NT) keep(kb);
+    } else if (!(thr_d > 0.0)) {  // C_m < thr for no m: the top block alone
+      by_count = true;
+      K = 1;
+    } else {
+      const uint64_t thr = (uint64_t)ceil(thr_d);
+      // largest v with sum(mass >= v) >= thr (v = 0 qualifies: the sum is Z)
+      const uint64_t top = block_max_u64(
+          [&] {
+            uint64_t x = 0;
+#pragma unroll
+            for (int j = 0; j < KPT; ++j) x = u[j] > x ? u[j] : x;
+            return x;
+          }(),
+          red);
+      uint64_t v = 0;
+      for (int bit = top ? 63 - __clzll((long long)top) : -1; bit >= 0; --bit) {
+        const uint64_t v2 = v | (1ull << bit);
+        uint64_t part = 0;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) part += u[j] >= v2 ? u[j] : 0ull;
+        if (block_sum_u64(part, red) >= thr) v = v2;
+      }
+      uint64_t gpart = 0;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) gpart += u[j] > v ? u[j] : 0ull;
+      const uint64_t s_gt = block_sum_u64(gpart, red);
+      // ties at v taken in index order (block tid + 256 j: slot j, then
+      // lower waves, then lower lanes)
+      // v >= 1: sum(mass >= 1) = Z >= thr
+      const uint64_t n_eq_take = v ? (thr - s_gt - 1) / v + 1 : 0;
+      uint32_t *eqc = sh.eqc[0];  // [KPT][TK_NW]
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const bool eq = tid + TK_NT * j < n_kb && u[j] == v;
+        const uint64_t bmsk = __ballot(eq);
+        if (lane == 0) eqc[j * TK_NW + w] = (uint32_t)__popcll(bmsk);
+      }
+      __syncthreads();
+      uint64_t eq_before = 0;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const int64_t kb = tid + TK_NT * j;
+        const bool eq = kb < n_kb && u[j] == v;
+        const uint64_t bmsk = __ballot(eq);
+        uint64_t rank = eq_before + (uint64_t)__popcll(bmsk & lt);
+#pragma unroll
+        for (int x = 0; x < TK_NW; ++x) rank += x < w ? eqc[j * TK_NW + x] : 0u;
+        if (kb < n_kb && (u[j] > v || (eq && rank < n_eq_take))) keep(kb);
+#pragma unroll
+        for (int x = 0; x < TK_NW; ++x) eq_before += eqc[j * TK_NW + x];
+      }
+    }
+  }
+  if (by_count) {
+    tk_reg_select_bits<KPT>(u, (int32_t)n_kb, K, sh, [&](int j, int32_t i, bool take) {
+      if (take) keep(i);
+    });
+  }
+  __syncthreads();
+  // the own block (selection.py:591): the block whose first token is pos0
+  if (tid == 0 && pos0 % blk == 0 && pos0 / blk < n_kb) keep(pos0 / blk);
+  __syncthreads();
+  tk_emit_bitmap_row(bm, n_kb, -1, 0, 0, p.width, p.out_idx + row * p.width, p.out_count + row,
+                     sh.wtmp[1]);
+}
+
+}  // namespace la
+
+using namespace la;
+
+static int64_t ceil_log2(int64_t x) {
+  int64_t l = 0;
+  while (((int64_t)1 << l) < x) ++l;
+  return l;
+}
+
+static int xattn_lds(const la_xattn_select_args *a, int64_t n_kb, int64_t ns, size_t &bytes) {
+  bytes = (size_t)xa_align16(a->block * a->D * 4) + (size_t)(n_kb * ns * 8) +
+          (size_t)((n_kb + 31) / 32 * 4);
+  return bytes <= 120 * 1024 ? LA_OK : LA_ERR_UNSUPPORTED;
+}
+
+extern "C" int la_xattn_select(const la_xattn_select_args *a, void *stream) {
+  LA_REQUIRE(a && a->q && a->k && a->out_idx && a->out_count, "la_xattn_select: null pointer");
+  LA_REQUIRE(a->B > 0 && a->Hq > 0 && a->Hkv > 0 && a->Tq > 0 && a->T > 0 && a->D > 0,
+             "la_xattn_select: bad shape");
+  LA_REQUIRE(a->Hq % a->Hkv == 0, "n_heads must be a multiple of n_kv_heads");
+  LA_REQUIRE(a->block >= 1 && a->block <= 64 && a->stride >= 1, "la_xattn_select: block in [1, 64], stride >= 1");
+  LA_REQUIRE(a->offset >= 0, "la_xattn_select: offset >= 0");
+  LA_REQUIRE(a->mode == 0 || a->mode == 1, "la_xattn_select: mode 0 (threshold) or 1 (top-k)");
+  LA_REQUIRE(a->mode == 1 || a->alpha, "la_xattn_select: threshold mode needs per-head alpha");
+  LA_REQUIRE(a->mode == 0 || a->topk >= 1, "la_xattn_select: topk >= 1");
+  LA_REQUIRE(a->in_dtype == LA_F32 || a->in_dtype == LA_BF16 || a->in_dtype == LA_F16,
+             "la_xattn_select: q/k dtype");
+  const int64_t n_kb = ceil_div(a->T, a->block), n_qb = ceil_div(a->Tq, a->block);
+  const int64_t ns = (2 * a->block - 2) / a->stride + 1;
+  LA_REQUIRE(a->width >= (a->mode == 1 ? std::min(a->topk, n_kb) + 1 : n_kb),
+             "la_xattn_select: width below the largest selection");
+  if (n_kb > 16 * TK_NT)
+    return fail(LA_ERR_UNSUPPORTED, "la_xattn_select: at most %d key blocks", 16 * TK_NT);
+  size_t lds = 0;
+  if (xattn_lds(a, n_kb, ns, lds) != LA_OK)
+    return fail(LA_ERR_UNSUPPORTED, "la_xattn_select: %zu bytes of LDS per row (max 120 KiB)", lds);
+  if (a->in_dtype == LA_BF16)
+    LA_REQUIRE((uintptr_t)a->k % 16 == 0 && a->D % 8 == 0 && a->k_sb % 8 == 0 && a->k_sh % 8 == 0 &&
+                   a->k_st % 8 == 0,
+               "la_xattn_select: bf16 key rows must be 16-byte aligned");
+  XaKP p{};
+  p.q = a->q;
+  p.k = a->k;
+  p.out_idx = a->out_idx;
+  p.out_count = a->out_count;
+  p.alpha = a->alpha;
+  p.B = a->B; p.Hq = a->Hq; p.Hkv = a->Hkv; p.Tq = a->Tq; p.T = a->T; p.D = a->D;
+  p.q_sb = a->q_sb; p.q_sh = a->q_sh; p.q_st = a->q_st;
+  p.k_sb = a->k_sb; p.k_sh = a->k_sh; p.k_st = a->k_st;
+  p.blk = a->block; p.r = a->stride; p.n_slots = ns; p.offset = a->offset;
+  p.n_qb = n_qb; p.n_kb = n_kb; p.topk = a->topk; p.width = a->width;
+  p.inv_sqrt_d = a->inv_sqrt_d;
+  p.two_f = std::ldexp(1.0, (int)(52 - ceil_log2(n_kb * ns)));
+  p.in_dt = a->in_dtype;
+  p.mode = a->mode;
+  const int64_t nwg = a->B * a->Hq * n_qb;
+  LA_REQUIRE(nwg < ((int64_t)1 << 31), "la_xattn_select: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  const int kpt = (int)ceil_div(n_kb, TK_NT);
+  auto launch = [&](auto kern) -> int {
+    if (lds > 64 * 1024)
+      LA_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    kern<<<dim3((unsigned)nwg), TK_NT, lds, st>>>(p);
+    return (int)LA_OK;
+  };
+  int rc;
+  if (kpt <= 1)
+    rc = launch(&xattn_select_kernel<1>);
+  else if (kpt <= 4)
+    rc = launch(&xattn_select_kernel<4>);
+  else
+    rc = launch(&xattn_select_kernel<16>);
+  if (rc != LA_OK) return rc;
+  LA_LAUNCHED();
+  return LA_OK;
+}

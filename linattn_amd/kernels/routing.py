@@ -1,4 +1,5 @@
-"""Per-query block routing on gfx950: MoBA's gate and NSA's blockwise selection.
+"""Block routing on gfx950: MoBA's gate, NSA's blockwise selection and
+XAttention's antidiagonal block selection.
 
 MoBAAttention.select (variants/selection.py:610-640) and
 NSAAttention.selection_mask (variants/native_sparse.py:78-93) compute the same
@@ -13,13 +14,14 @@ function of the inputs.
 from __future__ import annotations
 
 import ctypes
-from typing import Tuple
+import math
+from typing import Optional, Sequence, Tuple, Union
 
 import torch
 
 from linattn_amd import _native as N
 
-__all__ = ["gate_select_hip", "nsa_selection_hip"]
+__all__ = ["gate_select_hip", "nsa_selection_hip", "xattn_select_hip"]
 
 
 def gate_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int, topk: int,
@@ -65,3 +67,64 @@ def nsa_selection_hip(q: torch.Tensor, k: torch.Tensor, *, block: int, selected_
     """NSAAttention.selection_mask (native_sparse.py:78-93) as block lists:
     the same routing as MoBA with ``selected_blocks`` blocks per query."""
     return gate_select_hip(q, k, block=block, topk=selected_blocks, offset=offset)
+
+
+def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride: int = 8,
+                     threshold: Union[float, Sequence[float]] = 0.9, offset: int = 0,
+                     topk: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """XAttention's block selection (XAttention.antidiagonal_scores / select,
+    selection.py:528-595) for every (b, query head, query block).
+
+    Slot scores are the strided antidiagonal sums of each (query block, key
+    block) gram matrix (stride ``stride``, blocks of ``block`` tokens) times
+    1/sqrt(D); the softmax over a row's visible (block, slot) pairs gives the
+    block masses; ``threshold`` (a float, or one value per query head as the
+    reference's ``threshold_per_head``) keeps the minimal prefix of blocks,
+    by mass, whose cumulative mass reaches it (_cumulative_select,
+    selection.py:62-69); with ``topk`` the top-k blocks by mass are kept
+    instead (select_mode "topk").  The own block is OR'd in and blocks past
+    causality dropped.  Masses are exact integers of fixed-point weights from
+    a deterministic exp, so ties and the threshold crossing are a fixed
+    function of the inputs (ties to the lowest block).
+
+    q (B, Hq, Tq, D) at positions offset + t; k (B, Hkv, T, D).  Returns ids
+    (B, Hq, n_qb, W) ascending, -1 padded (W = n_kb, or min(topk, n_kb) + 1)
+    and counts (B, Hq, n_qb)."""
+    dev = N.require_gpu(q, k, what="xattn_select_hip")
+    if q.dim() != 4 or k.dim() != 4 or q.shape[0] != k.shape[0] or q.shape[3] != k.shape[3]:
+        raise ValueError("q (B, Hq, Tq, D) and k (B, Hkv, T, D) expected")
+    if q.dtype != k.dtype:
+        raise ValueError("q and k must share a dtype")
+    B, Hq, Tq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    if Hq % Hkv:
+        raise ValueError("n_heads must be a multiple of n_kv_heads")
+    if q.stride(3) != 1 or k.stride(3) != 1:
+        raise ValueError("q and k rows must be contiguous")
+    if not 1 <= block <= 64 or stride < 1 or offset < 0:
+        raise ValueError("block in [1, 64], stride >= 1 and offset >= 0 required")
+    if topk is not None and topk < 1:
+        raise ValueError("topk >= 1 required")
+    n_qb, n_kb = -(-Tq // block), -(-T // block)
+    width = min(topk, n_kb) + 1 if topk is not None else n_kb
+    ids = torch.empty(B, Hq, n_qb, width, dtype=torch.int32, device=dev)
+    counts = torch.empty(B, Hq, n_qb, dtype=torch.int32, device=dev)
+    alpha = None
+    a = N.LaXattnSelectArgs()
+    if topk is None:
+        th = torch.as_tensor(threshold, dtype=torch.float64).flatten()
+        if th.numel() not in (1, Hq):
+            raise ValueError("threshold: one value or one per query head")
+        alpha = th.expand(Hq).contiguous().to(dev)
+        a.alpha = alpha.data_ptr()
+    a.q, a.k, a.out_idx, a.out_count = q.data_ptr(), k.data_ptr(), ids.data_ptr(), counts.data_ptr()
+    a.B, a.Hq, a.Hkv, a.Tq, a.T, a.D = B, Hq, Hkv, Tq, T, D
+    a.q_sb, a.q_sh, a.q_st = q.stride(0), q.stride(1), q.stride(2)
+    a.k_sb, a.k_sh, a.k_st = k.stride(0), k.stride(1), k.stride(2)
+    a.block, a.stride, a.offset, a.width = block, stride, offset, width
+    a.topk = int(topk or 0)
+    a.inv_sqrt_d = 1.0 / math.sqrt(D)
+    a.mode = 0 if topk is None else 1
+    a.in_dtype = N.dtype_code(q.dtype)
+    N.check(N.load().la_xattn_select(ctypes.byref(a), N.stream_handle(dev)), "xattn_select_hip")
+    return ids, counts

@@ -1,7 +1,7 @@
 """``<backend>_<variant>`` registry of the HIP backend.
 
 Mirrors the reference's ``KERNEL_VARIANTS`` / ``build`` routing
-(src/linattn/registry.py:139-146, 225-236): names ``hip_quest``, ``hip_dsa``, ``hip_moba``,
+(src/linattn/registry.py:139-146, 225-236): names ``hip_quest``, ``hip_dsa``, ``hip_moba``, ``hip_xattention``,
 ``hip_sliding_window`` and ``hip_streaming_sink`` map to the torch variant
 they implement; unknown names raise ``KeyError`` like the reference.
 """

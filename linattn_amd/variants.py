@@ -12,6 +12,8 @@ selection kernels and runs the HIP executor, while ``stats``/``read_budget``/
                          indexing, sink + window OR'd in
 * ``hip_moba``           MoBAAttention (selection.py:610-640): per-query routing by
                          q . mean(K block), own block added
+* ``hip_xattention``     XAttention (selection.py:500-595): strided antidiagonal
+                         block scores, cumulative-mass threshold (or top-k)
 * ``hip_sliding_window`` SlidingWindowAttention (variants/local.py:22-61)
 * ``hip_streaming_sink`` StreamingSinkAttention (local.py:64-80)
 
@@ -30,9 +32,10 @@ from linattn_amd.core import AttnConfig, AttentionVariant
 from linattn_amd.kernels.block_sparse import sparse_attention
 from linattn_amd.kernels.fused_indexer import indexer_topk
 from linattn_amd.kernels.quest_pages import alloc_page_meta, page_update_hip, quest_select_hip
-from linattn_amd.kernels.routing import gate_select_hip
+from linattn_amd.kernels.prefill import block_sparse_prefill
+from linattn_amd.kernels.routing import gate_select_hip, xattn_select_hip
 
-__all__ = ["HipAttention", "HipQuest", "HipDSA", "HipMoBA", "HipSlidingWindow",
+__all__ = ["HipAttention", "HipQuest", "HipDSA", "HipMoBA", "HipXAttention", "HipSlidingWindow",
            "HipStreamingSink", "SUPPORTED"]
 
 
@@ -322,10 +325,73 @@ class HipMoBA(HipAttention):
         return super().flops(seq_len, batch) + int(sel)
 
 
+class HipXAttention(HipAttention):
+    """XAttention (selection.py:500-595) on the GPU: per query block, the
+    strided antidiagonal scores of every visible key block, softmax block
+    masses and the minimal prefix of blocks reaching ``cfg.threshold``
+    (``xattn_select_hip``), then the executor reads those blocks intersected
+    with causality.
+
+    extras: ``xattn_block`` (default 8), ``antidiagonal_stride`` (default
+    ``cfg.stride``), ``select_mode`` ("threshold", default, or "topk" with
+    ``cfg.topk_blocks``), ``threshold_per_head``.  The reference's
+    "top_ratio" mode compares the cumulative probability mass against a block
+    count (selection.py:583-585 with :598-606), which keeps every block; it
+    is not offered.  64-token blocks over a whole bf16 prefill (offset 0,
+    head_dim 128) run the MFMA prefill kernel; otherwise every query row reads
+    its block's list through ``sparse_attention``."""
+
+    reference = "xattention"
+
+    def __init__(self, cfg=None, **kw):
+        super().__init__(cfg, **kw)
+        ex = self.cfg.extras
+        self.block = int(ex.get("xattn_block", 8))
+        self.r = int(ex.get("antidiagonal_stride", self.cfg.stride))
+        self.select_mode = ex.get("select_mode", "threshold")
+        if self.select_mode not in ("threshold", "topk"):
+            raise ValueError(f"hip_xattention: select_mode {self.select_mode!r} not supported "
+                             "(threshold or topk)")
+
+    def attend(self, q, state, offset: int = 0):
+        k, v = state["k"], state["v"]
+        blk = self.block
+        if self.select_mode == "topk":
+            ids, counts = xattn_select_hip(q, k, block=blk, stride=self.r, offset=offset,
+                                           topk=self.cfg.topk_blocks)
+        else:
+            th = self.cfg.extras.get("threshold_per_head", self.cfg.threshold)
+            ids, counts = xattn_select_hip(q, k, block=blk, stride=self.r, threshold=th,
+                                           offset=offset)
+        Tq, T = q.shape[2], k.shape[2]
+        if (blk == 64 and offset == 0 and Tq == T and q.shape[3] == 128
+                and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16):
+            out = block_sparse_prefill(q, k, v, ids, counts, block_size=64, out_dtype=q.dtype)
+            rows = ids.repeat_interleave(blk, dim=2)[:, :, :Tq]
+        else:
+            rows = ids.repeat_interleave(blk, dim=2)[:, :, :Tq].contiguous()
+            rcounts = counts.repeat_interleave(blk, dim=2)[:, :, :Tq].contiguous()
+            out = sparse_attention(q, k, v, rows, unit=blk, counts=rcounts, causal=True,
+                                   offset=offset, out_dtype=q.dtype)
+        self._extra = {"blocks_per_query": float(counts.to(torch.float64).mean()),
+                       "reads_per_query": _reads_per_query(rows, blk, offset, T)}
+        return out
+
+    def read_budget(self, seq_len, batch=1):
+        return float(seq_len)  # data dependent: up to the whole causal prefix
+
+    def flops(self, seq_len, batch=1):
+        blk, c = self.block, self.cfg
+        n_b = (seq_len + blk - 1) // blk
+        sel = 2 * 2 * batch * c.n_heads * n_b * n_b * blk * blk / self.r * c.head_dim / blk
+        return super().flops(seq_len, batch) + int(sel)
+
+
 SUPPORTED = {
     "quest": HipQuest,
     "dsa": HipDSA,
     "moba": HipMoBA,
+    "xattention": HipXAttention,
     "sliding_window": HipSlidingWindow,
     "streaming_sink": HipStreamingSink,
 }

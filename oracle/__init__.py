@@ -84,6 +84,11 @@ def lib() -> ctypes.CDLL:
     L.or_sparse_attend.argtypes = [_D, _i64, _i64, _VP, _VP, ctypes.c_int, _F32, _F32, _I32, _i64,
                                    _i64, _i64, _i64, _i64, _i64, _I64, _i64, ctypes.c_double, _D, _D]
     L.or_sparse_attend.restype = ctypes.c_int
+    L.or_exp_det.argtypes = [ctypes.c_double]
+    L.or_exp_det.restype = ctypes.c_double
+    L.or_xattn_select.argtypes = [_D, _D, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_double,
+                                  ctypes.c_int, ctypes.c_double, _i64, _i64, _I32, _I32]
+    L.or_xattn_select.restype = ctypes.c_int
     _LIB = L
     return L
 
@@ -547,6 +552,49 @@ def gate_select(q, k, *, block: int, topk: int, offset: int = 0) -> np.ndarray:
                 u = sorted(set(int(x) for x in idx[b, h, t] if x >= 0) | {int(own[t])})
                 out[b, h, t, :len(u)] = u
     return out
+
+
+# ------------------------------------------------------------- XAttention --
+def xattn_select(q, k, *, block: int = 8, stride: int = 8, threshold=0.9, offset: int = 0,
+                 topk: Optional[int] = None):
+    """XAttention's block selection (selection.py:528-595) per (b, query
+    head, query block), in the integer-mass form the kernel computes
+    (la_oracle.c or_xattn_select): antidiagonal slot scores in fp64, weights
+    by a deterministic exp, block masses as fixed-point integers, then the
+    cumulative threshold (``threshold`` a float or one value per query head)
+    or, with ``topk``, the top-k blocks; own block OR'd, invisible blocks
+    dropped.  Returns (ids (B, Hq, n_qb, width) ascending, -1 padded,
+    counts (B, Hq, n_qb)); width = n_kb, or min(topk, n_kb) + 1."""
+    q, k = to_f64(q), to_f64(k)
+    B, Hq, Tq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    n_qb, n_kb = -(-Tq // block), -(-T // block)
+    mode = 1 if topk is not None else 0
+    width = min(topk, n_kb) + 1 if mode else n_kb
+    alphas = np.broadcast_to(np.asarray(threshold, dtype=np.float64), (Hq,))
+    inv = 1.0 / math.sqrt(D)
+    L = lib()
+    ids = np.full((B, Hq, n_qb, width), -1, dtype=np.int32)
+    counts = np.zeros((B, Hq, n_qb), dtype=np.int32)
+    for b in range(B):
+        for h in range(Hq):
+            a = np.ascontiguousarray(q[b, h])
+            c = np.ascontiguousarray(k[b, h // G])
+            o = np.zeros((n_qb, width), dtype=np.int32)
+            n = np.zeros(n_qb, dtype=np.int32)
+            rc = L.or_xattn_select(_p(a, _D), _p(c, _D), Tq, T, D, block, stride, offset, inv,
+                                   mode, float(alphas[h]), int(topk or 0), width, _p(o, _I32),
+                                   _p(n, _I32))
+            if rc != 0:
+                raise ValueError("or_xattn_select: bad arguments")
+            ids[b, h], counts[b, h] = o, n
+    return ids, counts
+
+
+def exp_det(x: float) -> float:
+    """The deterministic exp of the XAttention weights (la_oracle.c)."""
+    return lib().or_exp_det(float(x))
 
 
 # ------------------------------------------------------------------ local --

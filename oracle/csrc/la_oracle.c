@@ -14,6 +14,9 @@
  *   or_mean_pool      core.py:102-120 (block_reduce, mean, tail repeats last row)
  *   or_dot_rows       selection.py:339-345 (pooled q . pooled k block scores)
  *   or_sparse_attend  block_sparse.py:40-75, decode_attn.c:39-65 (gather + softmax)
+ *   or_exp_det        a deterministic exp (fixed fma sequence) for XAttention
+ *   or_xattn_select   selection.py:528-595 (antidiagonal scores, cumulative
+ *                     mass threshold or top-k over integer block masses)
  *
  * Canonical arithmetic (the selection contract the HIP kernels reproduce):
  *   - inputs are fp32 / bf16 values widened exactly to fp64;
@@ -247,5 +250,153 @@ int or_sparse_attend(const double *q, int64_t G, int64_t D, const void *k, const
     }
     for (int64_t d = 0; d < D; ++d) o[d] /= l;
   }
+  return 0;
+}
+
+/* ------------------------------------------------------- XAttention ---- */
+
+/* exp(x) for x <= 0 by a fixed sequence of correctly rounded operations, so
+ * that csrc/xattn.hip (the same sequence) reproduces every bit: 0 below -700;
+ * x = k*ln2 + r with the fdlibm two-part ln2 and fused multiply-adds; e^r by
+ * the degree-13 Taylor polynomial in Horner form (fma); times 2^k built from
+ * exponent bits. */
+double or_exp_det(double x) {
+  if (!(x > -700.0)) return 0.0;
+  const double kf = nearbyint(x * 1.4426950408889634);
+  double r = fma(-kf, 6.93147180369123816490e-01, x);
+  r = fma(-kf, 1.90821492927058770002e-10, r);
+  double p = 1.6059043836821613e-10;
+  p = fma(p, r, 2.08767569878681e-09);
+  p = fma(p, r, 2.505210838544172e-08);
+  p = fma(p, r, 2.755731922398589e-07);
+  p = fma(p, r, 2.7557319223985893e-06);
+  p = fma(p, r, 2.48015873015873e-05);
+  p = fma(p, r, 0.0001984126984126984);
+  p = fma(p, r, 0.001388888888888889);
+  p = fma(p, r, 0.008333333333333333);
+  p = fma(p, r, 0.041666666666666664);
+  p = fma(p, r, 0.16666666666666666);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  uint64_t bits = (uint64_t)((int64_t)kf + 1023) << 52;
+  double two_k;
+  memcpy(&two_k, &bits, 8);
+  return p * two_k;
+}
+
+typedef struct {
+  uint64_t mass;
+  int64_t kb;
+} or_mass_t;
+
+static int or_mass_cmp(const void *pa, const void *pb) {
+  const or_mass_t *a = (const or_mass_t *)pa, *b = (const or_mass_t *)pb;
+  if (a->mass != b->mass) return a->mass > b->mass ? -1 : 1;
+  return a->kb < b->kb ? -1 : (a->kb > b->kb);
+}
+
+/* XAttention.antidiagonal_scores + select (variants/selection.py:528-595)
+ * for one (batch, query head): q [Tq][D] and the head's KV rows k [T][D]
+ * (fp64 images of the inputs).  Blocks of blk tokens; slot s (antidiagonal
+ * offset o = s*r <= 2*blk - 2, selection.py:554) = sum over i increasing of
+ * the dot products q[qb*blk+i] . k[kb*blk+o-i] (fma over d increasing; rows
+ * past Tq / T are zero rows, F.pad at :544-546), times inv_sqrt_d (:566).
+ * Visible blocks: kb*blk <= qb*blk + offset (:573-575).  Weights
+ * or_exp_det(slot - row max) as integers nearbyint(w * 2^F), F = 52 -
+ * ceil(log2(n_kb*n_slots)); block mass = the sum over its slots (:576-579).
+ * mode 0: blocks sorted by (mass desc, index asc), keep 1 + #{m : C_m <
+ * ceil(alpha*Z)} (C_m prefix sums, Z the total; alpha*Z > Z keeps all;
+ * _cumulative_select :62-69); mode 1: the first min(topk, n_kb) (:581-582).
+ * Then the own block (first token qb*blk + offset) is OR'd in and invisible
+ * blocks dropped (:591-592).  out [n_qb][width] ascending, -1 padded;
+ * count [n_qb].  Returns 0, or -1 on a bad argument. */
+int or_xattn_select(const double *q, const double *k, int64_t Tq, int64_t T, int64_t D,
+                    int64_t blk, int64_t r, int64_t offset, double inv_sqrt_d, int mode,
+                    double alpha, int64_t topk, int64_t width, int32_t *out, int32_t *count) {
+  if (blk < 1 || r < 1 || Tq < 1 || T < 1 || D < 1 || offset < 0) return -1;
+  const int64_t n_qb = (Tq + blk - 1) / blk, n_kb = (T + blk - 1) / blk;
+  const int64_t ns = (2 * blk - 2) / r + 1;
+  int64_t lg = 0;
+  while (((int64_t)1 << lg) < n_kb * ns) ++lg;
+  const double two_f = ldexp(1.0, (int)(52 - lg));
+  double *S = (double *)malloc((size_t)(n_kb * ns) * sizeof(double));
+  or_mass_t *m = (or_mass_t *)malloc((size_t)n_kb * sizeof(or_mass_t));
+  unsigned char *keep = (unsigned char *)malloc((size_t)n_kb);
+  if (!S || !m || !keep) {
+    free(S);
+    free(m);
+    free(keep);
+    return -1;
+  }
+  for (int64_t qb = 0; qb < n_qb; ++qb) {
+    const int64_t pos0 = qb * blk + offset;
+    int64_t lim = pos0 / blk;
+    if (lim > n_kb - 1) lim = n_kb - 1;
+    double mx = -INFINITY;
+    for (int64_t kb = 0; kb <= lim; ++kb) {
+      for (int64_t s = 0; s < ns; ++s) {
+        const int64_t o = s * r;
+        const int64_t i0 = o - blk + 1 > 0 ? o - blk + 1 : 0, i1 = o < blk - 1 ? o : blk - 1;
+        double acc = 0.0;
+        for (int64_t i = i0; i <= i1; ++i) {
+          const int64_t qr = qb * blk + i, kr = kb * blk + (o - i);
+          double e = 0.0;
+          for (int64_t d = 0; d < D; ++d) {
+            const double qv = qr < Tq ? q[qr * D + d] : 0.0;
+            const double kv = kr < T ? k[kr * D + d] : 0.0;
+            e = fma(qv, kv, e);
+          }
+          acc = acc + e;
+        }
+        S[kb * ns + s] = acc * inv_sqrt_d;
+        if (S[kb * ns + s] > mx) mx = S[kb * ns + s];
+      }
+    }
+    uint64_t Z = 0;
+    for (int64_t kb = 0; kb < n_kb; ++kb) {
+      uint64_t ms = 0;
+      if (kb <= lim)
+        for (int64_t s = 0; s < ns; ++s)
+          ms += (uint64_t)nearbyint(or_exp_det(S[kb * ns + s] - mx) * two_f);
+      m[kb].mass = ms;
+      m[kb].kb = kb;
+      Z += ms;
+    }
+    qsort(m, (size_t)n_kb, sizeof(or_mass_t), or_mass_cmp);
+    int64_t n_keep;
+    if (mode == 1) {
+      n_keep = topk < n_kb ? topk : n_kb;
+    } else {
+      const double thr_d = alpha * (double)Z;
+      if (thr_d > (double)Z) {
+        n_keep = n_kb;
+      } else {
+        const uint64_t thr = thr_d > 0.0 ? (uint64_t)ceil(thr_d) : 0;
+        uint64_t c = 0;
+        n_keep = 1;
+        for (int64_t i = 0; i < n_kb; ++i) {
+          c += m[i].mass;
+          if (c < thr) ++n_keep;
+        }
+        if (n_keep > n_kb) n_keep = n_kb;
+      }
+    }
+    memset(keep, 0, (size_t)n_kb);
+    for (int64_t i = 0; i < n_keep; ++i) keep[m[i].kb] = 1;
+    if (pos0 % blk == 0 && pos0 / blk < n_kb) keep[pos0 / blk] = 1;
+    int64_t c = 0;
+    int32_t *o = out + qb * width;
+    for (int64_t kb = 0; kb <= lim; ++kb)
+      if (keep[kb]) {
+        if (c < width) o[c] = (int32_t)kb;
+        ++c;
+      }
+    for (int64_t i = c; i < width; ++i) o[i] = -1;
+    count[qb] = (int32_t)(c < width ? c : width);
+  }
+  free(S);
+  free(m);
+  free(keep);
   return 0;
 }

@@ -16,8 +16,13 @@ from linattn_amd.registry import KERNEL_VARIANTS, build, describe_kernel
 
 def test_registry_names_and_errors():
     """registry.py:225-236: <backend>_<variant> names, KeyError otherwise."""
-    assert set(KERNEL_VARIANTS) == {"hip_quest", "hip_dsa", "hip_moba", "hip_sliding_window",
-                                    "hip_streaming_sink"}
+    assert set(KERNEL_VARIANTS) == {"hip_quest", "hip_dsa", "hip_moba", "hip_xattention",
+                                    "hip_sliding_window", "hip_streaming_sink"}
+    assert describe_kernel("hip_xattention")["reference"] == "xattention"
+    # top_ratio compares cumulative mass with a block count (selection.py:583-585):
+    # not offered
+    with pytest.raises(ValueError):
+        build("hip_xattention", extras={"select_mode": "top_ratio"})
     assert describe_kernel("hip_moba")["reference"] == "moba"
     assert describe_kernel("hip_quest")["reference"] == "quest"
     assert build("hip_quest").name == "hip_quest"

@@ -404,3 +404,112 @@ def test_window_mask():
     m = oracle.window_mask(4, 8, 4, window=2, sink=1)
     assert m[0].tolist() == [True, False, False, True, True, False, False, False]
     assert m[3].tolist() == [True, False, False, False, False, False, True, True]
+
+
+# --------------------------------------------------------- XAttention ----
+def test_exp_det_matches_libm():
+    """The deterministic exp of the XAttention weights against math.exp:
+    within 4 ulp over [-700, 0]; exp(0) = 1; 0 below -700."""
+    xs = np.concatenate([-np.logspace(-12, np.log10(699.9), 2000), [-0.0, 0.0, -1e-300, -699.99]])
+    for x in xs:
+        got, ref = oracle.exp_det(x), math.exp(x)
+        assert abs(got - ref) <= 4 * math.ulp(ref), (x, got, ref)
+    assert oracle.exp_det(0.0) == 1.0
+    assert oracle.exp_det(-700.0) == 0.0 and oracle.exp_det(-1e9) == 0.0
+
+
+def _xattn_float_reference(q, k, *, block, stride, threshold, offset, topk=None):
+    """XAttention.select (selection.py:528-595) restated with numpy floats:
+    antidiagonal sums by einsum over the whole (query block, key block) gram
+    tensor, fp64 softmax over the visible (block, slot) pairs, a stable sort
+    of the block masses and their cumulative sum.  Independent of the
+    oracle's integer masses; equal selections unless a mass tie or the
+    threshold crossing sits within rounding."""
+    q, k = q.astype(np.float64), k.astype(np.float64)
+    Tq, D = q.shape
+    T = k.shape[0]
+    n_qb, n_kb = -(-Tq // block), -(-T // block)
+    qp = np.zeros((n_qb * block, D)); qp[:Tq] = q
+    kp = np.zeros((n_kb * block, D)); kp[:T] = k
+    gram = np.einsum("aid,bjd->abij", qp.reshape(n_qb, block, D), kp.reshape(n_kb, block, D))
+    offs = list(range(0, 2 * block - 1, stride))
+    S = np.zeros((n_qb, n_kb, len(offs)))
+    ii = np.arange(block)
+    for s, o in enumerate(offs):
+        jj = o - ii
+        ok = (jj >= 0) & (jj < block)
+        S[..., s] = gram[:, :, ii[ok], jj[ok]].sum(-1)
+    S /= math.sqrt(D)
+    out = []
+    for qb in range(n_qb):
+        pos0 = qb * block + offset
+        vis = np.arange(n_kb) * block <= pos0
+        flat = np.where(vis[:, None], S[qb], -np.inf)
+        p = np.exp(flat - flat.max())
+        mass = (p / p.sum()).sum(-1)
+        order = sorted(range(n_kb), key=lambda j: (-mass[j], j))
+        if topk is not None:
+            n_keep = min(topk, n_kb)
+        else:
+            cs = np.cumsum(mass[order])
+            n_keep = min(int((cs < threshold).sum()) + 1, n_kb)
+        sel = set(order[:n_keep])
+        if pos0 % block == 0 and pos0 // block < n_kb:
+            sel.add(pos0 // block)
+        out.append(sorted(j for j in sel if vis[j]))
+    return out
+
+
+@pytest.mark.parametrize("block,stride,threshold,offset,topk,T", [
+    (8, 8, 0.9, 0, None, 203), (8, 4, 0.6, 0, None, 128), (16, 8, 0.95, 5, None, 150),
+    (4, 2, 0.5, 0, None, 61), (8, 8, None, 0, 3, 203), (8, 8, 1.5, 0, None, 100)])
+def test_xattn_select_matches_float_restatement(block, stride, threshold, offset, topk, T):
+    r = rng(21)
+    B, Hq, Hkv, D = 1, 2, 1, 32
+    Tq = T - offset
+    q = r.standard_normal((B, Hq, Tq, D)).astype(np.float32)
+    k = r.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    k[0, 0, r.permutation(T)[:T // 10]] *= 4.0  # peaked rows
+    ids, counts = oracle.xattn_select(q, k, block=block, stride=stride,
+                                      threshold=threshold if threshold else 0.9, offset=offset,
+                                      topk=topk)
+    for h in range(Hq):
+        ref = _xattn_float_reference(q[0, h], k[0, 0], block=block, stride=stride,
+                                     threshold=threshold, offset=offset, topk=topk)
+        for qb, lst in enumerate(ref):
+            got = [int(x) for x in ids[0, h, qb] if x >= 0]
+            assert got == lst, (h, qb, got, lst)
+            assert counts[0, h, qb] == len(lst)
+
+
+def test_xattn_known_answer():
+    """Two 2-token blocks, stride 1: slot scores by hand.  q rows (1,0),
+    (0,1); k rows (1,0), (0,1), (5,0), (0,5).  Query block 1 sees key block 0
+    (slots: q0.k0 = 1, q0.k1 + q1.k0 = 0, q1.k1 = 1) and key block 1 (slots 5,
+    0, 5), so block 1 holds e^5-weighted mass and alone reaches 0.9; block 0
+    (the own block of query block 0) is listed only for query block 0."""
+    q = np.array([[[[1.0, 0.0], [0.0, 1.0], [1.0, 0.0], [0.0, 1.0]]]], dtype=np.float32)
+    k = np.array([[[[1.0, 0.0], [0.0, 1.0], [5.0, 0.0], [0.0, 5.0]]]], dtype=np.float32)
+    ids, counts = oracle.xattn_select(q * math.sqrt(2), k, block=2, stride=1, threshold=0.9)
+    assert ids[0, 0, 0].tolist() == [0, -1] and counts[0, 0, 0] == 1
+    assert ids[0, 0, 1].tolist() == [1, -1] and counts[0, 0, 1] == 1
+    ids, _ = oracle.xattn_select(q * math.sqrt(2), k, block=2, stride=1, threshold=0.99999)
+    assert ids[0, 0, 1].tolist() == [0, 1]
+
+
+def test_xattn_full_budget_recovers_dense():
+    """threshold > 1 (or top-k over every block) reads every visible block:
+    attention over the selection equals dense causal attention
+    (test_budgets.py:64-81)."""
+    r = rng(22)
+    q = r.standard_normal((1, 2, 70, 16)).astype(np.float32)
+    k = r.standard_normal((1, 1, 70, 16)).astype(np.float32)
+    v = r.standard_normal((1, 1, 70, 16)).astype(np.float32)
+    for kw in (dict(threshold=1.5), dict(topk=100)):
+        ids, counts = oracle.xattn_select(q, k, block=8, stride=8, **kw)
+        rows = np.repeat(ids, 8, axis=2)[:, :, :70]
+        out = oracle.attend_lists(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                                  rows, unit=8, causal=True)
+        dense = oracle.dense_attention(q.astype(np.float64), np.repeat(k, 2, 1).astype(np.float64),
+                                       np.repeat(v, 2, 1).astype(np.float64), causal=True)
+        assert np.abs(out - dense).max() < 1e-12
