@@ -149,14 +149,26 @@ __global__ __launch_bounds__(TK_NT) void xattn_select_kernel(XaKP p) {
         if (kr < p.T) {
           const int64_t ko = kbase + kr * p.k_st;
           if (p.in_dt == LA_BF16) {
+            // 128 dims at a time: all sixteen 16-byte loads of the chunk are
+            // issued before its (serial) fma chain
             const uint16_t *kp = (const uint16_t *)p.k + ko;
-            for (int64_t d = 0; d < D; d += 8) {
-              const uint4 v = *(const uint4 *)(kp + d);
-              const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+            for (int64_t d0 = 0; d0 < D; d0 += 128) {
+              const int nch = (int)min((int64_t)16, (D - d0) / 8);
+              uint4 kv[16];
 #pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                e = __builtin_fma((double)qi[d + 2 * u], (double)bf16lo(wv[u]), e);
-                e = __builtin_fma((double)qi[d + 2 * u + 1], (double)bf16hi(wv[u]), e);
+              for (int c = 0; c < 16; ++c)
+                if (c < nch) kv[c] = *(const uint4 *)(kp + d0 + 8 * c);
+#pragma unroll
+              for (int c = 0; c < 16; ++c) {
+                if (c < nch) {
+                  const uint32_t wv[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
+                  const float *qc = qi + d0 + 8 * c;
+#pragma unroll
+                  for (int u = 0; u < 4; ++u) {
+                    e = __builtin_fma((double)qc[2 * u], (double)bf16lo(wv[u]), e);
+                    e = __builtin_fma((double)qc[2 * u + 1], (double)bf16hi(wv[u]), e);
+                  }
+                }
               }
             }
           } else {
