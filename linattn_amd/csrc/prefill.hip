@@ -181,13 +181,12 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   for (int dt = 0; dt < 8; ++dt)
     voffs[dt] = (32 * kh + vr) * PF_D + 8 * ((2 * dt + ((c16 >> 1) & 1)) ^ vsw) + 4 * (c16 & 1);
 
-  // S^T = K Q^T + bias over this wave's 32 keys of the K block in LDS slot
-  // `slot` (the bias is 0, or -inf where the mask removes a key)
-  auto scores = [&](int slot, const f32x4 (&bias)[2][2], f32x4 (&st)[2][2]) {
+  // S^T = K Q^T over this wave's 32 keys of the K block in LDS slot `slot`
+  auto scores = [&](int slot, f32x4 (&st)[2][2]) {
     const uint16_t *sk = smem + slot * PF_BLK;
 #pragma unroll
     for (int kt2 = 0; kt2 < 2; ++kt2) {
-      f32x4 s0 = bias[0][kt2], s1 = bias[1][kt2];
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const bf16x8 a = *(const bf16x8 *)&sk[koffs[s] + 16 * kt2 * PF_D];
@@ -207,16 +206,12 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[qg][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // The mask of block kbx in this wave's key half as a score bias: -inf on
-  // keys past the causal diagonal or past T, and on every key of a -1 entry.
-  // Only those blocks are masked (a branch ahead of the score MFMAs, so the
-  // step body stays one block); keys and positions fit in int32 (T < 2^30 is
-  // checked at launch).
-  auto mask_bias = [&](int kbx, f32x4 (&bias)[2][2]) {
-#pragma unroll
-    for (int qg = 0; qg < 2; ++qg)
-#pragma unroll
-      for (int kt2 = 0; kt2 < 2; ++kt2) bias[qg][kt2] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The mask of block kbx in this wave's key half: -inf on keys past the
+  // causal diagonal or past T, and on every key of a -1 entry, written over
+  // the block's scores.  Only those blocks (diagonal, partial, empty: a
+  // wave-uniform branch) pay for it; keys and positions fit in int32
+  // (T < 2^30 is checked at launch).
+  auto apply_mask = [&](int kbx, f32x4 (&sc)[2][2]) {
     const int key0 = kbx * PF_BS + 32 * kh;  // first key of this half
     const bool need = kbx < 0 || (p.causal && key0 + 31 > (int)qb * PF_BS + 32 * qh) ||
                       key0 + 32 > (int)p.T;
@@ -229,7 +224,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
         for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            bias[qg][kt2][e] = (16 * kt2 + 4 * g + e > lim) ? __int_as_float(0xff800000) : 0.f;
+            if (16 * kt2 + 4 * g + e > lim) sc[qg][kt2][e] = __int_as_float(0xff800000);
       }
     }
   };
@@ -290,9 +285,9 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     if (c1) clear_rows(kb1, 1);
     if (c0 || c1) lds_barrier();
   }
-  f32x4 st[2][2], bias[2][2];
-  mask_bias(kb, bias);
-  scores(0, bias, st);
+  f32x4 st[2][2];
+  scores(0, st);
+  apply_mask(kb, st);
   {
     float alpha[2];
     settle_max(st, true, alpha);  // acc is still zero: no rescale
@@ -309,9 +304,9 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     const int kb2 = j + 2 < n ? sload_i32(list + j + 2) : 0;
     if (j + 2 < n) dma_k(kb2, par);            // held block j (scored a step ago)
     if (j + 1 < n) dma_v(kb1, 2 + (par ^ 1));  // held block j-1 (multiplied)
-    mask_bias(kb1, bias);
     f32x4 sn[2][2];
-    scores(par ^ 1, bias, sn);
+    scores(par ^ 1, sn);
+    apply_mask(kb1, sn);
     // P = P_hi + P_lo in bf16 (P_lo = bf16(P - P_hi)): the product keeps ~16
     // mantissa bits of each weight, so bf16 rounding of P costs ~2^-17
     // relative instead of 2^-9 (which alone exceeds 2e-3 on rows whose mass
