@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences timed on the CPU")
     ap.add_argument("--shared", action="store_true",
                     help="per-query-head page lists instead of the GQA union")
+    ap.add_argument("--pmc-workload", choices=["c3", "c5"],
+                    help="one warm-up and one timed step of C3 (prefill) or C5 (fp8 decode), "
+                         "then a device copy of COPY_MIB MiB; run under rocprofv3 --pmc")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="C4 only, then a device copy of COPY_MIB MiB (the counter scale "
                          "reference); run under rocprofv3 --pmc")
@@ -379,6 +382,13 @@ def main() -> int:
     from linattn_amd.kernels.quest_pages import quest_select_hip
 
     dev = torch.device("cuda:0")
+    if args.pmc_workload:
+        res = {"c3": bench_c3, "c5": bench_c5}[args.pmc_workload](dev, 1, 1)
+        a = torch.empty(COPY_MIB << 20, dtype=torch.uint8, device=dev)
+        torch.empty_like(a).copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_workload": args.pmc_workload, "copy_bytes": COPY_MIB << 20, **res}))
+        return 0
     cfg = dict(C4)
     union = not args.shared
     q, pool_k, pool_v, pt, mins, maxs = setup_c4(dev, cfg)
