@@ -69,6 +69,25 @@ def nsa_selection_hip(q: torch.Tensor, k: torch.Tensor, *, block: int, selected_
     return gate_select_hip(q, k, block=block, topk=selected_blocks, offset=offset)
 
 
+_ALPHAS = {}
+
+
+def _alphas(threshold, Hq: int, dev: torch.device) -> torch.Tensor:
+    """Per-head thresholds on the device without a host sync: a device fill
+    for one value, a cached copy for a per-head list."""
+    if isinstance(threshold, (int, float)):
+        return torch.full((Hq,), float(threshold), dtype=torch.float64, device=dev)
+    th = tuple(float(x) for x in threshold)
+    if len(th) == 1:
+        return torch.full((Hq,), th[0], dtype=torch.float64, device=dev)
+    if len(th) != Hq:
+        raise ValueError("threshold: one value or one per query head")
+    key = (th, str(dev))
+    if key not in _ALPHAS:
+        _ALPHAS[key] = torch.tensor(th, dtype=torch.float64).to(dev)
+    return _ALPHAS[key]
+
+
 def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride: int = 8,
                      threshold: Union[float, Sequence[float]] = 0.9, offset: int = 0,
                      topk: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -112,10 +131,7 @@ def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride
     alpha = None
     a = N.LaXattnSelectArgs()
     if topk is None:
-        th = torch.as_tensor(threshold, dtype=torch.float64).flatten()
-        if th.numel() not in (1, Hq):
-            raise ValueError("threshold: one value or one per query head")
-        alpha = th.expand(Hq).contiguous().to(dev)
+        alpha = _alphas(threshold, Hq, dev)
         a.alpha = alpha.data_ptr()
     a.q, a.k, a.out_idx, a.out_count = q.data_ptr(), k.data_ptr(), ids.data_ptr(), counts.data_ptr()
     a.B, a.Hq, a.Hkv, a.Tq, a.T, a.D = B, Hq, Hkv, Tq, T, D
