@@ -52,10 +52,11 @@ def test_xattn_select_bit_exact(dev, dtype, b, hq, hkv, t, d, block, stride, thr
 
 
 @pytest.mark.parametrize("t,tq,block,topk", [(300, 300, 8, 5), (8300, 64, 8, 40),
-                                             (8300, 64, 8, None)])
+                                             (8300, 64, 8, None), (32768, 16, 8, None)])
 def test_xattn_select_topk_and_offset(dev, t, tq, block, topk):
     """Top-k mode, and a chunk of queries at the end of a long cache
-    (offset = T - Tq; more than 1024 key blocks per row)."""
+    (offset = T - Tq; more than 1024 key blocks per row; at T = 32768 the
+    4096 key blocks take 68 KiB of LDS per row, above the default 64 KiB)."""
     q, k, _ = inputs(1, 2, 1, tq, t, 64, seed=32, dtype=torch.bfloat16)
     kw = dict(block=block, stride=8, offset=t - tq)
     if topk is not None:
