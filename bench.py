@@ -475,7 +475,12 @@ def main() -> int:
         rec = json.loads(tpath.read_text())
         if rec.get("kernel") == ATTN_KERNEL:
             traffic = rec.get("traffic_bytes")
-    meta_bytes = 2 * mins.numel() * 2 + B * Hq * (T // ps) * 8 * 2  # min+max, scores w+r
+    # selection traffic: page min+max read, q read, lists and counts written;
+    # the fused union selector (one kernel) keeps its fp64 score rows on chip,
+    # the per-head form writes them and reads them back for the top-k
+    meta_bytes = 2 * mins.numel() * 2 + q.numel() * 2 + ids.numel() * 4 + counts.numel() * 4
+    if not (union and Hq > Hkv):
+        meta_bytes += B * Hq * (T // ps) * 8 * 2
     step_bytes = att_bytes + meta_bytes
     tok_s = B / (ms_step * 1e-3)
     att_gbs = att_bytes / (ms_launch * 1e-3) / 1e9

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 5
+#define LA_ABI_VERSION 6
 
 /* element types */
 enum {
@@ -45,8 +45,24 @@ enum {
   LA_ERR_WORKSPACE = 4    /* workspace smaller than *_workspace() */
 };
 
+/* device status bits (la_device_status) */
+enum {
+  LA_DEV_TOPK_TIMEOUT = 1 /* a bounded wait of the multi-workgroup top-k ran out */
+};
+
 /* ABI version of the loaded library (LA_ABI_VERSION). */
 int la_abi_version(void);
+
+/*
+ * Status bits the kernels raised on the current device since the last clear
+ * (LA_DEV_*), after the given stream has drained; clear != 0 resets them.
+ * Kernels report failures they detect on the device here instead of through a
+ * return code (a launch returns before the kernel runs): a row of
+ * la_topk_rows / la_indexer_topk whose multi-workgroup selection timed out
+ * comes back with count -1 and -1 ids, and LA_DEV_TOPK_TIMEOUT is raised.
+ * No counterpart in the reference (its kernels report nothing).  Synchronous.
+ */
+int la_device_status(uint32_t *bits, int32_t clear, void *stream);
 
 /* Message describing the last non-zero status returned on this thread. */
 const char *la_last_error(void);

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -40,7 +40,10 @@ EXPORTED = (
     "la_gate_select_workspace",
     "la_gate_select",
     "la_xattn_select",
+    "la_device_status",
 )
+
+LA_DEV_TOPK_TIMEOUT = 1
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -182,6 +185,7 @@ def load() -> ctypes.CDLL:
     L.la_gate_select.argtypes = [P(LaGateSelectArgs), _vp]
     L.la_xattn_select.argtypes = [P(LaXattnSelectArgs), _vp]
     L.la_xattn_select.restype = ctypes.c_int
+    L.la_device_status.argtypes = [ctypes.POINTER(ctypes.c_uint32), _i32, _vp]
     for name in EXPORTED:
         fn = getattr(L, name)
         if fn.restype is None or fn.restype is ctypes.c_int:
@@ -201,6 +205,18 @@ def check(rc: int, what: str) -> None:
     if rc == LA_ERR_INVALID:
         raise ValueError(f"{what}: {msg}")
     raise RuntimeError(f"{what}: status {rc}: {msg}")
+
+
+def device_status(device: Optional[torch.device] = None, clear: bool = True) -> int:
+    """Status bits the kernels raised on ``device`` (LA_DEV_*), read after its
+    current stream drains (a host synchronisation: for tests and debugging,
+    not for hot loops)."""
+    dev = device or torch.device("cuda", torch.cuda.current_device())
+    bits = ctypes.c_uint32(0)
+    with torch.cuda.device(dev):
+        check(load().la_device_status(ctypes.byref(bits), 1 if clear else 0, stream_handle(dev)),
+              "device_status")
+    return int(bits.value)
 
 
 _DT = {torch.float32: LA_F32, torch.bfloat16: LA_BF16, torch.float16: LA_F16,

@@ -74,6 +74,7 @@ __device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
 // device cannot hold one row's chunks at once.
 struct WidePlan {
   int64_t C = 0, R = 0, state_bytes = 0, bytes = 0;
+  bool plain = false;  // ordinary launch instead of a cooperative one
 };
 WidePlan wide_plan(const TopkKParams &p);
 int topk_wide_launch(const TopkKParams &p, const WidePlan &W, void *ws, hipStream_t st);

@@ -20,8 +20,12 @@
 //
 // The waits need every workgroup of a row resident at once: the kernel is
 // launched cooperatively (the runtime refuses a grid that cannot be), rows
-// go in batches that fit, and every wait is bounded.
+// go in batches that fit, and every wait is bounded.  A wait that runs out
+// marks its row; once every batch (and the final sort) has run,
+// tw_finish_kernel pads each marked row with -1, sets its count to -1 and
+// raises LA_DEV_TOPK_TIMEOUT in the device status word (la_device_status).
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 
@@ -36,7 +40,11 @@ constexpr int TW_RB = 11;                              // radix digit bits
 constexpr int TW_BINS = 1 << TW_RB;
 constexpr int TW_BPT = TW_BINS / TK_NT;               // bins per thread in the scan
 constexpr int TW_PASSES = (64 + TW_RB - 1) / TW_RB;
-constexpr uint32_t TW_SPIN_LIMIT = 1u << 20;           // polls before a wait gives up
+constexpr uint32_t TW_SPIN_LIMIT = 1u << 20;           // default polls before a wait gives up
+
+// Status bits raised by kernels of this library on the current device, read
+// and cleared by la_device_status.
+__device__ uint32_t la_dev_status;
 
 // Per-row state in the workspace, zeroed before each launch.
 struct TwRowState {
@@ -52,7 +60,10 @@ struct TwKP {
   uint64_t *slots;    // [row of this launch][C]: (eq + 1) << 32 | gt once published
   double *cand_sc;    // order 0: candidate rows (NG x k) for the final sort
   int32_t *cand_id;
+  int32_t *row_err;   // [NG]: set when a wait of the row ran out
   int64_t row0, C;
+  uint32_t spin_limit;
+  uint32_t unreachable;  // fault injection: no wait can ever be satisfied
 };
 
 __device__ __forceinline__ uint32_t tw_load(const uint32_t *p) {
@@ -97,6 +108,11 @@ __global__ __launch_bounds__(TK_NT) void topk_wide_kernel(TwKP a) {
   uint32_t need = K;
   bool all_in = (int64_t)K >= n_v;
   uint32_t expect = (uint32_t)n_v;  // keys of the row matching the prefix
+  const uint32_t bump = a.unreachable;
+  auto give_up = [&]() {
+    __hip_atomic_store(&st->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&a.row_err[gi], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   int top = 63;
   for (int pass = 0; !all_in && top >= 0; ++pass) {
     const int shift = top >= TW_RB - 1 ? top - (TW_RB - 1) : 0;
@@ -125,7 +141,8 @@ __global__ __launch_bounds__(TK_NT) void topk_wide_kernel(TwKP a) {
     // number: bins only grow, so such a read saw every bin's final count.
     // Thread t holds bins TW_BINS - 1 - TW_BPT * t downwards.
     if (tid == 0) {
-      for (uint32_t spins = 0; tw_load(&st->cnt[pass]) < expect && spins < TW_SPIN_LIMIT; ++spins)
+      for (uint32_t spins = 0; tw_load(&st->cnt[pass]) < expect + bump && spins < a.spin_limit;
+           ++spins)
         __builtin_amdgcn_s_sleep(2);
     }
     __syncthreads();
@@ -138,9 +155,9 @@ __global__ __launch_bounds__(TK_NT) void topk_wide_kernel(TwKP a) {
         csum += h[e];
       }
       incl = tk_block_incl_scan(csum, wtmp[0], tot);
-      if (tot == expect) break;
-      if (spins >= TW_SPIN_LIMIT) {
-        if (tid == 0) __hip_atomic_store(&st->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tot == expect + bump) break;
+      if (spins >= a.spin_limit) {
+        if (tid == 0) give_up();
         return;
       }
       __builtin_amdgcn_s_sleep(2);
@@ -188,15 +205,15 @@ __global__ __launch_bounds__(TK_NT) void topk_wide_kernel(TwKP a) {
   // counts of the chunks before this one
   uint32_t gb = 0, eb = 0, bad = 0;
   for (int64_t x = tid; x < c; x += TK_NT) {
-    uint64_t v = tw_load64(&slots[x]);
+    uint64_t v = bump ? 0 : tw_load64(&slots[x]);
     uint32_t spins = 0;
-    while (v == 0 && ++spins <= TW_SPIN_LIMIT) {
+    while (v == 0 && ++spins <= a.spin_limit) {
       __builtin_amdgcn_s_sleep(2);
-      v = tw_load64(&slots[x]);
+      v = bump ? 0 : tw_load64(&slots[x]);
     }
     if (v == 0) {
       bad = 1;
-      __hip_atomic_store(&st->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      give_up();
     } else {
       gb += (uint32_t)v;
       eb += (uint32_t)(v >> 32) - 1u;
@@ -281,6 +298,25 @@ __global__ __launch_bounds__(256) void tw_clear_kernel(uint4 *p, int64_t n16) {
     p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
+// After every batch (and the sort of a sorted selection): rows whose wait ran
+// out get -1 ids, -inf values and count -1, and the device status word
+// records the timeout.  One workgroup per row.
+__global__ __launch_bounds__(256) void tw_finish_kernel(TopkKParams p, const int32_t *row_err) {
+  const int64_t gi = blockIdx.x;
+  if (row_err[gi] == 0) return;
+  const TkRow rw = tk_row(p, gi);
+  int32_t *oi = p.out_idx + rw.orow * p.width;
+  for (int64_t x = threadIdx.x; x < p.width; x += 256) oi[x] = -1;
+  if (p.out_val)
+    for (int64_t x = threadIdx.x; x < p.width; x += 256)
+      p.out_val[rw.orow * p.width + x] = __int_as_float(0xff800000);
+  if (threadIdx.x == 0) {
+    if (p.out_count) p.out_count[rw.orow] = -1;
+    __hip_atomic_fetch_or(&la_dev_status, (uint32_t)LA_DEV_TOPK_TIMEOUT, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 // Workgroups of the wide kernel one device holds at once (0: no cooperative
@@ -309,6 +345,7 @@ WidePlan wide_plan(const TopkKParams &p) {
   // without cooperative launch, and tested against the same oracle)
   const char *env = getenv("LA_TOPK_WIDE");
   if (env && env[0] == '0') return W;
+  W.plain = env && strcmp(env, "plain") == 0;
   const int64_t cap = wide_capacity();
   W.C = ceil_div(p.n, TW_CHUNK);
   if (cap <= 0 || W.C > cap || p.n >= ((int64_t)1 << 31)) {
@@ -317,7 +354,7 @@ WidePlan wide_plan(const TopkKParams &p) {
   }
   W.R = std::min(p.NG, cap / W.C);
   W.state_bytes = align256(W.R * (int64_t)sizeof(TwRowState)) + align256(W.R * W.C * 8);
-  W.bytes = W.state_bytes;
+  W.bytes = W.state_bytes + align256(p.NG * 4);
   if (p.order == 0) W.bytes += align256(p.NG * p.k * 8) + align256(p.NG * p.k * 4);
   return W;
 }
@@ -330,32 +367,77 @@ int topk_wide_launch(const TopkKParams &p, const WidePlan &W, void *ws, hipStrea
   a.state = (TwRowState *)base;
   a.slots = (uint64_t *)(base + align256(W.R * (int64_t)sizeof(TwRowState)));
   a.C = W.C;
+  a.row_err = (int32_t *)(base + W.state_bytes);
+  const int64_t err_bytes = align256(p.NG * 4);
   if (p.order == 0) {
-    a.cand_sc = (double *)(base + W.state_bytes);
-    a.cand_id = (int32_t *)(base + W.state_bytes + align256(p.NG * p.k * 8));
+    a.cand_sc = (double *)(base + W.state_bytes + err_bytes);
+    a.cand_id = (int32_t *)(base + W.state_bytes + err_bytes + align256(p.NG * p.k * 8));
+  }
+  // wait limits: LA_TOPK_WIDE_SPIN polls (default 2^20); LA_TOPK_WIDE_FAULT=1
+  // makes every wait unsatisfiable (tests of the timeout path)
+  a.spin_limit = TW_SPIN_LIMIT;
+  if (const char *e = getenv("LA_TOPK_WIDE_SPIN")) a.spin_limit = (uint32_t)strtoul(e, nullptr, 10);
+  if (const char *e = getenv("LA_TOPK_WIDE_FAULT")) a.unreachable = e[0] == '1' ? 1u : 0u;
+  // the row flags once, then the state of each batch
+  {
+    const int64_t n16 = (W.state_bytes + err_bytes) / 16;
+    tw_clear_kernel<<<(unsigned)std::min<int64_t>(ceil_div(n16, 256), 1024), 256, 0, st>>>(
+        (uint4 *)base, n16);
+    LA_LAUNCHED();
   }
   const int64_t n16 = W.state_bytes / 16;
   const unsigned clear_grid = (unsigned)std::min<int64_t>(ceil_div(n16, 256), 1024);
   for (int64_t row0 = 0; row0 < p.NG; row0 += W.R) {
     const int64_t rows = std::min(W.R, p.NG - row0);
-    tw_clear_kernel<<<clear_grid, 256, 0, st>>>((uint4 *)base, n16);
-    LA_LAUNCHED();
+    if (row0 > 0) {
+      tw_clear_kernel<<<clear_grid, 256, 0, st>>>((uint4 *)base, n16);
+      LA_LAUNCHED();
+    }
     a.row0 = row0;
-    void *args[] = {&a};
-    LA_HIP(hipLaunchCooperativeKernel((const void *)topk_wide_kernel,
-                                      dim3((unsigned)W.C, (unsigned)rows), dim3(TK_NT), args, 0,
-                                      st));
+    const dim3 grid((unsigned)W.C, (unsigned)rows);
+    if (W.plain) {
+      // LA_TOPK_WIDE=plain: an ordinary launch of the same grid (it fits the
+      // device at once, but residency is not guaranteed: a wait that runs out
+      // is reported as above).  For profilers that cannot follow a
+      // cooperative launch.
+      topk_wide_kernel<<<grid, TK_NT, 0, st>>>(a);
+      LA_LAUNCHED();
+    } else {
+      void *args[] = {&a};
+      LA_HIP(hipLaunchCooperativeKernel((const void *)topk_wide_kernel, grid, dim3(TK_NT), args,
+                                        0, st));
+    }
   }
-  if (p.order == 1) return LA_OK;
-  // sorted output: order the K winners of each row by (score desc, index asc)
-  TopkKParams f = p;
-  f.scores = a.cand_sc;
-  f.row_stride = p.k;
-  f.n = p.k;
-  f.pos_unit = 0;
-  f.n_valid_tab = nullptr;
-  f.cand_idx = a.cand_id;
-  return topk_launch(f, st);
+  if (p.order == 0) {
+    // sorted output: order the K winners of each row by (score desc, index asc)
+    TopkKParams f = p;
+    f.scores = a.cand_sc;
+    f.row_stride = p.k;
+    f.n = p.k;
+    f.pos_unit = 0;
+    f.n_valid_tab = nullptr;
+    f.cand_idx = a.cand_id;
+    const int rc = topk_launch(f, st);
+    if (rc != LA_OK) return rc;
+  }
+  tw_finish_kernel<<<dim3((unsigned)p.NG), 256, 0, st>>>(p, a.row_err);
+  LA_LAUNCHED();
+  return LA_OK;
 }
 
 }  // namespace la
+
+using namespace la;
+
+extern "C" int la_device_status(uint32_t *bits, int32_t clear, void *stream) {
+  LA_REQUIRE(bits != nullptr, "la_device_status: null pointer");
+  LA_HIP(hipStreamSynchronize((hipStream_t)stream));
+  LA_HIP(hipMemcpyFromSymbol(bits, HIP_SYMBOL(la_dev_status), sizeof(uint32_t), 0,
+                             hipMemcpyDeviceToHost));
+  if (clear) {
+    const uint32_t zero = 0;
+    LA_HIP(hipMemcpyToSymbol(HIP_SYMBOL(la_dev_status), &zero, sizeof(uint32_t), 0,
+                             hipMemcpyHostToDevice));
+  }
+  return LA_OK;
+}

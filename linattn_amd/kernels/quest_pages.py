@@ -113,9 +113,12 @@ def page_scores_hip(q: torch.Tensor, mins: torch.Tensor, maxs: torch.Tensor,
 
 def _topk(scores: torch.Tensor, *, k: int, width: int, group: int, order: int,
           pos_offset: int, pos_unit: int, force_own: bool, with_values: bool = False,
-          sink: int = 0, window: int = 0):
+          sink: int = 0, window: int = 0, n_valid: Optional[torch.Tensor] = None):
     B, H, Tq, n = scores.shape
     dev = scores.device
+    if n_valid is not None and (n_valid.dtype != torch.int32 or n_valid.shape != (Tq,)
+                                or not n_valid.is_contiguous()):
+        raise ValueError("n_valid must be contiguous int32 (Tq,)")
     ids = torch.empty(B, H // group, Tq, width, dtype=torch.int32, device=dev)
     counts = torch.empty(B, H // group, Tq, dtype=torch.int32, device=dev)
     vals = torch.empty(B, H, Tq, width, dtype=torch.float32, device=dev) if with_values else None
@@ -127,6 +130,7 @@ def _topk(scores: torch.Tensor, *, k: int, width: int, group: int, order: int,
     a.sink_units, a.window_units = sink, window
     a.pos_offset, a.pos_unit = pos_offset, pos_unit
     a.force_own, a.order = int(force_own), order
+    a.n_valid = N.ptr(n_valid)
     L = N.load()
     ws_bytes = L.la_topk_rows_workspace(ctypes.byref(a))
     ws = N.workspace(ws_bytes, dev)

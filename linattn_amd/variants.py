@@ -271,6 +271,11 @@ class HipDSA(HipAttention):
         extra = torch.cat([sink.expand(B, H, tq, -1), win.expand(B, H, tq, -1)], dim=-1)
         allv = torch.cat([sel, extra], dim=-1)
         allv = torch.where((allv >= 0) & (allv < t_k), allv, torch.full_like(allv, -1))
+        # effective_mask's fallback (selection.py:100-107): a row with no
+        # causal entry reads the query's own token (clamped to the last key)
+        own = pos.clamp(max=t_k - 1).expand(B, H, tq, 1)
+        empty = ~((allv >= 0) & (allv <= pos)).any(-1, keepdim=True)
+        allv = torch.cat([allv, torch.where(empty, own, torch.full_like(own, -1))], dim=-1)
         allv = allv.sort(dim=-1).values
         dup = torch.zeros_like(allv, dtype=torch.bool)
         dup[..., 1:] = allv[..., 1:] == allv[..., :-1]

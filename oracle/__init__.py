@@ -49,7 +49,7 @@ __all__ = [
     "window_mask",
     "fp8_quantize",
     "fp8_decode",
-    "bf16_round",
+    "effective_mask",
     "to_f64",
 ]
 
@@ -111,14 +111,6 @@ def to_f64(x) -> np.ndarray:
     except ImportError:  # pragma: no cover
         pass
     return np.asarray(x, dtype=np.float64)
-
-
-def bf16_round(x: np.ndarray) -> np.ndarray:
-    """Round fp32/fp64 values to bf16 (nearest-even) and return them as fp64."""
-    f = np.asarray(x, dtype=np.float32)
-    u = f.view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
-    return (u.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
 # ------------------------------------------------------------------- core --
@@ -603,6 +595,21 @@ def window_mask(t_q: int, t_k: int, offset: int, window: int, sink: int) -> np.n
     qi = np.arange(t_q)[:, None] + offset
     kj = np.arange(t_k)[None, :]
     return (kj <= qi) & (((qi - kj) < window) | (kj < sink))
+
+
+def effective_mask(select: np.ndarray, offset: int = 0) -> np.ndarray:
+    """BlockSelectionAttention.effective_mask (selection.py:86-108): the
+    selection (..., Tq, Tk) intersected with causality (key j <= offset + t);
+    a row left with no key reads the query's own token, position offset + t
+    clamped to the last key (selection.py:100-107)."""
+    sel = np.asarray(select, dtype=bool)
+    tq, tk = sel.shape[-2:]
+    allow = sel & causal_mask(tq, tk, offset)
+    empty = ~allow.any(-1)
+    own = np.minimum(np.arange(tq) + offset, tk - 1)
+    fallback = np.zeros_like(allow)
+    fallback[..., np.arange(tq), own] = True
+    return allow | (fallback & empty[..., None])
 
 
 # -------------------------------------------------------------------- fp8 --

@@ -372,7 +372,8 @@ def test_config4_paged_quest_decode_full_size(dev, union):
     permuted page table, 2048-token budget with the last page forced.
     Every list is checked by properties on the GPU (own page present, sorted
     and unique, selected scores dominate unselected ones with the index tie
-    rule); two sequences are checked against the oracle bit for bit."""
+    rule), and every one of the 64 sequences against the oracle: page ids bit
+    for bit, outputs within 2e-3."""
     B, Hq, Hkv, T, D, ps, topk = 64, 32, 8, 65536, 128, 64, 32
     P = T // ps
     g = torch.Generator(device=dev).manual_seed(0)
@@ -411,17 +412,26 @@ def test_config4_paged_quest_decode_full_size(dev, union):
         got = torch.zeros(B, Hq, P, dtype=torch.bool, device=dev)
         got.scatter_(-1, ids.squeeze(2).long(), True)
         assert torch.equal(got, want)
-    # two sequences against the oracle
+    # the page bounds of two sequences against the oracle (two KV heads each)
     for b in (0, 37):
-        qb = q[b:b + 1].cpu()
-        mb, xb = mins[b:b + 1].cpu(), maxs[b:b + 1].cpu()
-        rid = oracle.quest_select(qb, mb, xb, page_size=ps, topk=topk, offset=T - 1,
-                                  gqa_union=union)
-        assert np.array_equal(ids[b:b + 1].cpu().numpy(), rid)
-        kb = pool_k[pt[b].long()].permute(1, 0, 2, 3).reshape(1, Hkv, T, D).cpu()
-        vb = pool_v[pt[b].long()].permute(1, 0, 2, 3).reshape(1, Hkv, T, D).cpu()
-        om, ox = oracle.page_bounds(kb[:, :2], ps)
-        assert np.array_equal(oracle.to_f64(mb[:, :2]), om)
-        assert np.array_equal(oracle.to_f64(xb[:, :2]), ox)
-        ref = oracle.attend_lists(qb, kb, vb, rid, unit=ps, causal=True, offset=T - 1)
-        assert np.abs(out[b:b + 1].cpu().double().numpy() - ref).max() < 2e-3
+        kb = pool_k[pt[b].long(), :2].permute(1, 0, 2, 3).reshape(1, 2, T, D).cpu()
+        om, ox = oracle.page_bounds(kb, ps)
+        assert np.array_equal(oracle.to_f64(mins[b:b + 1, :2].cpu()), om)
+        assert np.array_equal(oracle.to_f64(maxs[b:b + 1, :2].cpu()), ox)
+    # every sequence against the oracle: its selected pages gathered into a
+    # compact pool, addressed through a remapped page table
+    ids_h, out_h = ids.cpu().numpy(), out.cpu().double().numpy()
+    mins_h, maxs_h, q_h = mins.cpu(), maxs.cpu(), q.cpu()
+    pt_h = pt.cpu().long()
+    for b in range(B):
+        rid = oracle.quest_select(q_h[b:b + 1], mins_h[b:b + 1], maxs_h[b:b + 1], page_size=ps,
+                                  topk=topk, offset=T - 1, gqa_union=union)
+        assert np.array_equal(ids_h[b:b + 1], rid), b
+        sel = np.unique(rid[rid >= 0])
+        phys = pt_h[b, torch.from_numpy(sel).long()]
+        ck, cv = pool_k[phys.to(dev)].cpu(), pool_v[phys.to(dev)].cpu()
+        cpt = np.zeros((1, P), dtype=np.int32)
+        cpt[0, sel] = np.arange(sel.size, dtype=np.int32)
+        ref = oracle.attend_lists(q_h[b:b + 1], ck, cv, rid, unit=ps, causal=True, offset=T - 1,
+                                  page_table=cpt, page_size=ps)
+        assert np.abs(out_h[b:b + 1] - ref).max() < 2e-3, b

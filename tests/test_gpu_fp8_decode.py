@@ -89,8 +89,9 @@ def test_fp8_indexer_decode_mid_sequence(dev):
 
 def test_config5_fp8_decode_full_size(dev):
     """C5: batch 16, context 131072, 64-token pages, 32/8 heads, D=128, fp8 KV,
-    indexer (4 x 64, bf16) top-4096.  All lists checked for structure, one
-    sequence against the oracle."""
+    indexer (4 x 64, bf16) top-4096.  All lists checked for structure, and
+    every one of the 16 sequences against the oracle: token ids bit for bit,
+    outputs within 1e-2 of the fp8-dequantised attention."""
     B, Hq, Hkv, T, D, ps, HI, d, topk = 16, 32, 8, 131072, 128, 64, 4, 64, 4096
     x = c5_inputs(B, Hq, Hkv, T, D, ps, HI, d, seed=0, dev=dev)
     q, kc, vc, ks, vs, pt, q_idx, k_idx, w = x
@@ -101,18 +102,19 @@ def test_config5_fp8_decode_full_size(dev):
     s = idx.sort(-1).values
     assert (s[..., 1:] > s[..., :-1]).all()
     assert torch.isfinite(out).all()
-    # the oracle on one sequence (its pages only, to bound host memory)
-    b = 5
-    sel_pages = torch.unique(pt[b]).long()
-    remap = torch.full((kc.shape[0],), -1, dtype=torch.int32, device=dev)
-    remap[sel_pages] = torch.arange(sel_pages.numel(), dtype=torch.int32, device=dev)
-    pt_b = remap[pt[b].long()].view(1, -1)
-    ri = oracle.indexer_topk(q_idx[b:b + 1].cpu(), k_idx[b:b + 1].cpu(), w[b:b + 1].cpu(), topk,
-                             causal=True, offset=T - 1)[1]
-    assert np.array_equal(idx[b:b + 1].cpu().numpy(), index_order(ri))
-    ids = np.broadcast_to(ri.reshape(1, 1, 1, -1), (1, Hkv, 1, topk))
-    ref = oracle.attend_lists(q[b:b + 1].cpu(), kc[sel_pages].cpu(), vc[sel_pages].cpu(), ids,
-                              unit=1, causal=True, offset=T - 1, page_table=pt_b.cpu().numpy(),
-                              page_size=ps, k_scale=ks[sel_pages].cpu(),
-                              v_scale=vs[sel_pages].cpu())
-    assert np.abs(out[b:b + 1].cpu().double().numpy() - ref).max() < 1e-2
+    # the oracle on every sequence (its pages only, to bound host memory)
+    idx_h, out_h = idx.cpu().numpy(), out.cpu().double().numpy()
+    for b in range(B):
+        sel_pages = torch.unique(pt[b]).long()
+        remap = torch.full((kc.shape[0],), -1, dtype=torch.int32, device=dev)
+        remap[sel_pages] = torch.arange(sel_pages.numel(), dtype=torch.int32, device=dev)
+        pt_b = remap[pt[b].long()].view(1, -1)
+        ri = oracle.indexer_topk(q_idx[b:b + 1].cpu(), k_idx[b:b + 1].cpu(), w[b:b + 1].cpu(),
+                                 topk, causal=True, offset=T - 1)[1]
+        assert np.array_equal(idx_h[b:b + 1], index_order(ri)), b
+        ids = np.broadcast_to(ri.reshape(1, 1, 1, -1), (1, Hkv, 1, topk))
+        ref = oracle.attend_lists(q[b:b + 1].cpu(), kc[sel_pages].cpu(), vc[sel_pages].cpu(),
+                                  ids, unit=1, causal=True, offset=T - 1,
+                                  page_table=pt_b.cpu().numpy(), page_size=ps,
+                                  k_scale=ks[sel_pages].cpu(), v_scale=vs[sel_pages].cpu())
+        assert np.abs(out_h[b:b + 1] - ref).max() < 1e-2, b

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import oracle
+from linattn_amd import _native as N
 from linattn_amd.kernels.quest_pages import _topk
 
 pytestmark = pytest.mark.gpu
@@ -52,6 +53,61 @@ def test_topk_long_rows_segmented_fallback(dev, monkeypatch, order):
     got = ids[0, 0].cpu().numpy()
     want = ref_i if order == 0 else np.sort(ref_i, axis=-1)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("order", [1, 0])
+def test_topk_wide_many_batches_short_prefixes(dev, order):
+    """The multi-workgroup kernel over more rows than one cooperative launch
+    holds (300 rows of 65536 keys go in several batches), with valid prefixes
+    shorter than k, equal to k and in between; ascending-index (order 1) and
+    sorted (order 0) output.  The device status stays clean."""
+    n, k, Tq = 65536, 3000, 300
+    g = torch.Generator().manual_seed(11)
+    sc = torch.randint(-50, 50, (1, 1, Tq, n), generator=g).double()
+    sc[0, 0, ::3] = torch.randn(Tq // 3, n, generator=g, dtype=torch.float64)
+    nv = torch.randint(k, n + 1, (Tq,), generator=g).to(torch.int32)
+    nv[:6] = torch.tensor([1, 100, k - 1, k, k + 1, 2 * k], dtype=torch.int32)
+    N.device_status(dev)
+    ids, counts, _ = _topk(sc.to(dev), k=k, width=k, group=1, order=order, pos_offset=0,
+                           pos_unit=0, force_own=False, n_valid=nv.to(dev))
+    assert N.device_status(dev) == 0
+    ri, _ = oracle.topk_rows(sc[0, 0].numpy(), k, n_valid=nv.numpy())
+    want = ri if order == 0 else np.sort(np.where(ri < 0, n, ri), axis=-1)
+    if order == 1:
+        want = np.where(want == n, -1, want)
+    assert np.array_equal(ids[0, 0].cpu().numpy(), want)
+    assert np.array_equal(counts[0, 0].cpu().numpy(), np.minimum(nv.numpy(), k))
+
+
+@pytest.mark.parametrize("order", [1, 0])
+def test_topk_wide_timeout_is_reported(dev, monkeypatch, order):
+    """A bounded wait that runs out must not pass for a result.  With
+    LA_TOPK_WIDE_FAULT=1 no wait of the multi-workgroup kernel can be
+    satisfied, and with LA_TOPK_WIDE_SPIN=64 each gives up after 64 polls, so
+    every workgroup exits normally: every row comes back with count -1 and -1
+    ids, and the device status carries LA_DEV_TOPK_TIMEOUT.  The next call
+    without the fault is correct again."""
+    n, k, Tq = 65536, 1000, 4
+    g = torch.Generator().manual_seed(12)
+    sc = torch.randn(1, 1, Tq, n, generator=g, dtype=torch.float64).to(dev)
+    N.device_status(dev)
+    monkeypatch.setenv("LA_TOPK_WIDE_FAULT", "1")
+    monkeypatch.setenv("LA_TOPK_WIDE_SPIN", "64")
+    ids, counts, vals = _topk(sc, k=k, width=k, group=1, order=order, pos_offset=0, pos_unit=0,
+                              force_own=False, with_values=order == 0)
+    assert N.device_status(dev) & N.LA_DEV_TOPK_TIMEOUT
+    assert (counts == -1).all() and (ids == -1).all()
+    if order == 0:
+        assert torch.isneginf(vals).all()
+    monkeypatch.delenv("LA_TOPK_WIDE_FAULT")
+    monkeypatch.delenv("LA_TOPK_WIDE_SPIN")
+    ids, counts, _ = _topk(sc, k=k, width=k, group=1, order=order, pos_offset=0, pos_unit=0,
+                           force_own=False)
+    assert N.device_status(dev) == 0
+    ri, _ = oracle.topk_rows(sc[0, 0].cpu().numpy(), k)
+    want = ri if order == 0 else np.sort(ri, axis=-1)
+    assert np.array_equal(ids[0, 0].cpu().numpy(), want)
+    assert (counts == k).all()
 
 
 def test_topk_short_rows_pad(dev):

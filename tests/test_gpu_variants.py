@@ -136,6 +136,31 @@ def test_hip_dsa_matches_oracle(dev, ratio):
     assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
 
 
+def test_hip_dsa_empty_rows_read_own_token(dev):
+    """No sink and no window: early queries whose indexer top-k holds only
+    future keys fall back to their own token (effective_mask,
+    selection.py:100-107), and every output equals the oracle's attention
+    over oracle.effective_mask of the indexer selection."""
+    c = cfg(compress_ratio=1, window_size=0, sink_size=0, topk_tokens=4,
+            extras={"indexer_heads": 4, "indexer_dim": 16})
+    q, k, v = inputs(1, 4, 2, 96, 64, seed=15)
+    var = build("hip_dsa", c)
+    out, _, stats = var.forward(q.to(dev), k.to(dev), v.to(dev), chunk=96, collect_stats=True)
+    q_idx, k_idx, w = var.indexer_inputs(q.to(dev), k.to(dev))
+    H, T = 4, 96
+    _, idx = oracle.indexer_topk(q_idx.cpu(), k_idx.cpu(), w.cpu(), c.topk_tokens)
+    sel = np.zeros((1, H, T, T), dtype=bool)
+    for h in range(H):
+        for t in range(T):
+            sel[0, h, t, [x for x in idx[h, t] if x >= 0]] = True
+    mask = oracle.effective_mask(sel, offset=0)
+    empty = ~(sel & oracle.causal_mask(T, T, 0)).any(-1)
+    assert empty.sum() > 0  # the fallback is exercised
+    ref = oracle.dense_attention(q, k, v, mask=mask)
+    assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
+    assert abs(stats[0]["reads_per_query"] - mask.sum(-1).mean()) < 1e-9
+
+
 # ---------------------------------------------------------------- MoBA ----
 def moba_oracle(q, k, v, c, chunk):
     """MoBAAttention.forward (selection.py:610-640) chunk by chunk: routing

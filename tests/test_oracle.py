@@ -151,6 +151,108 @@ def test_attend_lists_causal_and_empty():
     assert np.array_equal(empty, np.zeros_like(empty))
 
 
+def _token_mask(ids, unit, tq, tk, offset, causal=True):
+    """Token mask of unit lists (B, L, Tq, N): the units' tokens below Tk,
+    intersected with causality."""
+    B, L = ids.shape[:2]
+    m = np.zeros((B, L, tq, tk), dtype=bool)
+    for b in range(B):
+        for h in range(L):
+            for t in range(tq):
+                for u in ids[b, h, t if ids.shape[2] > 1 else 0]:
+                    if u >= 0:
+                        m[b, h, t, u * unit:min(tk, (u + 1) * unit)] = True
+    if causal:
+        m &= oracle.causal_mask(tq, tk, offset)
+    return m
+
+
+def test_attend_lists_bf16_elements_match_dense():
+    """The bf16 element reader of attend_lists (raw 16-bit words) against
+    dense attention over the same values widened by torch, through the token
+    mask of the lists (GQA lists shared by two query heads)."""
+    r = rng(32)
+    B, Hq, Hkv, T, D, unit, Tq, off = 2, 4, 2, 48, 16, 8, 3, 30
+    k = torch.from_numpy(r.standard_normal((B, Hkv, T, D))).bfloat16()
+    v = torch.from_numpy(r.standard_normal((B, Hkv, T, D))).bfloat16()
+    q = torch.from_numpy(r.standard_normal((B, Hq, Tq, D))).bfloat16()
+    # distinct units per row (a repeated unit would be attended twice), one
+    # of them visible, some slots empty
+    ids = np.stack([np.stack([np.stack([np.r_[3, r.choice([0, 1, 2, 4, 5], 2, replace=False)]
+                                        for _ in range(Tq)]) for _ in range(Hkv)])
+                    for _ in range(B)])
+    ids[r.random(ids.shape) < 0.2] = -1
+    ids[..., 0] = 3
+    got = oracle.attend_lists(q, k, v, ids, unit=unit, causal=True, offset=off)
+    mask = np.repeat(_token_mask(ids, unit, Tq, T, off), Hq // Hkv, axis=1)
+    ref = oracle.dense_attention(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                                 mask=mask)
+    assert np.abs(got - ref).max() < 1e-12
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_attend_lists_fp8_elements_match_dequantised_dense(paged):
+    """The fp8 reader of attend_lists (e4m3fn codes times the per-token K and
+    V scales) against dense attention over K and V dequantised by torch,
+    code.float() * scale (kv/quant.py:105-109), contiguous and through a
+    page table."""
+    r = rng(33)
+    B, Hq, Hkv, T, D, ps, Tq, off = 2, 4, 2, 64, 16, 8, 2, 50
+    kf = torch.from_numpy(r.standard_normal((B, Hkv, T, D))).float() * 3
+    vf = torch.from_numpy(r.standard_normal((B, Hkv, T, D))).float()
+    ks = kf.abs().amax(-1, keepdim=True).clamp_min(1e-8) / 448.0
+    vs = vf.abs().amax(-1, keepdim=True).clamp_min(1e-8) / 448.0
+    kc, vc = (kf / ks).to(torch.float8_e4m3fn), (vf / vs).to(torch.float8_e4m3fn)
+    # torch's own e4m3fn decode, times the scale in fp64 (exact: a 4-bit code
+    # mantissa times a 24-bit scale); the reference's fp32 product
+    # (kv/quant.py:105-109) rounds it to within 2^-24 relative
+    kd, vd = kc.to(torch.float64) * ks.double(), vc.to(torch.float64) * vs.double()
+    assert torch.allclose(kd.float(), kc.to(torch.float32) * ks, rtol=2.0 ** -23, atol=0)
+    q = torch.from_numpy(r.standard_normal((B, Hq, Tq, D)))
+    ids = np.stack([np.stack([np.stack([np.r_[1, r.choice(np.r_[0, 2:T // ps], 3, replace=False)]
+                                        for _ in range(Tq)]) for _ in range(Hkv)])
+                    for _ in range(B)])
+    ids[r.random(ids.shape) < 0.2] = -1
+    ids[..., 0] = 1
+    mask = np.repeat(_token_mask(ids, ps, Tq, T, off), Hq // Hkv, axis=1)
+    ref = oracle.dense_attention(q.numpy(), kd.double().numpy(), vd.double().numpy(), mask=mask)
+    if not paged:
+        got = oracle.attend_lists(q, kc, vc, ids, unit=ps, causal=True, offset=off,
+                                  k_scale=ks, v_scale=vs)
+    else:
+        P = T // ps
+        pt = r.permutation(B * P).reshape(B, P).astype(np.int32)
+        pk = torch.zeros(B * P, Hkv, ps, D, dtype=torch.float8_e4m3fn)
+        pv = torch.zeros_like(pk)
+        pks = torch.zeros(B * P, Hkv, ps)
+        pvs = torch.zeros(B * P, Hkv, ps)
+        for b in range(B):
+            for p in range(P):
+                sl = slice(p * ps, (p + 1) * ps)
+                pk[pt[b, p]], pv[pt[b, p]] = kc[b, :, sl], vc[b, :, sl]
+                pks[pt[b, p]], pvs[pt[b, p]] = ks[b, :, sl, 0], vs[b, :, sl, 0]
+        got = oracle.attend_lists(q, pk, pv, ids, unit=ps, causal=True, offset=off,
+                                  page_table=pt, page_size=ps, k_scale=pks, v_scale=pvs)
+    assert np.abs(got - ref).max() < 1e-12
+
+
+def test_effective_mask_fallback_reads_own_token():
+    """selection.py:100-107: a row whose selection is empty, or entirely in
+    the future, reads the query's own token; other rows are the selection
+    intersected with causality."""
+    sel = np.zeros((1, 1, 4, 6), dtype=bool)
+    sel[0, 0, 1, 5] = True          # only a future key (query 1 sits at 3)
+    sel[0, 0, 2, [0, 5]] = True     # one past key and one future key
+    m = oracle.effective_mask(sel, offset=2)
+    assert m[0, 0, 0].tolist() == [False, False, True, False, False, False]
+    assert m[0, 0, 1].tolist() == [False, False, False, True, False, False]
+    assert m[0, 0, 2].tolist() == [True, False, False, False, False, False]
+    assert m[0, 0, 3].tolist() == [False, False, False, False, False, True]
+    # past the last key, the own position clamps to it
+    m2 = oracle.effective_mask(np.zeros((1, 2), dtype=bool), offset=5)
+    assert m2.tolist() == [[False, True]]
+
+
 @pytest.mark.skipif(not REF_LIB.exists(), reason="reference C decode not built (oracle/_ref)")
 def test_attend_lists_matches_reference_c_decode():
     """The reference's own decode_attn.c (built from source into oracle/_ref)
@@ -272,6 +374,70 @@ def test_quest_full_budget_recovers_dense():
     out = oracle.attend_lists(q, k, v, ids, unit=ps, causal=True, offset=0)
     ref = oracle.dense_attention(q.numpy(), k.double().numpy(), v.double().numpy())
     assert np.abs(out - ref).max() < 1e-12
+
+
+def _page_select_bruteforce(q, mins, maxs, page_size, topk, offset):
+    """page_select_torch (quest_pages.py:58-78) spelled out per row: the bound
+    as an elementwise maximum summed by numpy, visibility and the own page of
+    selection.py:219-231, then a sort by (-score, page)."""
+    q, mins, maxs = (np.asarray(x, dtype=np.float64) for x in (q, mins, maxs))
+    B, Hq, Tq, D = q.shape
+    Hkv, P = mins.shape[1], mins.shape[2]
+    G = Hq // Hkv
+    k = max(1, min(topk, P))
+    scores = np.zeros((B, Hq, Tq, P))
+    ids = np.full((B, Hq, Tq, k), -1, dtype=np.int64)
+    for b in range(B):
+        for h in range(Hq):
+            for t in range(Tq):
+                pos = offset + t
+                qv = q[b, h, t][None, :]
+                bound = np.maximum(qv * mins[b, h // G], qv * maxs[b, h // G]).sum(-1)
+                own = min(pos // page_size, P - 1)
+                row = np.array([bound[p] if p * page_size <= pos else -math.inf
+                                for p in range(P)])
+                row[own] = math.inf
+                scores[b, h, t] = row
+                vis = [p for p in range(P) if p * page_size <= pos]
+                want = sorted(vis, key=lambda p: (-row[p], p))[:k]
+                ids[b, h, t, :len(want)] = want
+    return ids, scores
+
+
+def test_page_select_integer_inputs_bruteforce():
+    """oracle.page_select == brute force, exactly: small-integer q and keys
+    make every product and sum exact, and make ties frequent (the tie rule)."""
+    r = rng(30)
+    B, Hq, Hkv, T, D, ps = 2, 4, 2, 40, 6, 4
+    q = r.integers(-2, 3, size=(B, Hq, 5, D)).astype(np.float64)
+    k = r.integers(-3, 4, size=(B, Hkv, T, D)).astype(np.float64)
+    mins, maxs = oracle.page_bounds(k, ps)
+    for offset, topk in ((17, 3), (0, 2), (35, 20)):
+        ids, sc = oracle.page_select(q, mins, maxs, ps, topk, offset=offset)
+        want_ids, want_sc = _page_select_bruteforce(q, mins, maxs, ps, topk, offset)
+        assert np.array_equal(sc, want_sc), offset
+        assert np.array_equal(ids, want_ids), offset
+
+
+def test_page_select_real_inputs_own_page_per_query():
+    """Real-valued inputs: scores agree with the elementwise form to rounding,
+    the ids exactly; with Tq > 1 only entry (t, own(t)) of each row is +inf
+    (defect D1 of quest_pages.py:74-75 is not reproduced)."""
+    r = rng(31)
+    B, Hq, Hkv, T, D, ps, Tq, offset = 1, 4, 1, 64, 16, 8, 6, 20
+    q = r.standard_normal((B, Hq, Tq, D))
+    k = r.standard_normal((B, Hkv, T, D))
+    mins, maxs = oracle.page_bounds(k, ps)
+    ids, sc = oracle.page_select(q, mins, maxs, ps, 3, offset=offset)
+    want_ids, want_sc = _page_select_bruteforce(q, mins, maxs, ps, 3, offset)
+    fin = np.isfinite(want_sc)
+    assert np.array_equal(fin, np.isfinite(sc))
+    assert np.allclose(sc[fin], want_sc[fin], rtol=0, atol=1e-12)
+    assert np.array_equal(ids, want_ids)
+    for t in range(Tq):
+        own = (offset + t) // ps
+        assert np.array_equal(np.isposinf(sc[0, :, t]).nonzero()[1], np.full(Hq, own))
+        assert ids[0, 0, t, 0] == own
 
 
 # ------------------------------------------------------------ indexer ----
