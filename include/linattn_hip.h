@@ -143,6 +143,22 @@ size_t la_sparse_attention_workspace(const la_sparse_attn_args *a, const la_kv *
 int la_sparse_attention(const la_sparse_attn_args *a, const la_kv *kv, void *stream);
 
 /*
+ * la_sparse_attention without any allocation and without a workspace
+ * argument: the split-K partials go to a static device array of
+ * LA_NOALLOC_MAX_WORKSPACE bytes that the library keeps on every device it
+ * runs on until the process ends (a->workspace / ws_bytes are ignored).
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Calls whose la_sparse_attention_workspace() exceeds the
+ * limit fail with LA_ERR_WORKSPACE before launching anything.  Every call on
+ * one device shares that device's array: calls that overlap in time on one
+ * device (other streams, other threads) race; the partials are written whole
+ * by each call, so nothing needs clearing between calls.
+ */
+#define LA_NOALLOC_MAX_WORKSPACE ((size_t)16 << 20)
+int la_sparse_attention_noalloc(const la_sparse_attn_args *a, const la_kv *kv, void *stream);
+
+/*
  * Quest page metadata: channel-wise min / max of the keys of every page.
  * Replaces page_bounds_torch / page_update_triton
  * (kernels/triton/quest_pages.py:38-48, 84-100, 134-142) and

@@ -26,6 +26,7 @@ EXPORTED = (
     "la_last_error",
     "la_sparse_attention_workspace",
     "la_sparse_attention",
+    "la_sparse_attention_noalloc",
     "la_quest_page_bounds",
     "la_quest_scores",
     "la_quest_select",
@@ -44,6 +45,7 @@ EXPORTED = (
 )
 
 LA_DEV_TOPK_TIMEOUT = 1
+NOALLOC_MAX_WORKSPACE = 16 << 20  # LA_NOALLOC_MAX_WORKSPACE
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -164,6 +166,7 @@ def load() -> ctypes.CDLL:
     L.la_sparse_attention_workspace.argtypes = [P(LaSparseAttnArgs), P(LaKV)]
     L.la_sparse_attention_workspace.restype = ctypes.c_size_t
     L.la_sparse_attention.argtypes = [P(LaSparseAttnArgs), P(LaKV), _vp]
+    L.la_sparse_attention_noalloc.argtypes = [P(LaSparseAttnArgs), P(LaKV), _vp]
     L.la_quest_page_bounds.argtypes = [P(LaKV), _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp,
                                        _i64, _i64, _i64, _i64, _i32, _vp]
     L.la_quest_scores.argtypes = [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp,

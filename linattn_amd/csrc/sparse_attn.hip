@@ -17,6 +17,8 @@
 #include <algorithm>
 #include <cstdlib>
 
+#include <mutex>
+
 #include "common.h"
 #include "kv_access.h"
 
@@ -883,16 +885,11 @@ extern "C" size_t la_sparse_attention_workspace(const la_sparse_attn_args *a, co
   return pl.ws;
 }
 
-extern "C" int la_sparse_attention(const la_sparse_attn_args *a, const la_kv *kv, void *stream) {
-  Plan pl{};
-  int rc = plan_attn(a, kv, pl);
-  if (rc != LA_OK) return rc;
-  if (pl.ws > 0) {
-    LA_REQUIRE(a->workspace != nullptr, "sparse attention: workspace required");
-    if ((size_t)a->ws_bytes < pl.ws)
-      return fail(LA_ERR_WORKSPACE, "sparse attention: workspace %lld < %zu bytes",
-                  (long long)a->ws_bytes, pl.ws);
-  }
+namespace la {
+
+// Launch of a planned attention with its split-K partials in `ws`.
+static int sparse_attention_run(const la_sparse_attn_args *a, const la_kv *kv, const Plan &pl,
+                                void *ws, hipStream_t st) {
   AttnKP p{};
   p.q = a->q;
   p.out = a->out;
@@ -926,10 +923,9 @@ extern "C" int la_sparse_attention(const la_sparse_attn_args *a, const la_kv *kv
   p.staged = kv->page_table ? (kv->page_size % a->unit == 0) : 0;
   p.unit_shift = is_pow2(a->unit) ? ilog2(a->unit) : -1;
   if (pl.splits > 1) {
-    p.ws_ml = (float *)a->workspace;
+    p.ws_ml = (float *)ws;
     p.ws_acc = p.ws_ml + pl.R * pl.G * pl.splits * 2;
   }
-  hipStream_t st = (hipStream_t)stream;
   switch (kv->dtype) {
     case LA_F32: return dispatch_d<LA_F32>(p, a->D, pl.G, st);
     case LA_BF16: return dispatch_d<LA_BF16>(p, a->D, pl.G, st);
@@ -938,4 +934,65 @@ extern "C" int la_sparse_attention(const la_sparse_attn_args *a, const la_kv *kv
       return dispatch_d<LA_FP8_E4M3>(p, a->D, pl.G, st);
     default: return fail(LA_ERR_INVALID, "KV dtype");
   }
+}
+
+// Static scratch of the allocation-free entry point: one array per device,
+// held until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is only a stand-in for the symbol): the
+// device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t LA_NOALLOC_SCRATCH = LA_NOALLOC_MAX_WORKSPACE;
+__device__ __align__(256) unsigned char scratch[LA_NOALLOC_SCRATCH];
+
+constexpr int LA_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[LA_MAX_DEVICES];
+
+// Device address of this device's scratch (looked up on its first use, with
+// that device current).
+static int scratch_ptr(void **out) {
+  int dev = 0;
+  LA_HIP(hipGetDevice(&dev));
+  LA_REQUIRE(dev >= 0 && dev < LA_MAX_DEVICES, "sparse attention (no-alloc): device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    LA_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    LA_REQUIRE(ptr != nullptr, "sparse attention (no-alloc): no scratch address");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return LA_OK;
+}
+
+}  // namespace la
+
+extern "C" int la_sparse_attention(const la_sparse_attn_args *a, const la_kv *kv, void *stream) {
+  Plan pl{};
+  int rc = plan_attn(a, kv, pl);
+  if (rc != LA_OK) return rc;
+  if (pl.ws > 0) {
+    LA_REQUIRE(a->workspace != nullptr, "sparse attention: workspace required");
+    if ((size_t)a->ws_bytes < pl.ws)
+      return fail(LA_ERR_WORKSPACE, "sparse attention: workspace %lld < %zu bytes",
+                  (long long)a->ws_bytes, pl.ws);
+  }
+  return sparse_attention_run(a, kv, pl, a->workspace, (hipStream_t)stream);
+}
+
+extern "C" int la_sparse_attention_noalloc(const la_sparse_attn_args *a, const la_kv *kv,
+                                           void *stream) {
+  Plan pl{};
+  int rc = plan_attn(a, kv, pl);
+  if (rc != LA_OK) return rc;
+  if (pl.ws > LA_NOALLOC_SCRATCH)
+    return fail(LA_ERR_WORKSPACE,
+                "sparse attention (no-alloc): %zu bytes of split partials exceed the %zu-byte "
+                "static scratch (fewer splits, or la_sparse_attention with a workspace)",
+                pl.ws, LA_NOALLOC_SCRATCH);
+  void *ws = nullptr;
+  if (pl.ws > 0) {
+    rc = scratch_ptr(&ws);
+    if (rc != LA_OK) return rc;
+  }
+  return sparse_attention_run(a, kv, pl, ws, (hipStream_t)stream);
 }

@@ -77,7 +77,8 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: tor
                      page_table: Optional[torch.Tensor] = None, page_size: Optional[int] = None,
                      kv_len: Optional[torch.Tensor] = None, k_scale: Optional[torch.Tensor] = None,
                      v_scale: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-                     out_dtype: Optional[torch.dtype] = None, num_splits: int = 0) -> torch.Tensor:
+                     out_dtype: Optional[torch.dtype] = None, num_splits: int = 0,
+                     no_alloc: bool = False) -> torch.Tensor:
     """Attention of q over the units listed in ``ids``.
 
     q: (B, Hq, Tq, D).  k/v: contiguous (B, Hkv, T, D) or, with ``page_table``
@@ -86,7 +87,10 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: tor
     group) or L = Hq (one list per query head); entry u covers tokens
     [u*unit, (u+1)*unit); -1 entries are skipped.
     fp8 (float8_e4m3fn) K/V need fp32 per-token scales.
-    Returns (B, Hq, Tq, D) in ``out_dtype`` (default q.dtype)."""
+    Returns (B, Hq, Tq, D) in ``out_dtype`` (default q.dtype).
+    ``no_alloc`` runs la_sparse_attention_noalloc: no workspace is allocated
+    (the library's static per-device scratch holds the split partials; pass
+    ``out`` as well for a call that allocates nothing)."""
     dev = N.require_gpu(q, k, v, ids, counts, page_table, kv_len, k_scale, v_scale,
                         what="sparse_attention")
     if q.dim() != 4:
@@ -135,6 +139,10 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: tor
     a.out_dtype = N.dtype_code(out.dtype)
     a.causal = 1 if causal else 0
     L = N.load()
+    if no_alloc:
+        N.check(L.la_sparse_attention_noalloc(ctypes.byref(a), ctypes.byref(kv),
+                                              N.stream_handle(dev)), "sparse_attention(no_alloc)")
+        return out
     ws_bytes = L.la_sparse_attention_workspace(ctypes.byref(a), ctypes.byref(kv))
     ws = N.workspace(ws_bytes, dev)
     a.workspace = N.ptr(ws)
