@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 6
+#define LA_ABI_VERSION 7
 
 /* element types */
 enum {
@@ -47,7 +47,8 @@ enum {
 
 /* device status bits (la_device_status) */
 enum {
-  LA_DEV_TOPK_TIMEOUT = 1 /* a bounded wait of the multi-workgroup top-k ran out */
+  LA_DEV_TOPK_TIMEOUT = 1,  /* a bounded wait of the multi-workgroup top-k ran out */
+  LA_DEV_PREFILL_RANGE = 2  /* la_block_sparse_prefill met a finite |v| >= 2^22 (outputs inf) */
 };
 
 /* ABI version of the loaded library (LA_ABI_VERSION). */
@@ -468,13 +469,17 @@ typedef struct {
 int la_xattn_select(const la_xattn_select_args *a, void *stream);
 
 /*
- * Block-sparse causal prefill on the matrix cores (MFMA bf16, fp32 accumulate).
+ * Block-sparse causal prefill on the matrix cores (fp32 accumulate).
  * The executor of block_sparse_attention (block_sparse.py:80-163) for lists
  * shared by a whole query block: query block qb of head h attends the key
  * blocks ids[b][h][qb][0..count) of block_size 64 tokens, with the causal mask
  * j <= i applied in-kernel (the reference's selector applies it through the
  * token mask, selection.py:86-108).  q (B,Hq,T,128), k/v (B,Hkv,T,128) bf16;
- * out (B,Hq,T,128) in out_dtype (F32 or BF16).
+ * out (B,Hq,T,128) in out_dtype (F32 or BF16).  Scores by bf16 MFMA; the
+ * softmax weights and V enter the PV product as fp16 (V converted once into
+ * the workspace, each 64-token block scaled by a power of two that keeps it
+ * in fp16 range).  scale must be positive.  Workspace:
+ * la_block_sparse_prefill_workspace() bytes, 256-byte aligned.
  */
 typedef struct {
   const void *q;
@@ -483,6 +488,8 @@ typedef struct {
   void *out;
   const int32_t *ids;
   const int32_t *counts;
+  void *workspace;
+  int64_t ws_bytes;
   int64_t B, Hq, Hkv, T, D;
   int64_t q_sb, q_sh, q_st;
   int64_t k_sb, k_sh, k_st;
@@ -495,6 +502,7 @@ typedef struct {
   int32_t reserved;
 } la_prefill_args;
 
+size_t la_block_sparse_prefill_workspace(const la_prefill_args *a);
 int la_block_sparse_prefill(const la_prefill_args *a, void *stream);
 
 #ifdef __cplusplus

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -36,6 +36,7 @@ EXPORTED = (
     "la_indexer_topk",
     "la_block_select_workspace",
     "la_block_select",
+    "la_block_sparse_prefill_workspace",
     "la_block_sparse_prefill",
     "la_paged_kv_append",
     "la_gate_select_workspace",
@@ -45,6 +46,7 @@ EXPORTED = (
 )
 
 LA_DEV_TOPK_TIMEOUT = 1
+LA_DEV_PREFILL_RANGE = 2
 NOALLOC_MAX_WORKSPACE = 16 << 20  # LA_NOALLOC_MAX_WORKSPACE
 
 _vp = ctypes.c_void_p
@@ -136,6 +138,7 @@ class LaXattnSelectArgs(ctypes.Structure):
 
 class LaPrefillArgs(ctypes.Structure):
     _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp), ("ids", _vp), ("counts", _vp),
+                ("workspace", _vp), ("ws_bytes", _i64),
                 ("B", _i64), ("Hq", _i64), ("Hkv", _i64), ("T", _i64), ("D", _i64),
                 ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64), ("k_sb", _i64), ("k_sh", _i64),
                 ("k_st", _i64), ("v_sb", _i64), ("v_sh", _i64), ("v_st", _i64), ("o_sb", _i64),
@@ -181,6 +184,8 @@ def load() -> ctypes.CDLL:
     L.la_block_select_workspace.argtypes = [P(LaBlockSelectArgs)]
     L.la_block_select_workspace.restype = ctypes.c_size_t
     L.la_block_select.argtypes = [P(LaBlockSelectArgs), _vp]
+    L.la_block_sparse_prefill_workspace.argtypes = [P(LaPrefillArgs)]
+    L.la_block_sparse_prefill_workspace.restype = ctypes.c_size_t
     L.la_block_sparse_prefill.argtypes = [P(LaPrefillArgs), _vp]
     L.la_paged_kv_append.argtypes = [P(LaKvAppendArgs), _vp]
     L.la_gate_select_workspace.argtypes = [P(LaGateSelectArgs)]

@@ -17,6 +17,9 @@ void set_error(const char *fmt, ...);
 int fail(int code, const char *fmt, ...);
 // compute units of the current device (cached per thread and device)
 int num_cus();
+// Status bits of prefill.hip's kernels on the current device (read after the
+// caller synchronised), optionally cleared.
+int prefill_status(uint32_t *bits, bool clear);
 
 #define LA_REQUIRE(cond, ...)                               \
   do {                                                      \

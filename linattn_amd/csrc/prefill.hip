@@ -6,6 +6,19 @@
 // in-kernel on the diagonal block.  Head dim 128, bf16 inputs, fp32 accumulate,
 // online softmax in the log2 domain.
 //
+// Precision of the PV product: the weights P go to the matrix core as fp16
+// (11 significant bits; bf16's 8 alone err by up to 2^-9 of the largest weight,
+// which exceeds 2e-3 on rows whose mass sits on a few keys), and the row sum is
+// taken from the same rounded weights, so a rounding shared by every weight
+// cancels in the division.  V is therefore converted once to fp16 by
+// prefill_v16_kernel, each 64-token block scaled by a power of two 2^-e
+// (e = 0 unless the block's largest |v| reaches 2^15; e <= 7, so |v| < 2^22),
+// which keeps every bf16 value of magnitude >= 2^(e-17) exact.  The kernel
+// folds 2^e into the weights of that block (exp2(x + e): at most 2^15, still
+// an fp16) and weighs them by 2^-e in the row sum.  Blocks with |v| >= 2^22
+// raise LA_DEV_PREFILL_RANGE in the device status word (their fp16 copy
+// overflows to inf).
+//
 // Per workgroup: 4 waves = 2 query halves (32 queries) x 2 key halves (32 of
 // every 64-key block).  Each listed key block's K and V (64 x 128, bf16) are
 // copied global -> LDS by the gfx950 LDS-DMA loads (global_load_lds_dwordx4),
@@ -29,6 +42,7 @@
 //                   so neither P nor V is shuffled.
 // Workgroups are remapped so that the query heads of one KV head and adjacent
 // query blocks run on the same XCD (shared L2 for their common key blocks).
+#include <algorithm>
 #include <climits>
 
 #include "common.h"
@@ -37,6 +51,10 @@ namespace la {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -51,16 +69,91 @@ constexpr int PF_BLK = PF_BS * PF_D;  // elements of one staged K or V block (16
 // transpose reads: 8 rows x 2 chunks per 32 lanes).
 __device__ __forceinline__ int pf_swz(int r) { return (2 * (r & 7)) ^ ((r >> 3) & 1); }
 
+// IEEE maximum (NaN-propagating): gfx950 v_maximum3_f32 without the
+// canonicalising moves fmaxf needs in IEEE mode.
+__device__ __forceinline__ float pf_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float pf_pair16_max(float x) { const float2 p = pair16(x); return pf_max(p.x, p.y); }
+__device__ __forceinline__ float pf_pair32_max(float x) { const float2 p = pair32(x); return pf_max(p.x, p.y); }
+
+// Two wave-uniform 32-bit reads through the scalar cache, waited for together.
+__device__ __forceinline__ void sload2_i32(const int32_t *p0, const int32_t *p1, int32_t &a, int32_t &b) {
+  asm volatile("s_load_dword %0, %2, 0x0\n\ts_load_dword %1, %3, 0x0\n\ts_waitcnt lgkmcnt(0)"
+               : "=&s"(a), "=&s"(b) : "s"(p0), "s"(p1) : "memory");
+}
+
 struct PfKP {
-  const uint16_t *q, *k, *v;
+  const uint16_t *q, *k, *v;  // v: the fp16 copy (B, Hkv, T, 128), contiguous
+  const int32_t *vexp;        // (B, Hkv, nkb): V block kb holds v * 2^-vexp
   void *out;
   const int32_t *ids, *counts;
   int64_t B, Hq, Hkv, T;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
-  int64_t width, nqb;
-  float qscale;  // scale * log2(e)
+  int64_t width, nqb, nkb;
+  uint32_t k_blk, v_blk;  // elements between consecutive 64-token blocks of K / V
+  float qscale;   // scale * log2(e)
+  float thr_gap;  // 8 / qscale: raw-score headroom above the reference maximum
   int32_t causal, out_dt;
 };
+
+// Status bits this file's kernels raise on the current device (read through
+// la_device_status).
+__device__ uint32_t la_pf_status;
+
+// V (bf16, any strides with a unit stride over D) -> fp16, one workgroup per
+// 64-token block of one (b, KV head): e = min(7, max(0, E - 141)) for the
+// block's largest |v| with biased bf16 exponent E (so |v| * 2^-e < 2^15 when
+// E <= 148), then v16 = fp16(v * 2^-e), rounded to nearest even.  Rows past
+// T are not written.
+__global__ __launch_bounds__(256) void prefill_v16_kernel(const uint16_t *v, int64_t v_sb,
+                                                          int64_t v_sh, int64_t v_st, int64_t Hkv,
+                                                          int64_t T, int64_t nkb, uint16_t *v16,
+                                                          int32_t *vexp) {
+  __shared__ uint32_t wmax[4];
+  const int64_t blk = blockIdx.x;
+  const int64_t kb = blk % nkb, bh = blk / nkb;
+  const int64_t b = bh / Hkv, kvh = bh % Hkv;
+  const int tid = threadIdx.x;
+  const uint16_t *src = v + b * v_sb + kvh * v_sh;
+  uint16_t *dst = v16 + bh * T * PF_D;
+  u32x4 x[4];
+  uint32_t mx = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = kb * PF_BS + (tid >> 4) + 16 * i;
+    x[i] = row < T ? __builtin_nontemporal_load((const u32x4 *)(src + row * v_st + 8 * (tid & 15)))
+                   : u32x4{0u, 0u, 0u, 0u};
+    const uint32_t w[4] = {x[i][0], x[i][1], x[i][2], x[i][3]};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mx = max(mx, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
+  }
+  // |v| bit patterns order like the values (NaN above inf: e then saturates)
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+  if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+  __syncthreads();
+  mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  const int e = min(7, max(0, (int)(mx >> 7) - 141));
+  if (tid == 0) {
+    vexp[blk] = e;
+    if ((int)(mx >> 7) > 148 && mx < 0x7f80u)  // finite |v| >= 2^22 (inf and NaN pass through)
+      __hip_atomic_fetch_or(&la_pf_status, (uint32_t)LA_DEV_PREFILL_RANGE, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = kb * PF_BS + (tid >> 4) + 16 * i;
+    if (row >= T) continue;
+    const uint32_t w[4] = {x[i][0], x[i][1], x[i][2], x[i][3]};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = __builtin_amdgcn_ldexpf(bf16lo(w[j]), -e);
+      const float hi = __builtin_amdgcn_ldexpf(bf16hi(w[j]), -e);
+      o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+    }
+    *(uint4 *)(dst + row * PF_D + 8 * (tid & 15)) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
 
 __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // K slots 0..1, V slots 2..3 (64 KiB: two workgroups per CU); after the
@@ -83,14 +176,17 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   const int64_t h = kvh * G + hg;
 
   const int qh = w >> 1, kh = w & 1;  // query half, key half
+  const int qhu = __builtin_amdgcn_readfirstlane(qh), khu = __builtin_amdgcn_readfirstlane(kh);
+  const int T32 = (int)p.T, nkb32 = (int)p.nkb;
   int64_t q_row[2];                    // this lane's query in each 16-query group
   bf16x8 qreg[2][4];
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg) {
     q_row[qg] = qb * PF_BS + 32 * qh + 16 * qg + c16;
     const uint16_t *qp = p.q + b * p.q_sb + h * p.q_sh + min(q_row[qg], p.T - 1) * p.q_st;
+    // q is read once: streamed past the caches that keep the K/V blocks
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qreg[qg][s] = *(const bf16x8 *)(qp + 32 * s + 8 * g);
+    for (int s = 0; s < 4; ++s) qreg[qg][s] = __builtin_nontemporal_load((const bf16x8 *)(qp + 32 * s + 8 * g));
   }
   const int32_t *list = p.ids + ((b * p.Hq + h) * p.nqb + qb) * p.width;
   const int n = p.counts ? min((int)p.counts[(b * p.Hq + h) * p.nqb + qb], (int)p.width)
@@ -102,12 +198,10 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     if (p.out_dt == LA_BF16) {
       const bf16x2 x = __builtin_convertvector((f32x2{r[0], r[1]}), bf16x2);
       const bf16x2 y = __builtin_convertvector((f32x2{r[2], r[3]}), bf16x2);
-      uint2 u;
-      u.x = *(const uint32_t *)&x;
-      u.y = *(const uint32_t *)&y;
-      *(uint2 *)((uint16_t *)p.out + o) = u;
+      const u32x2 u = {__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, y)};
+      __builtin_nontemporal_store(u, (u32x2 *)((uint16_t *)p.out + o));
     } else {
-      *(f32x4 *)((float *)p.out + o) = r;
+      __builtin_nontemporal_store(r, (f32x4 *)((float *)p.out + o));
     }
   };
   if (n <= 0) {  // an empty list attends nothing: zero rows (n is workgroup-uniform)
@@ -122,7 +216,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 
   const uint16_t *kbh = p.k + b * p.k_sb + kvh * p.k_sh;
   const uint16_t *vbh = p.v + b * p.v_sb + kvh * p.v_sh;
-  auto whole_block = [&](int kb) { return kb >= 0 && (int64_t)kb * PF_BS + PF_BS <= p.T; };
+  const int32_t *vexp = p.vexp + (b * p.Hkv + kvh) * p.nkb;
+  auto whole_block = [&](int kb) { return kb >= 0 && kb * PF_BS + PF_BS <= T32; };
   // LDS slots of PF_BLK elements: K in 0..1, V in 2..3
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t *)smem);
   const int wu = __builtin_amdgcn_readfirstlane(w);
@@ -138,10 +233,11 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     kvo[t] = (uint32_t)((((int64_t)(16 * t + drow)) * p.k_st + 8 * dch) * 2);
     vvo[t] = (uint32_t)((((int64_t)(16 * t + drow)) * p.v_st + 8 * dch) * 2);
   }
-  auto dma_part = [&](const uint16_t *bh, int64_t st, const uint32_t (&vo)[4], int kb, int slot) {
+  auto dma_part = [&](const uint16_t *bh, int64_t st, uint32_t blk, const uint32_t (&vo)[4], int kb,
+                      int slot) {
     const uint32_t m0 = lds0 + 2 * (slot * PF_BLK + 4 * wu * PF_D);
     if (whole_block(kb)) {
-      const uint16_t *base = bh + (int64_t)kb * PF_BS * st;
+      const uint16_t *base = bh + (uint32_t)kb * blk;  // fits 32 bits (checked at launch)
 #pragma unroll
       for (int t = 0; t < 4; ++t)
         asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(vo[t]), "s"(base),
@@ -155,15 +251,15 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       }
     }
   };
-  auto dma_k = [&](int kb, int slot) { dma_part(kbh, p.k_st, kvo, kb, slot); };
-  auto dma_v = [&](int kb, int slot) { dma_part(vbh, p.v_st, vvo, kb, slot); };
+  auto dma_k = [&](int kb, int slot) { dma_part(kbh, p.k_st, p.k_blk, kvo, kb, slot); };
+  auto dma_v = [&](int kb, int slot) { dma_part(vbh, p.v_st, p.v_blk, vvo, kb, slot); };
   // rows of a landed partial block that lie past T (or all rows of a -1
   // entry) are cleared, so masked keys hold zeros rather than copies
   auto clear_rows = [&](int kb, int slot) {
     uint16_t *d = smem + slot * PF_BLK;
     for (int ch = tid; ch < PF_BS * 16; ch += PF_NT) {
       const int r = ch >> 4;
-      if (kb < 0 || (int64_t)kb * PF_BS + r >= p.T) *(uint4 *)(d + r * PF_D + 8 * (ch & 15)) = uint4{0, 0, 0, 0};
+      if (kb < 0 || kb * PF_BS + r >= T32) *(uint4 *)(d + r * PF_D + 8 * (ch & 15)) = uint4{0, 0, 0, 0};
     }
   };
 
@@ -198,8 +294,12 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     }
   };
 
-  // m: reference maximum of the raw (unscaled) scores of this lane's query, per group
-  float m[2] = {__int_as_float(0xff800000), __int_as_float(0xff800000)}, l[2] = {0.f, 0.f};
+  // m: reference maximum of the raw (unscaled) scores of this lane's query,
+  // per group; thr = m + thr_gap, the raw score above which m must be raised;
+  // nmu = -m * qscale (0 while m = -inf), the exponent offset of the weights
+  const float NEG_INF = __int_as_float(0xff800000);
+  float m[2] = {NEG_INF, NEG_INF}, thr[2] = {NEG_INF, NEG_INF}, l[2] = {0.f, 0.f};
+  float nmu[2] = {0.f, 0.f};
   f32x4 acc[2][8];
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg)
@@ -208,50 +308,56 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 
   // The mask of block kbx in this wave's key half: -inf on keys past the
   // causal diagonal or past T, and on every key of a -1 entry, written over
-  // the block's scores.  Only those blocks (diagonal, partial, empty: a
-  // wave-uniform branch) pay for it; keys and positions fit in int32
-  // (T < 2^30 is checked at launch).
-  auto apply_mask = [&](int kbx, f32x4 (&sc)[2][2]) {
-    const int key0 = kbx * PF_BS + 32 * kh;  // first key of this half
-    const bool need = kbx < 0 || (p.causal && key0 + 31 > (int)qb * PF_BS + 32 * qh) ||
-                      key0 + 32 > (int)p.T;
-    if (need) {
-#pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
-        const int last = min(p.causal ? (int)q_row[qg] : INT_MAX, (int)p.T - 1);
-        const int lim = kbx < 0 ? -1 : last - key0;  // keys past lim are masked
-#pragma unroll
-        for (int kt2 = 0; kt2 < 2; ++kt2)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (16 * kt2 + 4 * g + e > lim) sc[qg][kt2][e] = __int_as_float(0xff800000);
-      }
-    }
+  // the block's scores.  Only those blocks (diagonal, partial, empty) need it;
+  // keys and positions fit in int32 (T < 2^30 is checked at launch).
+  auto needs_mask = [&](int kbx) {
+    const int key0 = kbx * PF_BS + 32 * khu;  // first key of this half
+    return kbx < 0 || (p.causal && key0 + 31 > (int)qb * PF_BS + 32 * qhu) || key0 + 32 > T32;
   };
-  // Settle the reference maxima for a block's (masked) scores.  m is a
-  // reference maximum: it is raised (and l, acc rescaled) only when a row's
-  // maximum exceeds it by more than 2^8 in the exponent, so the weights stay
-  // below 256 and the rescale is rare; the final division by l is unchanged
-  // by the choice of reference.  Branch-free: l is scaled here, and the
-  // caller rescales acc by alpha when the result is true.  `valid` false
-  // leaves the state unchanged (scores of no block).
-  auto settle_max = [&](const f32x4 (&sc)[2][2], bool valid, float (&alpha)[2]) {
-    bool raise = false;
+  auto apply_mask = [&](int kbx, f32x4 (&sc)[2][2]) {
+    const int key0 = kbx * PF_BS + 32 * kh;
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      float mx = fmaxf(fmaxf(fmaxf(sc[qg][0][0], sc[qg][0][1]), fmaxf(sc[qg][0][2], sc[qg][0][3])),
-                       fmaxf(fmaxf(sc[qg][1][0], sc[qg][1][1]), fmaxf(sc[qg][1][2], sc[qg][1][3])));
-      mx = pair32_max(pair16_max(mx));
-      const float mn = fmaxf(m[qg], mx);
-      // (mn - m) is NaN while both are -inf: no raise.  Selects rather
-      // than branches (the exp is computed either way).
-      const bool up = (__ballot((mn - m[qg]) * p.qscale > 8.f) != 0) & valid;
-      alpha[qg] = fast_exp2(up ? (m[qg] - mn) * p.qscale : 0.f);  // 0 from m = -inf
-      m[qg] = up ? mn : m[qg];
-      l[qg] *= alpha[qg];
-      raise |= up;
+      const int last = min(p.causal ? (int)q_row[qg] : INT_MAX, T32 - 1);
+      const int lim = kbx < 0 ? -1 : last - key0;  // keys past lim are masked
+#pragma unroll
+      for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (16 * kt2 + 4 * g + e > lim) sc[qg][kt2][e] = NEG_INF;
     }
-    return raise;
+  };
+  // this lane's largest score of a block, per query group (v_max3 chains)
+  auto lane_max = [&](const f32x4 (&sc)[2][2], float (&mx)[2]) {
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg)
+      mx[qg] = pf_max(pf_max(pf_max(sc[qg][0][0], sc[qg][0][1]), pf_max(sc[qg][0][2], sc[qg][0][3])),
+                      pf_max(pf_max(sc[qg][1][0], sc[qg][1][1]), pf_max(sc[qg][1][2], sc[qg][1][3])));
+  };
+  // Settle the reference maxima for a block whose lane maxima are mx.  m is
+  // raised (and l, acc rescaled) only when some query's block maximum exceeds
+  // it by more than 2^8 in the exponent, so the weights stay below 256 (fp16
+  // holds them) and raises are rare; the final division by l is unchanged by
+  // the choice of reference.  The test is one compare per lane (any lane over
+  // its query's threshold); the exact column maximum (lane swaps) is formed
+  // only then.  alpha (the factor for acc) is returned through `alpha`.
+  auto settle_max = [&](float (&mx)[2], float (&alpha)[2]) {
+    bool any = false;
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      alpha[qg] = 1.f;
+      if (__ballot(mx[qg] > thr[qg]) != 0) {
+        const float cm = pf_pair32_max(pf_pair16_max(mx[qg]));
+        const float mn = pf_max(m[qg], cm);
+        alpha[qg] = (m[qg] == NEG_INF) ? 0.f : fast_exp2((m[qg] - mn) * p.qscale);
+        m[qg] = mn;
+        thr[qg] = mn + p.thr_gap;
+        nmu[qg] = (mn == NEG_INF) ? 0.f : -mn * p.qscale;
+        l[qg] *= alpha[qg];
+        any = true;
+      }
+    }
+    return any;
   };
   auto rescale_acc = [&](const float (&alpha)[2]) {
 #pragma unroll
@@ -261,14 +367,14 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   };
   // Software pipeline over the list.  Step j computes the scores of block
   // j+1 while the weights of block j are formed, then block j's PV product
-  // while the scores of block j+1 are masked and their maxima settled.  K
-  // block x lives in slot x % 2 and V block x in slot 2 + x % 2; both are
-  // fetched one step ahead (K of block j+2 and V of block j+1 during step j).
-  // List entries come through the scalar cache (see sload_i32).
-  const int kb = sload_i32(list);              // block 0
+  // while the maxima of block j+1 are taken.  K block x lives in slot x % 2
+  // and V block x in slot 2 + x % 2; both are fetched one step ahead (K of
+  // block j+2 and V of block j+1 during step j).  List entries and V block
+  // exponents come through the scalar cache (see sload_i32).
+  int kbj = sload_i32(list);                  // block j
   int kb1 = n > 1 ? sload_i32(list + 1) : 0;  // block j + 1
-  dma_k(kb, 0);
-  dma_v(kb, 2);
+  dma_k(kbj, 0);
+  dma_v(kbj, 2);
   if (n > 1) dma_k(kb1, 1);
   wait_vmcnt<0>();
 #pragma unroll
@@ -277,67 +383,48 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     for (int s = 0; s < 4; ++s) settle(qreg[qg][s]);  // q landed with the first blocks
   lds_barrier();
   {
-    const bool c0 = !whole_block(kb), c1 = n > 1 && !whole_block(kb1);
+    const bool c0 = !whole_block(kbj), c1 = n > 1 && !whole_block(kb1);
     if (c0) {
-      clear_rows(kb, 0);
-      clear_rows(kb, 2);
+      clear_rows(kbj, 0);
+      clear_rows(kbj, 2);
     }
     if (c1) clear_rows(kb1, 1);
     if (c0 || c1) lds_barrier();
   }
-  f32x4 st[2][2];
-  scores(0, st);
-  apply_mask(kb, st);
+  // scores of blocks with even / odd list position
+  f32x4 sA[2][2], sB[2][2];
+  scores(0, sA);
+  if (needs_mask(kbj)) apply_mask(kbj, sA);
   {
-    float alpha[2];
-    settle_max(st, true, alpha);  // acc is still zero: no rescale
+    float mx[2], alpha[2];
+    lane_max(sA, mx);
+    settle_max(mx, alpha);  // acc is still zero: no rescale
   }
   lds_barrier();  // every wave has read K slot 0 before step 0 refills it
 
-  // Step j: (A) the scores of block j+1 (of a stale slot when j+1 == n:
-  // computed, unused) with the weights of block j, then (B) block j's PV
-  // product with the maxima of block j+1.  Both halves are one branch-free
-  // block whose matrix and vector instructions are interleaved
-  // (sched_group_barrier), so that each wave keeps the matrix core and the
-  // VALU busy at once.
-  auto step = [&](int j, const int par) {
-    const int kb2 = j + 2 < n ? sload_i32(list + j + 2) : 0;
+  // Step j: all of the step's LDS operands are read first (K of block j+1,
+  // V of block j), then (A) the scores of block j+1 (of a stale slot when
+  // j+1 == n: computed, unused) with the weights of block j, then (B) block
+  // j's PV product with the lane maxima of block j+1.  The reads, A and B are
+  // one branch-free block whose matrix and vector instructions are
+  // interleaved (sched_group_barrier); the masks of diagonal / partial blocks
+  // and the rare raise of a reference maximum follow it.
+  auto step = [&](int j, const int par, f32x4 (&st)[2][2], f32x4 (&sn)[2][2]) {
+    // list entry j+2 and the exponent of V block j (V block j holds v * 2^-ev)
+    int kb2, ev;
+    sload2_i32(list + min(j + 2, n - 1), vexp + min(max(kbj, 0), nkb32 - 1), kb2, ev);
+    if (j + 2 >= n) kb2 = 0;
+    if (kbj < 0 || kbj >= nkb32) ev = 0;  // an empty or out-of-range entry reads no V
     if (j + 2 < n) dma_k(kb2, par);            // held block j (scored a step ago)
     if (j + 1 < n) dma_v(kb1, 2 + (par ^ 1));  // held block j-1 (multiplied)
-    f32x4 sn[2][2];
-    scores(par ^ 1, sn);
-    apply_mask(kb1, sn);
-    // P = P_hi + P_lo in bf16 (P_lo = bf16(P - P_hi)): the product keeps ~16
-    // mantissa bits of each weight, so bf16 rounding of P costs ~2^-17
-    // relative instead of 2^-9 (which alone exceeds 2e-3 on rows whose mass
-    // sits on a few keys).  Column c16 is this lane's query; the positive
-    // scale commutes with the max, so it is applied in the exponent.
-    bf16x8 ph[2], pl[2];
-#pragma unroll
-    for (int qg = 0; qg < 2; ++qg) {
-      const float mu = (m[qg] == __int_as_float(0xff800000)) ? 0.f : m[qg] * p.qscale;
-      float pv[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pv[e] = fast_exp2(__builtin_fmaf(st[qg][0][e], p.qscale, -mu));
-        pv[4 + e] = fast_exp2(__builtin_fmaf(st[qg][1][e], p.qscale, -mu));
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) l[qg] += pv[e];
-      // packed words: hw = bf16x2(P) (round to nearest), its exact fp32
-      // value from the halves, lw = bf16x2(P - hi)
-      uint32_t hw[4], lw[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        hw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{pv[2 * e], pv[2 * e + 1]}), bf16x2));
-        const float h0 = __uint_as_float(hw[e] << 16), h1 = __uint_as_float(hw[e] & 0xffff0000u);
-        lw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{pv[2 * e] - h0, pv[2 * e + 1] - h1}), bf16x2));
-      }
-      ph[qg] = __builtin_bit_cast(bf16x8, uint4{hw[0], hw[1], hw[2], hw[3]});
-      pl[qg] = __builtin_bit_cast(bf16x8, uint4{lw[0], lw[1], lw[2], lw[3]});
-    }
-    // O^T += V^T P^T over this wave's keys; each V^T operand serves both groups
+    const uint16_t *sk = smem + (par ^ 1) * PF_BLK;
     const uint16_t *sv = smem + (2 + par) * PF_BLK;
+    bf16x8 ka[2][4];
+    f16x8 va[8];
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ka[kt2][s] = *(const bf16x8 *)&sk[koffs[s] + 16 * kt2 * PF_D];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       // V^T rows through the LDS transpose read: lane (g, j) of a 16-lane group
@@ -346,35 +433,76 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       const uint16_t *v0 = sv + voffs[dt];
       const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)v0);
       const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(v0 + 16 * PF_D));
-      const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
-        acc[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[qg], acc[qg][dt], 0, 0, 0);
-        acc[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[qg], acc[qg][dt], 0, 0, 0);
-      }
+      va[dt] = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
-    float alpha[2];
-    const bool raise = settle_max(sn, j + 1 < n, alpha);
-    // order within the block: K reads, then the 16 score MFMAs each followed
-    // by weight VALU work, then V reads, then the 32 PV MFMAs each followed
-    // by VALU work of the next block's mask and maxima
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    // S^T = K Q^T for block j+1
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2) {
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kt2][s], qreg[0][s], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kt2][s], qreg[1][s], s1, 0, 0, 0);
+      }
+      sn[0][kt2] = s0;
+      sn[1][kt2] = s1;
+    }
+    // P = 2^ev * exp2(s*qscale - m*qscale) in fp16 (round to nearest even; at
+    // most 2^(8+ev) <= 2^15); l sums the rounded weights times 2^-ev (exact).
+    // Column c16 is this lane's query; the positive scale commutes with the
+    // max, so it is applied in the exponent.
+    const float evf = (float)ev;
+    // 2^-ev as an fp16 pair (0 <= ev <= 7: biased exponent 15 - ev)
+    const uint32_t wbits = (uint32_t)(15 - ev) << 10;
+    const f16x2 wl2 = __builtin_bit_cast(f16x2, wbits | (wbits << 16));
+    f16x8 ph[2];
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      const float c = nmu[qg] + evf;
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pv[e] = fast_exp2(__builtin_fmaf(st[qg][0][e], p.qscale, c));
+        pv[4 + e] = fast_exp2(__builtin_fmaf(st[qg][1][e], p.qscale, c));
+      }
+      f16x2 hw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hw[e] = __builtin_convertvector((f32x2{pv[2 * e], pv[2 * e + 1]}), f16x2);
+        l[qg] = __builtin_amdgcn_fdot2(hw[e], wl2, l[qg], false);
+      }
+      ph[qg] = __builtin_shufflevector(__builtin_shufflevector(hw[0], hw[1], 0, 1, 2, 3),
+                                       __builtin_shufflevector(hw[2], hw[3], 0, 1, 2, 3), 0, 1, 2,
+                                       3, 4, 5, 6, 7);
+    }
+    // O^T += V^T P^T over this wave's keys; each V^T operand serves both groups
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg)
+        acc[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], ph[qg], acc[qg][dt], 0, 0, 0);
+    float mx[2];
+    lane_max(sn, mx);
+    // order within the block: the 24 LDS reads, then the 16 score MFMAs each
+    // followed by weight VALU work, then the 16 PV MFMAs each followed by
+    // VALU work of the next block's maxima
+    __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 16; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
     }
-    if (raise) rescale_acc(alpha);
-#pragma unroll
-    for (int qg = 0; qg < 2; ++qg)
-#pragma unroll
-      for (int kt2 = 0; kt2 < 2; ++kt2) st[qg][kt2] = sn[qg][kt2];
+    if (j + 1 < n && needs_mask(kb1)) {
+      apply_mask(kb1, sn);
+      lane_max(sn, mx);
+    }
+    float alpha[2];
+    if (j + 1 < n && settle_max(mx, alpha)) rescale_acc(alpha);
     // this wave's loads have landed and every wave is done with the slots
     // that the next step refills
     wait_vmcnt<0>();
@@ -383,12 +511,13 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     if (ck) clear_rows(kb2, par);
     if (cv) clear_rows(kb1, 2 + (par ^ 1));
     if (ck || cv) lds_barrier();
+    kbj = kb1;
     kb1 = kb2;
   };
   for (int j = 0; j < n; j += 2) {
-    step(j, 0);
+    step(j, 0, sA, sB);
     if (j + 1 >= n) break;
-    step(j + 1, 1);
+    step(j + 1, 1, sB, sA);
   }
   // l is a per-lane partial over this lane's keys; sum the 4 lane groups.
 #pragma unroll
@@ -418,9 +547,9 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg) {
     const float m2 = red_ml[(qg * 2 + 0) * 16 + c16], l2 = red_ml[(qg * 2 + 1) * 16 + c16];
-    const float M = fmaxf(m[qg], m2);
-    const float a1 = (m[qg] == __int_as_float(0xff800000)) ? 0.f : fast_exp2((m[qg] - M) * p.qscale);
-    const float a2 = (m2 == __int_as_float(0xff800000)) ? 0.f : fast_exp2((m2 - M) * p.qscale);
+    const float M = pf_max(m[qg], m2);
+    const float a1 = (m[qg] == NEG_INF) ? 0.f : fast_exp2((m[qg] - M) * p.qscale);
+    const float a2 = (m2 == NEG_INF) ? 0.f : fast_exp2((m2 - M) * p.qscale);
     const float L = l[qg] * a1 + l2 * a2;
     const float inv = L > 0.f ? 1.f / L : 0.f;
     if (q_row[qg] >= p.T) continue;
@@ -439,7 +568,28 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 
 using namespace la;
 
-extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
+namespace la {
+
+int prefill_status(uint32_t *bits, bool clear) {
+  LA_HIP(hipMemcpyFromSymbol(bits, HIP_SYMBOL(la_pf_status), sizeof(uint32_t), 0,
+                             hipMemcpyDeviceToHost));
+  if (clear) {
+    const uint32_t zero = 0;
+    LA_HIP(hipMemcpyToSymbol(HIP_SYMBOL(la_pf_status), &zero, sizeof(uint32_t), 0,
+                             hipMemcpyHostToDevice));
+  }
+  return LA_OK;
+}
+
+static int64_t pf_align(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Workspace: the fp16 copy of V (B, Hkv, T, 128), then the block exponents.
+static int64_t prefill_ws_bytes(const la_prefill_args *a) {
+  const int64_t nkb = ceil_div(a->T, PF_BS);
+  return pf_align(a->B * a->Hkv * a->T * PF_D * 2) + pf_align(a->B * a->Hkv * nkb * 4);
+}
+
+static int prefill_validate(const la_prefill_args *a) {
   LA_REQUIRE(a && a->q && a->k && a->v && a->out && a->ids, "la_block_sparse_prefill: null pointer");
   LA_REQUIRE(a->B > 0 && a->Hq > 0 && a->Hkv > 0 && a->T > 0, "la_block_sparse_prefill: bad shape");
   LA_REQUIRE(a->Hq % a->Hkv == 0, "n_heads must be a multiple of n_kv_heads");
@@ -448,6 +598,7 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   LA_REQUIRE(a->out_dtype == LA_F32 || a->out_dtype == LA_BF16, "la_block_sparse_prefill: out dtype");
   LA_REQUIRE(a->width >= 1, "la_block_sparse_prefill: list width");
   LA_REQUIRE(a->T < ((int64_t)1 << 30), "la_block_sparse_prefill: T must be below 2^30");
+  LA_REQUIRE(a->scale > 0.f, "la_block_sparse_prefill: scale must be positive");
   // 16-byte vector access of q/k/v rows and of the output
   const bool al = ((uintptr_t)a->q % 16 == 0) && ((uintptr_t)a->k % 16 == 0) &&
                   ((uintptr_t)a->v % 16 == 0) && ((uintptr_t)a->out % 16 == 0) &&
@@ -455,10 +606,39 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
                   a->k_sh % 8 == 0 && a->k_st % 8 == 0 && a->v_sb % 8 == 0 && a->v_sh % 8 == 0 &&
                   a->v_st % 8 == 0 && a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_st % 4 == 0;
   LA_REQUIRE(al, "la_block_sparse_prefill: rows must be contiguous and 16-byte aligned");
+  return LA_OK;
+}
+
+}  // namespace la
+
+extern "C" size_t la_block_sparse_prefill_workspace(const la_prefill_args *a) {
+  if (prefill_validate(a) != LA_OK) return 0;
+  return (size_t)prefill_ws_bytes(a);
+}
+
+extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
+  const int rc = prefill_validate(a);
+  if (rc != LA_OK) return rc;
+  const int64_t ws_need = prefill_ws_bytes(a);
+  LA_REQUIRE(a->workspace != nullptr, "la_block_sparse_prefill: workspace required");
+  LA_REQUIRE((uintptr_t)a->workspace % 256 == 0, "la_block_sparse_prefill: workspace alignment");
+  if (a->ws_bytes < ws_need)
+    return fail(LA_ERR_WORKSPACE, "la_block_sparse_prefill: workspace %lld < %lld bytes",
+                (long long)a->ws_bytes, (long long)ws_need);
+  const int64_t nkb = ceil_div(a->T, PF_BS);
+  uint16_t *v16 = (uint16_t *)a->workspace;
+  int32_t *vexp = (int32_t *)((char *)a->workspace + pf_align(a->B * a->Hkv * a->T * PF_D * 2));
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nvb = a->B * a->Hkv * nkb;
+  LA_REQUIRE(nvb < ((int64_t)1 << 31), "la_block_sparse_prefill: too many key blocks");
+  prefill_v16_kernel<<<dim3((unsigned)nvb), 256, 0, st>>>((const uint16_t *)a->v, a->v_sb, a->v_sh,
+                                                          a->v_st, a->Hkv, a->T, nkb, v16, vexp);
+  LA_LAUNCHED();
   PfKP p{};
   p.q = (const uint16_t *)a->q;
   p.k = (const uint16_t *)a->k;
-  p.v = (const uint16_t *)a->v;
+  p.v = v16;
+  p.vexp = vexp;
   p.out = a->out;
   p.ids = a->ids;
   p.counts = a->counts;
@@ -468,16 +648,22 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   p.T = a->T;
   p.q_sb = a->q_sb; p.q_sh = a->q_sh; p.q_st = a->q_st;
   p.k_sb = a->k_sb; p.k_sh = a->k_sh; p.k_st = a->k_st;
-  p.v_sb = a->v_sb; p.v_sh = a->v_sh; p.v_st = a->v_st;
+  p.v_st = PF_D; p.v_sh = a->T * PF_D; p.v_sb = a->Hkv * a->T * PF_D;
+  LA_REQUIRE(nkb * PF_BS * std::max<int64_t>(a->k_st, PF_D) < ((int64_t)1 << 31),
+             "la_block_sparse_prefill: K rows of one head span >= 2^31 elements");
+  p.k_blk = (uint32_t)(PF_BS * a->k_st);
+  p.v_blk = (uint32_t)(PF_BS * PF_D);
   p.o_sb = a->o_sb; p.o_sh = a->o_sh; p.o_st = a->o_st;
   p.width = a->width;
   p.nqb = ceil_div(a->T, PF_BS);
+  p.nkb = nkb;
   p.qscale = a->scale * 1.4426950408889634f;
+  p.thr_gap = 8.f / p.qscale;
   p.causal = a->causal;
   p.out_dt = a->out_dtype;
   const int64_t nwg = a->B * a->Hq * p.nqb;
   LA_REQUIRE(nwg < ((int64_t)1 << 31), "la_block_sparse_prefill: too many query blocks");
-  prefill_kernel<<<dim3((unsigned)nwg), PF_NT, 0, (hipStream_t)stream>>>(p);
+  prefill_kernel<<<dim3((unsigned)nwg), PF_NT, 0, st>>>(p);
   LA_LAUNCHED();
   return LA_OK;
 }

@@ -439,5 +439,10 @@ extern "C" int la_device_status(uint32_t *bits, int32_t clear, void *stream) {
     LA_HIP(hipMemcpyToSymbol(HIP_SYMBOL(la_dev_status), &zero, sizeof(uint32_t), 0,
                              hipMemcpyHostToDevice));
   }
+  // status words of the other source files (each holds its own device symbol)
+  uint32_t more = 0;
+  const int rc = prefill_status(&more, clear != 0);
+  if (rc != LA_OK) return rc;
+  *bits |= more;
   return LA_OK;
 }

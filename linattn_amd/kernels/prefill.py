@@ -7,8 +7,8 @@ blocks, top-k with ties to the lowest block index, then the sink blocks and
 the local window (which includes the diagonal block) OR'd in.
 
 ``block_sparse_prefill`` is the executor (block_sparse.py:80-163) for lists
-shared by a 64-query block, run on the matrix cores (bf16 MFMA, fp32
-accumulation) with the causal mask applied in-kernel.
+shared by a 64-query block, run on the matrix cores (bf16 MFMA scores, fp16
+MFMA weights x V, fp32 accumulation) with the causal mask applied in-kernel.
 """
 
 from __future__ import annotations
@@ -98,7 +98,11 @@ def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids:
     a.scale = float(scale if scale is not None else 1.0 / math.sqrt(D))
     a.causal = 1 if causal else 0
     a.out_dtype = N.dtype_code(out.dtype)
-    N.check(N.load().la_block_sparse_prefill(ctypes.byref(a), N.stream_handle(dev)),
+    L = N.load()
+    ws_bytes = L.la_block_sparse_prefill_workspace(ctypes.byref(a))
+    ws = N.workspace(ws_bytes, dev)
+    a.workspace, a.ws_bytes = N.ptr(ws), ws_bytes
+    N.check(L.la_block_sparse_prefill(ctypes.byref(a), N.stream_handle(dev)),
             "block_sparse_prefill")
     return out
 

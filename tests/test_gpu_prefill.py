@@ -3,11 +3,14 @@ block-sparse causal prefill (within 2e-3 of the fp64 oracle, fp32 output)."""
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
 
 import oracle
+from linattn_amd import _native as N
 from linattn_amd.kernels.prefill import block_select_hip, block_sparse_prefill, sparse_prefill
 
 pytestmark = pytest.mark.gpu
@@ -121,3 +124,84 @@ def test_config3_full_size(dev):
         for qb, r in rows.items():
             got = out[b, h, qb * 64:(qb + 1) * 64].cpu().double().numpy()
             assert np.abs(got - r).max() < 2e-3, (b, h, qb)
+
+
+def fp64_block_attention(q, k, v, ids, counts, chunk=256):
+    """fp64 attention of every (b, h, query block) over its listed 64-key
+    blocks with the causal mask, on the device (torch fp64 matmuls over the
+    gathered blocks), as (B, Hq, T, D)."""
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    G, nqb, W = Hq // Hkv, ids.shape[2], ids.shape[3]
+    dev = q.device
+    out = torch.zeros(B, Hq, T, D, dtype=torch.float64, device=dev)
+    flat_ids = ids.reshape(-1, W).long()
+    flat_cnt = counts.reshape(-1).long()
+    ar64 = torch.arange(64, device=dev)
+    for s0 in range(0, B * Hq * nqb, chunk):
+        i = torch.arange(s0, min(s0 + chunk, B * Hq * nqb), device=dev)
+        b, h, qb = i // (Hq * nqb), (i // nqb) % Hq, i % nqb
+        lst = flat_ids[i]
+        ok = (lst >= 0) & (torch.arange(W, device=dev)[None, :] < flat_cnt[i][:, None])
+        tok = (lst.clamp(min=0)[:, :, None] * 64 + ar64).reshape(len(i), -1)
+        tok_ok = ok[:, :, None].expand(-1, -1, 64).reshape(len(i), -1) & (tok < T)
+        tok = tok.clamp(max=T - 1)
+        qrow = (qb[:, None] * 64 + ar64).clamp(max=T - 1)
+        qg = q[b[:, None], h[:, None], qrow].double()
+        kg = k[b[:, None], (h // G)[:, None], tok].double()
+        vg = v[b[:, None], (h // G)[:, None], tok].double()
+        sc = torch.bmm(qg, kg.transpose(1, 2).contiguous()) / math.sqrt(D)
+        allow = tok_ok[:, None, :] & (tok[:, None, :] <= qrow[:, :, None])
+        sc = sc.masked_fill(~allow, float("-inf"))
+        o = torch.bmm(torch.softmax(sc, dim=-1), vg)
+        rows = qb[:, None] * 64 + ar64
+        keep = rows < T
+        out[b[:, None].expand_as(rows)[keep], h[:, None].expand_as(rows)[keep], rows[keep]] = o[keep]
+    return out
+
+
+def test_config3_every_row_within_tolerance(dev):
+    """C3 at full size (2 x 32 x 32768 query rows): every output row of the
+    fp32-output prefill within 2e-3 of fp64 attention over its lists; the
+    bf16 output within bf16 rounding of it."""
+    B, Hq, Hkv, T, D = 2, 32, 8, 32768, 128
+    q, k, v = c3_inputs(B, Hq, Hkv, T, D, seed=0, device=dev)
+    out, ids, counts = sparse_prefill(q, k, v, topk=16, sink_blocks=1, window_blocks=4,
+                                      out_dtype=torch.float32)
+    ref = fp64_block_attention(q, k, v, ids, counts)
+    err = (out.double() - ref).abs()
+    assert err.max().item() < 2e-3, err.max().item()
+    out_b = block_sparse_prefill(q, k, v, ids, counts)
+    assert out_b.dtype == torch.bfloat16
+    assert ((out_b.double() - ref).abs() <= ref.abs() * 2.0 ** -8 + 2e-3).all()
+
+
+def test_prefill_large_v_blocks(dev):
+    """V blocks whose values reach 2^15..2^22 are converted to fp16 with a
+    power-of-two block exponent (folded back into the weights): outputs stay
+    within 2e-3 relative to the value scale.  A finite |v| >= 2^22 raises
+    LA_DEV_PREFILL_RANGE (its fp16 copy overflows)."""
+    q, k, v = c3_inputs(1, 4, 2, 512, 128, seed=6, outliers=False)
+    v = v.float()
+    v[0, 0, 128:192] *= 2.0 ** 18   # block 2 of KV head 0: e = 5 or 6
+    v[0, 1, 448:512] *= 2.0 ** 19   # block 7 of KV head 1 (|v| < 2^22): e = 6 or 7
+    v = v.bfloat16()
+    nqb = 8
+    ids = torch.full((1, 4, nqb, nqb), -1, dtype=torch.int32)
+    for i in range(nqb):
+        ids[:, :, i, :i + 1] = torch.arange(i + 1, dtype=torch.int32)
+    N.device_status(dev)
+    out = block_sparse_prefill(q.to(dev), k.to(dev), v.to(dev), ids.to(dev),
+                               out_dtype=torch.float32)
+    assert N.device_status(dev) == 0
+    ref = oracle.dense_attention(q, k, v)
+    scale = np.abs(v.double().numpy()).max(axis=(2, 3))[:, np.repeat(np.arange(2), 2)]
+    err = np.abs(out.cpu().double().numpy() - ref).max(axis=(2, 3))
+    assert (err < 2e-3 * np.maximum(scale, 1.0)).all(), (err, scale)
+    # a finite value beyond the fp16 range of its scaled block is reported
+    v2 = v.clone()
+    v2[0, 0, 5, 3] = 2.0 ** 23
+    out2 = block_sparse_prefill(q.to(dev), k.to(dev), v2.to(dev), ids.to(dev),
+                                out_dtype=torch.float32)
+    assert N.device_status(dev) & N.LA_DEV_PREFILL_RANGE
+    assert not torch.isfinite(out2[0, :2]).all()
