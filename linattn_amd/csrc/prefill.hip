@@ -44,6 +44,7 @@
 // query blocks run on the same XCD (shared L2 for their common key blocks).
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 #include "common.h"
 
@@ -217,7 +218,10 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   const uint16_t *kbh = p.k + b * p.k_sb + kvh * p.k_sh;
   const uint16_t *vbh = p.v + b * p.v_sb + kvh * p.v_sh;
   const int32_t *vexp = p.vexp + (b * p.Hkv + kvh) * p.nkb;
-  auto whole_block = [&](int kb) { return kb >= 0 && kb * PF_BS + PF_BS <= T32; };
+  // a block is whole (no row past T) and listed (>= 0) iff kb < T / 64 as
+  // an unsigned compare
+  const uint32_t nwhole = (uint32_t)(T32 / PF_BS);
+  auto whole_block = [&](int kb) { return (uint32_t)kb < nwhole; };
   // LDS slots of PF_BLK elements: K in 0..1, V in 2..3
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t *)smem);
   const int wu = __builtin_amdgcn_readfirstlane(w);
@@ -310,10 +314,11 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // causal diagonal or past T, and on every key of a -1 entry, written over
   // the block's scores.  Only those blocks (diagonal, partial, empty) need it;
   // keys and positions fit in int32 (T < 2^30 is checked at launch).
-  auto needs_mask = [&](int kbx) {
-    const int key0 = kbx * PF_BS + 32 * khu;  // first key of this half
-    return kbx < 0 || (p.causal && key0 + 31 > (int)qb * PF_BS + 32 * qhu) || key0 + 32 > T32;
-  };
+  // Blocks kb <= mask_lim need no mask in this wave: key 32 kh + 31 of the
+  // block is at most the first query of the wave's half (causal) and below T.
+  const int mask_lim = min(p.causal ? (int)qb - 1 + (qhu > khu ? 1 : 0) : INT_MAX,
+                           (T32 - 32 - 32 * khu) >> 6);
+  auto needs_mask = [&](int kbx) { return kbx < 0 || kbx > mask_lim; };
   auto apply_mask = [&](int kbx, f32x4 (&sc)[2][2]) {
     const int key0 = kbx * PF_BS + 32 * kh;
 #pragma unroll
@@ -342,10 +347,11 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // its query's threshold); the exact column maximum (lane swaps) is formed
   // only then.  alpha (the factor for acc) is returned through `alpha`.
   auto settle_max = [&](float (&mx)[2], float (&alpha)[2]) {
+    alpha[0] = alpha[1] = 1.f;
+    if (__ballot(mx[0] > thr[0] || mx[1] > thr[1]) == 0) return false;  // the common case
     bool any = false;
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      alpha[qg] = 1.f;
       if (__ballot(mx[qg] > thr[qg]) != 0) {
         const float cm = pf_pair32_max(pf_pair16_max(mx[qg]));
         const float mn = pf_max(m[qg], cm);
@@ -409,14 +415,18 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // one branch-free block whose matrix and vector instructions are
   // interleaved (sched_group_barrier); the masks of diagonal / partial blocks
   // and the rare raise of a reference maximum follow it.
-  auto step = [&](int j, const int par, f32x4 (&st)[2][2], f32x4 (&sn)[2][2]) {
-    // list entry j+2 and the exponent of V block j (V block j holds v * 2^-ev)
+  // FULL: j + 2 < n (every block of the step exists: the steady state,
+  // without edge conditions).
+  auto step = [&](auto full, int j, const int par, f32x4 (&st)[2][2], f32x4 (&sn)[2][2]) {
+    constexpr bool FULL = decltype(full)::value;
+    // list entry j+2 and the exponent of V block j (V block j holds v * 2^-ev;
+    // an empty or out-of-range entry reads exponent 0 from block 0)
     int kb2, ev;
-    sload2_i32(list + min(j + 2, n - 1), vexp + min(max(kbj, 0), nkb32 - 1), kb2, ev);
-    if (j + 2 >= n) kb2 = 0;
-    if (kbj < 0 || kbj >= nkb32) ev = 0;  // an empty or out-of-range entry reads no V
-    if (j + 2 < n) dma_k(kb2, par);            // held block j (scored a step ago)
-    if (j + 1 < n) dma_v(kb1, 2 + (par ^ 1));  // held block j-1 (multiplied)
+    const uint32_t kbe = (uint32_t)kbj < (uint32_t)nkb32 ? (uint32_t)kbj : 0u;
+    sload2_i32(list + (FULL ? j + 2 : min(j + 2, n - 1)), vexp + kbe, kb2, ev);
+    if (!FULL && j + 2 >= n) kb2 = 0;
+    if (FULL || j + 2 < n) dma_k(kb2, par);            // held block j (scored a step ago)
+    if (FULL || j + 1 < n) dma_v(kb1, 2 + (par ^ 1));  // held block j-1 (multiplied)
     const uint16_t *sk = smem + (par ^ 1) * PF_BLK;
     const uint16_t *sv = smem + (2 + par) * PF_BLK;
     bf16x8 ka[2][4];
@@ -497,27 +507,40 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
     }
-    if (j + 1 < n && needs_mask(kb1)) {
-      apply_mask(kb1, sn);
-      lane_max(sn, mx);
+    if (FULL || j + 1 < n) {
+      if (needs_mask(kb1)) {
+        apply_mask(kb1, sn);
+        lane_max(sn, mx);
+      }
+      float alpha[2];
+      if (settle_max(mx, alpha)) rescale_acc(alpha);
     }
-    float alpha[2];
-    if (j + 1 < n && settle_max(mx, alpha)) rescale_acc(alpha);
     // this wave's loads have landed and every wave is done with the slots
     // that the next step refills
     wait_vmcnt<0>();
     lds_barrier();
-    const bool ck = j + 2 < n && !whole_block(kb2), cv = j + 1 < n && !whole_block(kb1);
-    if (ck) clear_rows(kb2, par);
-    if (cv) clear_rows(kb1, 2 + (par ^ 1));
-    if (ck || cv) lds_barrier();
+    const bool ck = (FULL || j + 2 < n) && !whole_block(kb2);
+    const bool cv = (FULL || j + 1 < n) && !whole_block(kb1);
+    if (ck || cv) {
+      if (ck) clear_rows(kb2, par);
+      if (cv) clear_rows(kb1, 2 + (par ^ 1));
+      lds_barrier();
+    }
     kbj = kb1;
     kb1 = kb2;
   };
-  for (int j = 0; j < n; j += 2) {
-    step(j, 0, sA, sB);
+  using full_t = std::integral_constant<bool, true>;
+  using tail_t = std::integral_constant<bool, false>;
+  int j = 0;
+  for (; j + 3 < n; j += 2) {
+    step(full_t{}, j, 0, sA, sB);
+    step(full_t{}, j + 1, 1, sB, sA);
+  }
+  // the last one to three steps
+  for (; j < n; j += 2) {
+    step(tail_t{}, j, 0, sA, sB);
     if (j + 1 >= n) break;
-    step(j + 1, 1, sB, sA);
+    step(tail_t{}, j + 1, 1, sB, sA);
   }
   // l is a per-lane partial over this lane's keys; sum the 4 lane groups.
 #pragma unroll
