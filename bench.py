@@ -183,7 +183,8 @@ def bench_c3(dev, steps, warmup):
             "selected_block_pairs": pairs, "ms_prefill": round(ms, 4),
             "ms_block_select": round(ms_sel, 4), "TFLOPs": round(tflops, 1),
             "frac_mfma_bf16_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "note": "useful FLOPs; the PV product issues two bf16 MFMAs (P split hi+lo)"}
+            "note": "useful FLOPs (bf16 QK^T, fp16 weights x V); ms_prefill includes the fp16 V "
+                    "conversion pre-pass"}
 
 
 def bench_c5(dev, steps, warmup):

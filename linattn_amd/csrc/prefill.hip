@@ -76,6 +76,18 @@ __device__ __forceinline__ float pf_max(float a, float b) { return __builtin_ele
 __device__ __forceinline__ float pf_pair16_max(float x) { const float2 p = pair16(x); return pf_max(p.x, p.y); }
 __device__ __forceinline__ float pf_pair32_max(float x) { const float2 p = pair32(x); return pf_max(p.x, p.y); }
 
+// x / d and x % d for a wave-uniform x < 2^31 (shift when d = 2^sh)
+__device__ __forceinline__ uint32_t pf_div(uint32_t x, uint32_t d, int sh) { return sh >= 0 ? x >> sh : x / d; }
+
+// Three wave-uniform 32-bit reads through the scalar cache, waited for together.
+__device__ __forceinline__ void sload3_i32(const int32_t *p0, const int32_t *p1, const int32_t *p2,
+                                           int32_t &a, int32_t &b, int32_t &c) {
+  asm volatile(
+      "s_load_dword %0, %3, 0x0\n\ts_load_dword %1, %4, 0x0\n\ts_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(a), "=&s"(b), "=&s"(c) : "s"(p0), "s"(p1), "s"(p2) : "memory");
+}
+
 // Two wave-uniform 32-bit reads through the scalar cache, waited for together.
 __device__ __forceinline__ void sload2_i32(const int32_t *p0, const int32_t *p1, int32_t &a, int32_t &b) {
   asm volatile("s_load_dword %0, %2, 0x0\n\ts_load_dword %1, %3, 0x0\n\ts_waitcnt lgkmcnt(0)"
@@ -91,6 +103,7 @@ struct PfKP {
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
   int64_t width, nqb, nkb;
   uint32_t k_blk, v_blk;  // elements between consecutive 64-token blocks of K / V
+  int32_t sh_g, sh_nqb, sh_hkv;  // log2 of G, nqb, Hkv when powers of two, else -1
   float qscale;   // scale * log2(e)
   float thr_gap;  // 8 / qscale: raw-score headroom above the reference maximum
   int32_t causal, out_dt;
@@ -168,30 +181,31 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   const int64_t nwg = gridDim.x;
   const int64_t wg = blockIdx.x;
   const int64_t per_xcd = nwg / 8;
-  const int64_t lid = (wg < per_xcd * 8) ? (wg % 8) * per_xcd + wg / 8 : wg;
-  const int64_t G = p.Hq / p.Hkv;
-  const int64_t hg = lid % G;
-  const int64_t qb = (lid / G) % p.nqb;
-  const int64_t kvh = (lid / (G * p.nqb)) % p.Hkv;
-  const int64_t b = lid / (G * p.nqb * p.Hkv);
+  const uint32_t lid = (uint32_t)((wg < per_xcd * 8) ? (wg % 8) * per_xcd + wg / 8 : wg);
+  const uint32_t G = (uint32_t)(p.Hq / p.Hkv), nqbu = (uint32_t)p.nqb, hkvu = (uint32_t)p.Hkv;
+  const uint32_t l1 = pf_div(lid, G, p.sh_g), l2 = pf_div(l1, nqbu, p.sh_nqb);
+  const uint32_t l3 = pf_div(l2, hkvu, p.sh_hkv);
+  const int64_t hg = lid - l1 * G;
+  const int64_t qb = l1 - l2 * nqbu;
+  const int64_t kvh = l2 - l3 * hkvu;
+  const int64_t b = l3;
   const int64_t h = kvh * G + hg;
 
   const int qh = w >> 1, kh = w & 1;  // query half, key half
   const int qhu = __builtin_amdgcn_readfirstlane(qh), khu = __builtin_amdgcn_readfirstlane(kh);
   const int T32 = (int)p.T, nkb32 = (int)p.nkb;
   int64_t q_row[2];                    // this lane's query in each 16-query group
-  bf16x8 qreg[2][4];
 #pragma unroll
-  for (int qg = 0; qg < 2; ++qg) {
-    q_row[qg] = qb * PF_BS + 32 * qh + 16 * qg + c16;
-    const uint16_t *qp = p.q + b * p.q_sb + h * p.q_sh + min(q_row[qg], p.T - 1) * p.q_st;
-    // q is read once: streamed past the caches that keep the K/V blocks
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qreg[qg][s] = __builtin_nontemporal_load((const bf16x8 *)(qp + 32 * s + 8 * g));
-  }
+  for (int qg = 0; qg < 2; ++qg) q_row[qg] = qb * PF_BS + 32 * qh + 16 * qg + c16;
+  bf16x8 qreg[2][4];  // this lane's q fragments, loaded after the first block copies are issued
+  // the list length and its first two entries in one scalar wait (a list
+  // entry read past the count is never used)
   const int32_t *list = p.ids + ((b * p.Hq + h) * p.nqb + qb) * p.width;
-  const int n = p.counts ? min((int)p.counts[(b * p.Hq + h) * p.nqb + qb], (int)p.width)
-                         : (int)p.width;
+  const int32_t *cnt_p = p.counts ? p.counts + (b * p.Hq + h) * p.nqb + qb : list;
+  int n, kbj, kb1;
+  const int o1 = __builtin_amdgcn_readfirstlane(p.width > 1 ? 1 : 0);
+  sload3_i32(cnt_p, list, list + o1, n, kbj, kb1);
+  n = p.counts ? min(n, (int)p.width) : (int)p.width;
 
   // four output values of query group qg: dims 16 dt + 4 g .. + 3
   auto store4 = [&](int qg, int dt, f32x4 r) {
@@ -377,11 +391,17 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // and V block x in slot 2 + x % 2; both are fetched one step ahead (K of
   // block j+2 and V of block j+1 during step j).  List entries and V block
   // exponents come through the scalar cache (see sload_i32).
-  int kbj = sload_i32(list);                  // block j
-  int kb1 = n > 1 ? sload_i32(list + 1) : 0;  // block j + 1
+  if (n <= 1) kb1 = 0;
   dma_k(kbj, 0);
   dma_v(kbj, 2);
   if (n > 1) dma_k(kb1, 1);
+  // q, read once: streamed past the caches that keep the K/V blocks
+#pragma unroll
+  for (int qg = 0; qg < 2; ++qg) {
+    const uint16_t *qp = p.q + b * p.q_sb + h * p.q_sh + min(q_row[qg], p.T - 1) * p.q_st;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qreg[qg][s] = __builtin_nontemporal_load((const bf16x8 *)(qp + 32 * s + 8 * g));
+  }
   wait_vmcnt<0>();
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg)
@@ -549,16 +569,13 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   }
   // Merge the two key halves: the kh = 1 wave of each query half hands its
   // state to the kh = 0 wave through LDS (the staging buffers are free now).
-  float *red = (float *)smem + qh * (2 * 128 * 16 + 64);
-  float *red_o = red;                   // [qg][d][query]
-  float *red_ml = red + 2 * 128 * 16;   // [qg][m, l][query]
+  f32x4 *red_o = (f32x4 *)smem + qh * (2 * 8 * 64 + 16);  // [qg][dt][lane]
+  float *red_ml = (float *)(red_o + 2 * 8 * 64);            // [qg][m, l][query]
   if (kh == 1) {
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red_o[(qg * 128 + 16 * dt + 4 * g + e) * 16 + c16] = acc[qg][dt][e];
+      for (int dt = 0; dt < 8; ++dt) red_o[(qg * 8 + dt) * 64 + lane] = acc[qg][dt];
       if (g == 0) {
         red_ml[(qg * 2 + 0) * 16 + c16] = m[qg];
         red_ml[(qg * 2 + 1) * 16 + c16] = l[qg];
@@ -578,10 +595,10 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     if (q_row[qg] >= p.T) continue;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
+      const f32x4 o2 = red_o[(qg * 8 + dt) * 64 + lane];
       f32x4 r;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        r[e] = (acc[qg][dt][e] * a1 + red_o[(qg * 128 + 16 * dt + 4 * g + e) * 16 + c16] * a2) * inv;
+      for (int e = 0; e < 4; ++e) r[e] = (acc[qg][dt][e] * a1 + o2[e] * a2) * inv;
       store4(qg, dt, r);
     }
   }
@@ -682,6 +699,10 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   p.nkb = nkb;
   p.qscale = a->scale * 1.4426950408889634f;
   p.thr_gap = 8.f / p.qscale;
+  auto log2_or = [](int64_t x) { return is_pow2(x) ? ilog2(x) : -1; };
+  p.sh_g = log2_or(a->Hq / a->Hkv);
+  p.sh_nqb = log2_or(p.nqb);
+  p.sh_hkv = log2_or(a->Hkv);
   p.causal = a->causal;
   p.out_dt = a->out_dtype;
   const int64_t nwg = a->B * a->Hq * p.nqb;
