@@ -69,6 +69,7 @@ constexpr int PF_BLK = PF_BS * PF_D;  // elements of one staged K or V block (16
 // chunk), and rows r and r ^ 1 never share a chunk pair {2i, 2i+1} (V
 // transpose reads: 8 rows x 2 chunks per 32 lanes).
 __device__ __forceinline__ int pf_swz(int r) { return (2 * (r & 7)) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int pf_swz_k(int r) { return 2 * (r & 7); }
 
 // IEEE maximum (NaN-propagating): gfx950 v_maximum3_f32 without the
 // canonicalising moves fmaxf needs in IEEE mode.
@@ -244,15 +245,15 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // (lane%16) ^ swz(row)  (swz(row + 16 t) == swz(row)).  Whole blocks use a
   // block base in SGPRs and per-lane 32-bit byte offsets (no per-load VALU).
   const int drow = 4 * w + (lane >> 4);
-  const int dch = (lane & 15) ^ pf_swz(drow);
+  const int kdch = (lane & 15) ^ pf_swz_k(drow), vdch = (lane & 15) ^ pf_swz(drow);
   uint32_t kvo[4], vvo[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    kvo[t] = (uint32_t)((((int64_t)(16 * t + drow)) * p.k_st + 8 * dch) * 2);
-    vvo[t] = (uint32_t)((((int64_t)(16 * t + drow)) * p.v_st + 8 * dch) * 2);
+    kvo[t] = (uint32_t)((((int64_t)(16 * t + drow)) * p.k_st + 8 * kdch) * 2);
+    vvo[t] = (uint32_t)((((int64_t)(16 * t + drow)) * p.v_st + 8 * vdch) * 2);
   }
-  auto dma_part = [&](const uint16_t *bh, int64_t st, uint32_t blk, const uint32_t (&vo)[4], int kb,
-                      int slot) {
+  auto dma_part = [&](const uint16_t *bh, int64_t st, uint32_t blk, const uint32_t (&vo)[4], int dch,
+                      int kb, int slot) {
     const uint32_t m0 = lds0 + 2 * (slot * PF_BLK + 4 * wu * PF_D);
     if (whole_block(kb)) {
       const uint16_t *base = bh + (uint32_t)kb * blk;  // fits 32 bits (checked at launch)
@@ -269,8 +270,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       }
     }
   };
-  auto dma_k = [&](int kb, int slot) { dma_part(kbh, p.k_st, p.k_blk, kvo, kb, slot); };
-  auto dma_v = [&](int kb, int slot) { dma_part(vbh, p.v_st, p.v_blk, vvo, kb, slot); };
+  auto dma_k = [&](int kb, int slot) { dma_part(kbh, p.k_st, p.k_blk, kvo, kdch, kb, slot); };
+  auto dma_v = [&](int kb, int slot) { dma_part(vbh, p.v_st, p.v_blk, vvo, vdch, kb, slot); };
   // rows of a landed partial block that lie past T (or all rows of a -1
   // entry) are cleared, so masked keys hold zeros rather than copies
   auto clear_rows = [&](int kb, int slot) {
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // LDS element offsets of this lane's operand reads:
   // K: row 32 kh + c16 (+16 kt2), global chunk 4 s + g
   int koffs[4];
-  const int ksw = pf_swz(c16);
+  const int ksw = pf_swz_k(c16);
 #pragma unroll
   for (int s = 0; s < 4; ++s) koffs[s] = (32 * kh + c16) * PF_D + 8 * ((4 * s + g) ^ ksw);
   // V (transpose reads): row 32 kh + 4 g + c16/4 (+16), global column
@@ -567,39 +568,86 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   for (int qg = 0; qg < 2; ++qg) {
     l[qg] = pair32_sum(pair16_sum(l[qg]));
   }
-  // Merge the two key halves: the kh = 1 wave of each query half hands its
-  // state to the kh = 0 wave through LDS (the staging buffers are free now).
-  f32x4 *red_o = (f32x4 *)smem + qh * (2 * 8 * 64 + 16);  // [qg][dt][lane]
-  float *red_ml = (float *)(red_o + 2 * 8 * 64);            // [qg][m, l][query]
-  if (kh == 1) {
+  // Merge the two key halves.  The two waves of a query half exchange halves
+  // of their accumulators through LDS (the staging buffers are free now):
+  // the kh = 0 wave finalizes dims 0..63 and the kh = 1 wave dims 64..127,
+  // each with the other's partial sums of its dims and the other's m, l.
+  // red_o[qh][writer kh][qg][i][lane]: the writer's acc[qg][4 (1 - kh) + i].
+  f32x4 *red_o = (f32x4 *)smem;
+  float *red_ml = (float *)(red_o + 2 * 2 * 2 * 4 * 64);  // [qh][kh][qg][m, l][query]
+  // (the accumulator halves are picked by a wave-uniform branch: indexing
+  // acc by a runtime kh would move it to scratch memory)
+  auto acc_half = [&](int qg, int i, bool upper) { return upper ? acc[qg][4 + i] : acc[qg][i]; };
+  {
+    f32x4 *mine = red_o + ((qh * 2 + kh) * 2) * 4 * 64;
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
+      if (khu == 0) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) red_o[(qg * 8 + dt) * 64 + lane] = acc[qg][dt];
+        for (int i = 0; i < 4; ++i) mine[(qg * 4 + i) * 64 + lane] = acc_half(qg, i, true);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mine[(qg * 4 + i) * 64 + lane] = acc_half(qg, i, false);
+      }
       if (g == 0) {
-        red_ml[(qg * 2 + 0) * 16 + c16] = m[qg];
-        red_ml[(qg * 2 + 1) * 16 + c16] = l[qg];
+        red_ml[(((qh * 2 + kh) * 2 + qg) * 2 + 0) * 16 + c16] = m[qg];
+        red_ml[(((qh * 2 + kh) * 2 + qg) * 2 + 1) * 16 + c16] = l[qg];
       }
     }
   }
   __syncthreads();
-  if (kh == 1) return;
+  {
+    const int ok = 1 - kh;  // the partner wave
+    const f32x4 *theirs = red_o + ((qh * 2 + ok) * 2) * 4 * 64;
+    f32x4 o2[2][4];
+    float m2[2], l2[2];
 #pragma unroll
-  for (int qg = 0; qg < 2; ++qg) {
-    const float m2 = red_ml[(qg * 2 + 0) * 16 + c16], l2 = red_ml[(qg * 2 + 1) * 16 + c16];
-    const float M = pf_max(m[qg], m2);
-    const float a1 = (m[qg] == NEG_INF) ? 0.f : fast_exp2((m[qg] - M) * p.qscale);
-    const float a2 = (m2 == NEG_INF) ? 0.f : fast_exp2((m2 - M) * p.qscale);
-    const float L = l[qg] * a1 + l2 * a2;
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    if (q_row[qg] >= p.T) continue;
+    for (int qg = 0; qg < 2; ++qg) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const f32x4 o2 = red_o[(qg * 8 + dt) * 64 + lane];
-      f32x4 r;
+      for (int i = 0; i < 4; ++i) o2[qg][i] = theirs[(qg * 4 + i) * 64 + lane];
+      m2[qg] = red_ml[(((qh * 2 + ok) * 2 + qg) * 2 + 0) * 16 + c16];
+      l2[qg] = red_ml[(((qh * 2 + ok) * 2 + qg) * 2 + 1) * 16 + c16];
+    }
+    f32x4 r[2][4];
+    bool live[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = (acc[qg][dt][e] * a1 + o2[e] * a2) * inv;
-      store4(qg, dt, r);
+    for (int qg = 0; qg < 2; ++qg) {
+      const float M = pf_max(m[qg], m2[qg]);
+      const float a1 = (m[qg] == NEG_INF) ? 0.f : fast_exp2((m[qg] - M) * p.qscale);
+      const float a2 = (m2[qg] == NEG_INF) ? 0.f : fast_exp2((m2[qg] - M) * p.qscale);
+      const float L = l[qg] * a1 + l2[qg] * a2;
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      const float b1 = a1 * inv, b2 = a2 * inv;
+      if (khu == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[qg][i] = acc_half(qg, i, false) * b1 + o2[qg][i] * b2;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[qg][i] = acc_half(qg, i, true) * b1 + o2[qg][i] * b2;
+      }
+      live[qg] = q_row[qg] < p.T;
+    }
+    if (p.out_dt == LA_BF16) {
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg)
+        if (live[qg])
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int64_t o = b * p.o_sb + h * p.o_sh + q_row[qg] * p.o_st + 16 * (4 * kh + i) + 4 * g;
+            const bf16x2 x = __builtin_convertvector((f32x2{r[qg][i][0], r[qg][i][1]}), bf16x2);
+            const bf16x2 y = __builtin_convertvector((f32x2{r[qg][i][2], r[qg][i][3]}), bf16x2);
+            const u32x2 u = {__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, y)};
+            __builtin_nontemporal_store(u, (u32x2 *)((uint16_t *)p.out + o));
+          }
+    } else {
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg)
+        if (live[qg])
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int64_t o = b * p.o_sb + h * p.o_sh + q_row[qg] * p.o_st + 16 * (4 * kh + i) + 4 * g;
+            __builtin_nontemporal_store(r[qg][i], (f32x4 *)((float *)p.out + o));
+          }
     }
   }
 }
