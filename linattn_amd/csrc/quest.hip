@@ -334,9 +334,13 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
     uint64_t u[KPL];
 #pragma unroll
     for (int j = 0; j < KPL; ++j) u[j] = keys[g * NP + lane + 64 * j];
-    tk_wave_select_bits<KPL>(u, n_v, K, [&](int j, int32_t i, bool take) {
-      if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
-    });
+    // the wave's own key row (already in registers) is its selection scratch
+    __builtin_amdgcn_wave_barrier();
+    tk_wave_select_bits<KPL>(
+        u, n_v, K, [&](int j, int32_t i, bool take) {
+          if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
+        },
+        keys + g * NP);
   }
   __syncthreads();
   tk_emit_bitmap_row(bm, n_v, own, 0, 0, a.width, a.out_idx + row * a.width,

@@ -283,9 +283,15 @@ __device__ __forceinline__ void tk_reg_select_bits(uint64_t (&u)[KPT], int32_t n
 // T ends as the K-th largest key and its ties go to the lowest index.  No
 // LDS and no barrier.  Same selection as tk_reg_select.  emit(j, i, take) is
 // called by every lane for every slot j in increasing j.
+// With `scratch` (this wave's own LDS, >= TK_WCAP keys), once at most TK_WCAP
+// keys reach T the search continues over those candidates only, two per lane
+// (the keys below T can no longer be selected and do not change any later
+// count): the low bits cost two compares per step instead of KPL.
+constexpr int TK_WCAP = 128;
 template <int KPL, class Emit>
 __device__ __forceinline__ void tk_wave_select_bits(const uint64_t (&u_in)[KPL], int32_t n_v,
-                                                    uint32_t K, Emit emit) {
+                                                    uint32_t K, Emit emit,
+                                                    uint64_t *scratch = nullptr) {
   const int lane = threadIdx.x & 63;
   uint64_t u[KPL];  // units past n_v count as key 0, which no candidate reaches
 #pragma unroll
@@ -297,7 +303,34 @@ __device__ __forceinline__ void tk_wave_select_bits(const uint64_t (&u_in)[KPL],
   }
   uint64_t T = 0;  // count(u >= T) >= K throughout
   bool exact = false;
-  for (int bit = 63; bit >= 0; --bit) {
+  int bit = 63;
+  bool narrowed = false;
+  if (scratch) {
+    // the bits that every valid key shares are in T from the start (every
+    // valid key still reaches it): the search starts below them.  A forced
+    // unit (KEY_FORCED, above every score) is left out of the prefix: it
+    // reaches any T.
+    uint64_t hi = 0, lo = ~0ull;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const bool valid = lane + 64 * j < n_v && u[j] != KEY_FORCED;
+      hi = valid && u[j] > hi ? u[j] : hi;
+      lo = valid && u[j] < lo ? u[j] : lo;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t h2 = __shfl_xor(hi, o, 64), l2 = __shfl_xor(lo, o, 64);
+      hi = h2 > hi ? h2 : hi;
+      lo = l2 < lo ? l2 : lo;
+    }
+    const uint64_t diff = hi ^ lo;
+    if (hi >= lo && diff != 0) {
+      const int top = 63 - __clzll(diff);  // highest differing bit
+      T = hi & ~((2ull << top) - 1ull);     // (top == 63: no shared bits, T = 0)
+      bit = top;
+    }
+  }
+  for (; bit >= 0; --bit) {
     const uint64_t T2 = T | (1ull << bit);
     uint32_t c = 0;
 #pragma unroll
@@ -308,7 +341,40 @@ __device__ __forceinline__ void tk_wave_select_bits(const uint64_t (&u_in)[KPL],
         exact = true;
         break;
       }
+      if (KPL > 2 && scratch && c <= (uint32_t)TK_WCAP) {
+        narrowed = true;
+        --bit;
+        break;
+      }
     }
+  }
+  if (KPL > 2 && narrowed) {
+    // compact the keys >= T (at most TK_WCAP) and finish the search on them
+    const uint64_t lt = lanemask_lt(lane);
+    uint32_t base = 0;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const bool cand = u[j] >= T;
+      const uint64_t b = __ballot(cand);
+      if (cand) scratch[base + (uint32_t)__popcll(b & lt)] = u[j];
+      base += (uint32_t)__popcll(b);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const uint64_t v0 = (uint32_t)lane < base ? scratch[lane] : 0ull;
+    const uint64_t v1 = (uint32_t)lane + 64 < base ? scratch[lane + 64] : 0ull;
+    for (; bit >= 0; --bit) {
+      const uint64_t T2 = T | (1ull << bit);
+      const uint32_t c = (uint32_t)__popcll(__ballot(v0 >= T2)) + (uint32_t)__popcll(__ballot(v1 >= T2));
+      if (c >= K) {
+        T = T2;
+        if (c == K) {
+          exact = true;
+          break;
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the scratch may be reused by the caller
   }
   if (exact) {
 #pragma unroll
