@@ -358,7 +358,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ u32x4 load16_async(const void *ptr) {
   u32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr));
+  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(ptr));
   return v;
 }
 

@@ -233,6 +233,18 @@ struct QsKP {
   int32_t q_dt;
 };
 
+// read-once metadata: nontemporal loads
+__device__ __forceinline__ uint2 ntl(const uint2 *p) {
+  typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+  const v2u x = __builtin_nontemporal_load((const v2u *)p);
+  return uint2{x[0], x[1]};
+}
+__device__ __forceinline__ float4 ntl(const float4 *p) {
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  const v4f x = __builtin_nontemporal_load((const v4f *)p);
+  return float4{x[0], x[1], x[2], x[3]};
+}
+
 template <int MT, int G, int KPT>
 __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
   constexpr int NP = TK_NT * KPT;  // pages held (>= n_pages)
@@ -280,8 +292,8 @@ __global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
 #pragma unroll
         for (int j = 0; j < QD; ++j) {
           const int d = min(d0 + j, Dn - 1);
-          lo_v[buf][j] = pl[d * sd];
-          hi_v[buf][j] = ph[d * sd];
+          lo_v[buf][j] = ntl(pl + d * sd);
+          hi_v[buf][j] = ntl(ph + d * sd);
         }
       };
       auto widen = [](const V &v, double (&x)[PPT]) {

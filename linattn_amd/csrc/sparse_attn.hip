@@ -64,6 +64,18 @@ struct KvTraits<LA_FP8_E4M3> {
   using Vec = uint2;
 };
 
+// streamed (read-once) K/V rows: nontemporal loads
+__device__ __forceinline__ uint4 nt_ld(const uint4 *p) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  const v4u x = __builtin_nontemporal_load((const v4u *)p);
+  return uint4{x[0], x[1], x[2], x[3]};
+}
+__device__ __forceinline__ uint2 nt_ld(const uint2 *p) {
+  typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+  const v2u x = __builtin_nontemporal_load((const v2u *)p);
+  return uint2{x[0], x[1]};
+}
+
 template <int KT, int EPL>
 __device__ __forceinline__ void unpack(const typename KvTraits<KT>::Vec &v, float (&x)[EPL]) {
   if constexpr (KT == LA_F32) {
@@ -566,7 +578,7 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
       kok = rd_next.tok >= 0 && rd_next.tok + c <= lim32;
       const char *rp = rd_next.tok >= 0 ? kbase + rd_next.kb * ESZ : kbase;  // wave-uniform
 #pragma unroll
-      for (int s = 0; s < (F8 ? 2 : 4); ++s) kr[s] = *(const uint4 *)(rp + koff + 16 * (F8 ? 1 : 4) * s);
+      for (int s = 0; s < (F8 ? 2 : 4); ++s) kr[s] = nt_ld((const uint4 *)(rp + koff + 16 * (F8 ? 1 : 4) * s));
       if constexpr (F8) f8s.k = p.kv.k_scale[(rd_next.tok >= 0 ? rd_next.kb / D : 0) + c];
     } else {
       int64_t ko = 0, vo = 0, so = 0;
@@ -588,7 +600,7 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
     if constexpr (U16) {
       const bool ok = rd_next.tok >= 0 && rd_next.tok + 4 * u + slot <= lim32;
       const char *rp = rd_next.tok >= 0 ? vbase + rd_next.vb * ESZ : vbase;  // wave-uniform
-      const VVec x = *(const VVec *)(rp + voff + 4 * u * D * ESZ);
+      const VVec x = nt_ld((const VVec *)(rp + voff + 4 * u * D * ESZ));
       if constexpr (F8) vr[u] = ok ? x : uint2{0, 0}; else vr[u] = ok ? x : uint4{0, 0, 0, 0};
       if constexpr (F8) {
         const float sv = p.kv.v_scale[(rd_next.tok >= 0 ? rd_next.vb / D : 0) + 4 * u + slot];
