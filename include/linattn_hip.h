@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 7
+#define LA_ABI_VERSION 8
 
 /* element types */
 enum {
@@ -370,6 +370,12 @@ int la_indexer_topk(const la_indexer_args *a, void *stream);
  * Output out_idx (B, Hq, nqb, width) ascending, -1 padded; out_count (B,Hq,nqb).
  * The positive 1/sqrt(D) factor of the reference does not change the ranking
  * and is not applied.
+ * Ragged batches: lengths (optional, int32 [B] on the device) gives sequence
+ * b's length L_b in [0, T]; its rows past L_b are padding and are never read
+ * (the tail block repeats row L_b - 1), query blocks at or past L_b get empty
+ * lists (count 0), and every other list equals that of a call on sequence b
+ * alone with T = L_b.  The reference batches equal lengths only
+ * (core.py:250-252; its roadmap, docs/roadmap.md:6-25, names this extension).
  */
 typedef struct {
   const void *q;
@@ -384,6 +390,7 @@ typedef struct {
   int64_t block, topk, sink_blocks, window_blocks, width;
   int32_t in_dtype;
   int32_t reserved;
+  const int32_t *lengths; /* optional: per-sequence lengths (ragged batch) */
 } la_block_select_args;
 
 size_t la_block_select_workspace(const la_block_select_args *a);
@@ -480,6 +487,10 @@ int la_xattn_select(const la_xattn_select_args *a, void *stream);
  * the workspace, each 64-token block scaled by a power of two that keeps it
  * in fp16 range).  scale must be positive.  Workspace:
  * la_block_sparse_prefill_workspace() bytes, 256-byte aligned.
+ * Ragged batches: lengths (optional, int32 [B] on the device) gives sequence
+ * b's length L_b in [0, T]; q/k/v rows of sequence b at or past L_b are
+ * padding and are never read, its output rows there are written as zeros,
+ * and its other rows equal a call on sequence b alone with T = L_b.
  */
 typedef struct {
   const void *q;
@@ -500,6 +511,7 @@ typedef struct {
   int32_t causal;
   int32_t out_dtype;
   int32_t reserved;
+  const int32_t *lengths; /* optional: per-sequence lengths (ragged batch) */
 } la_prefill_args;
 
 size_t la_block_sparse_prefill_workspace(const la_prefill_args *a);

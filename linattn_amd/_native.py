@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -116,7 +116,7 @@ class LaBlockSelectArgs(ctypes.Structure):
                 ("D", _i64), ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64), ("k_sb", _i64),
                 ("k_sh", _i64), ("k_st", _i64), ("block", _i64), ("topk", _i64),
                 ("sink_blocks", _i64), ("window_blocks", _i64), ("width", _i64),
-                ("in_dtype", _i32), ("reserved", _i32)]
+                ("in_dtype", _i32), ("reserved", _i32), ("lengths", _vp)]
 
 
 class LaGateSelectArgs(ctypes.Structure):
@@ -144,7 +144,7 @@ class LaPrefillArgs(ctypes.Structure):
                 ("k_st", _i64), ("v_sb", _i64), ("v_sh", _i64), ("v_st", _i64), ("o_sb", _i64),
                 ("o_sh", _i64), ("o_st", _i64), ("block", _i64), ("width", _i64),
                 ("scale", ctypes.c_float), ("causal", _i32), ("out_dtype", _i32),
-                ("reserved", _i32)]
+                ("reserved", _i32), ("lengths", _vp)]
 
 
 _LIB: Optional[ctypes.CDLL] = None

@@ -18,13 +18,24 @@
 
 namespace la {
 
-// qbar/kbar[b][h][blk][d] = (sum_{i<bs} x[b][h][min(blk*bs+i, T-1)][d]) / bs
+// Rows of sequence b: lens[b] (clamped to [0, T]) in a ragged batch, else T.
+__device__ __forceinline__ int64_t seq_rows(const int32_t *lens, int64_t b, int64_t T) {
+  return lens ? min(max((int64_t)lens[b], (int64_t)0), T) : T;
+}
+
+// qbar/kbar[b][h][blk][d] = (sum_{i<bs} x[b][h][min(blk*bs+i, T_b-1)][d]) / bs
+// (T_b = seq_rows; a sequence without rows pools zeros, which no list reads)
 __global__ __launch_bounds__(128) void mean_pool_kernel(const void *x, int dt, int64_t T, int64_t D,
                                                         int64_t sb, int64_t sh, int64_t st,
                                                         int64_t bs, int64_t H, int64_t nb,
-                                                        double *out) {
+                                                        double *out, const int32_t *lens) {
   const int64_t blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int64_t base = b * sb + h * sh;
+  T = seq_rows(lens, b, T);
+  if (T == 0) {
+    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) out[((b * H + h) * nb + blk) * D + d] = 0.0;
+    return;
+  }
   for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
     double acc = 0.0;
     for (int64_t i = 0; i < bs; ++i) {
@@ -43,11 +54,17 @@ template <int ESZ, int NT>
 __global__ __launch_bounds__(NT) void mean_pool_vec_kernel(const void *x, int dt, int64_t T,
                                                             int64_t D, int64_t sb, int64_t sh,
                                                             int64_t st, int64_t bs, int64_t H,
-                                                            int64_t nb, double *out) {
+                                                            int64_t nb, double *out,
+                                                            const int32_t *lens) {
   extern __shared__ __align__(16) unsigned char rows[];  // bs rows of D * ESZ bytes
   constexpr int CH = 64 * 512 / 16 / NT;                  // chunks per thread (max)
   const int64_t blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
+  T = seq_rows(lens, b, T);
+  if (T == 0) {  // (workgroup-uniform)
+    for (int64_t d = tid; d < D; d += NT) out[((b * H + h) * nb + blk) * D + d] = 0.0;
+    return;
+  }
   const int rb = (int)(D * ESZ);  // bytes per row
   const int cpr = rb / 16;
   const int total = (int)bs * cpr;
@@ -143,11 +160,12 @@ __global__ __launch_bounds__(BS_NT) void block_score_kernel(const double *qbar, 
   }
 }
 
-// Mean of every `bs` rows of x[b][h] (rows past T repeat row T-1) into
-// out[b][h][blk][d] in fp64; bs = 1 is the exact widening to fp64.
+// Mean of every `bs` rows of x[b][h] (rows past T_b repeat row T_b-1) into
+// out[b][h][blk][d] in fp64; bs = 1 is the exact widening to fp64.  T_b is
+// lens[b] (ragged batch) or T.
 static void pool_rows(const void *x, int dt, int64_t B, int64_t H, int64_t T, int64_t D, int64_t sb,
                       int64_t sh, int64_t s_t, int64_t bs, int64_t nb, double *out,
-                      hipStream_t st) {
+                      hipStream_t st, const int32_t *lens = nullptr) {
   const int64_t esz = dt == LA_F32 ? 4 : 2;
   const dim3 grid((unsigned)nb, (unsigned)H, (unsigned)B);
   const bool vec = bs <= 64 && (D * esz) % 16 == 0 && D * esz <= 512 && (uintptr_t)x % 16 == 0 &&
@@ -156,15 +174,15 @@ static void pool_rows(const void *x, int dt, int64_t B, int64_t H, int64_t T, in
   // 128 threads when one thread per d covers the row (the block stays in LDS
   // only while it is summed, so several blocks per CU overlap)
   if (vec && esz == 4 && D <= 128)
-    mean_pool_vec_kernel<4, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+    mean_pool_vec_kernel<4, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
   else if (vec && esz == 4)
-    mean_pool_vec_kernel<4, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+    mean_pool_vec_kernel<4, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
   else if (vec && D <= 128)
-    mean_pool_vec_kernel<2, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+    mean_pool_vec_kernel<2, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
   else if (vec)
-    mean_pool_vec_kernel<2, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+    mean_pool_vec_kernel<2, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
   else
-    mean_pool_kernel<<<grid, 128, 0, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out);
+    mean_pool_kernel<<<grid, 128, 0, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
 }
 
 struct BsLayout {
@@ -217,10 +235,10 @@ extern "C" int la_block_select(const la_block_select_args *a, void *stream) {
   double *kbar = (double *)(ws + L.kbar_off);
   double *sc = (double *)(ws + L.sc_off);
   pool_rows(a->q, a->in_dtype, a->B, a->Hq, a->T, a->D, a->q_sb, a->q_sh, a->q_st, a->block, L.nqb,
-            qbar, st);
+            qbar, st, a->lengths);
   LA_LAUNCHED();
   pool_rows(a->k, a->in_dtype, a->B, a->Hkv, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block, L.nkb,
-            kbar, st);
+            kbar, st, a->lengths);
   LA_LAUNCHED();
   block_score_kernel<<<dim3((unsigned)ceil_div(L.nkb, BS_TK), (unsigned)ceil_div(L.nqb, BS_TQ),
                             (unsigned)(a->B * a->Hq)),
@@ -244,6 +262,10 @@ extern "C" int la_block_select(const la_block_select_args *a, void *stream) {
   tp.order = 1;
   tp.out_idx = a->out_idx;
   tp.out_count = a->out_count;
+  // ragged: the query blocks of sequence b at or past its length select nothing
+  tp.b_lens = a->lengths;
+  tp.rows_per_b = a->Hq * L.nqb;
+  tp.b_len_unit = a->block;
   return topk_launch(tp, st);
 }
 

@@ -108,6 +108,7 @@ struct PfKP {
   float qscale;   // scale * log2(e)
   float thr_gap;  // 8 / qscale: raw-score headroom above the reference maximum
   int32_t causal, out_dt;
+  const int32_t *lens;  // ragged batch: rows of sequence b (clamped to [0, T]); null: T
 };
 
 // Status bits this file's kernels raise on the current device (read through
@@ -122,14 +123,20 @@ __device__ uint32_t la_pf_status;
 __global__ __launch_bounds__(256) void prefill_v16_kernel(const uint16_t *v, int64_t v_sb,
                                                           int64_t v_sh, int64_t v_st, int64_t Hkv,
                                                           int64_t T, int64_t nkb, uint16_t *v16,
-                                                          int32_t *vexp) {
+                                                          int32_t *vexp, const int32_t *lens) {
   __shared__ uint32_t wmax[4];
   const int64_t blk = blockIdx.x;
   const int64_t kb = blk % nkb, bh = blk / nkb;
   const int64_t b = bh / Hkv, kvh = bh % Hkv;
   const int tid = threadIdx.x;
+  const int64_t Tfull = T;
+  if (lens) T = min(max((int64_t)lens[b], (int64_t)0), T);  // ragged: rows past T_b are padding
+  if (kb * PF_BS >= T) {  // a block of padding only: never listed
+    if (tid == 0) vexp[blk] = 0;
+    return;
+  }
   const uint16_t *src = v + b * v_sb + kvh * v_sh;
-  uint16_t *dst = v16 + bh * T * PF_D;
+  uint16_t *dst = v16 + bh * Tfull * PF_D;
   u32x4 x[4];
   uint32_t mx = 0;
 #pragma unroll
@@ -194,7 +201,10 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 
   const int qh = w >> 1, kh = w & 1;  // query half, key half
   const int qhu = __builtin_amdgcn_readfirstlane(qh), khu = __builtin_amdgcn_readfirstlane(kh);
-  const int T32 = (int)p.T, nkb32 = (int)p.nkb;
+  // rows of this sequence (a ragged batch's shorter sequences end early; their
+  // padding rows are never read)
+  const int64_t Tb = p.lens ? min(max((int64_t)sload_i32(p.lens + b), (int64_t)0), p.T) : p.T;
+  const int T32 = (int)Tb, nkb32 = (int)p.nkb;
   int64_t q_row[2];                    // this lane's query in each 16-query group
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg) q_row[qg] = qb * PF_BS + 32 * qh + 16 * qg + c16;
@@ -207,6 +217,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   const int o1 = __builtin_amdgcn_readfirstlane(p.width > 1 ? 1 : 0);
   sload3_i32(cnt_p, list, list + o1, n, kbj, kb1);
   n = p.counts ? min(n, (int)p.width) : (int)p.width;
+  if (qb * PF_BS >= Tb) n = 0;  // a query block past the sequence's end attends nothing
 
   // four output values of query group qg: dims 16 dt + 4 g .. + 3
   auto store4 = [&](int qg, int dt, f32x4 r) {
@@ -264,7 +275,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     } else {  // a partial last block or a -1 entry: rows clamped into [0, T)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int64_t key = min((int64_t)max(kb, 0) * PF_BS + 16 * t + drow, p.T - 1);
+        const int64_t key = min((int64_t)max(kb, 0) * PF_BS + 16 * t + drow, Tb - 1);
         asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(bh + key * st + 8 * dch),
                      "{m0}"(m0 + 2 * 16 * t * PF_D) : "memory");
       }
@@ -399,7 +410,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // q, read once: streamed past the caches that keep the K/V blocks
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg) {
-    const uint16_t *qp = p.q + b * p.q_sb + h * p.q_sh + min(q_row[qg], p.T - 1) * p.q_st;
+    const uint16_t *qp = p.q + b * p.q_sb + h * p.q_sh + min(q_row[qg], Tb - 1) * p.q_st;
 #pragma unroll
     for (int s = 0; s < 4; ++s) qreg[qg][s] = __builtin_nontemporal_load((const bf16x8 *)(qp + 32 * s + 8 * g));
   }
@@ -626,6 +637,9 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
         for (int i = 0; i < 4; ++i) r[qg][i] = acc_half(qg, i, true) * b1 + o2[qg][i] * b2;
       }
       live[qg] = q_row[qg] < p.T;
+      if (q_row[qg] >= Tb)  // padding rows of a shorter sequence are written as zeros
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[qg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     if (p.out_dt == LA_BF16) {
 #pragma unroll
@@ -720,7 +734,8 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   const int64_t nvb = a->B * a->Hkv * nkb;
   LA_REQUIRE(nvb < ((int64_t)1 << 31), "la_block_sparse_prefill: too many key blocks");
   prefill_v16_kernel<<<dim3((unsigned)nvb), 256, 0, st>>>((const uint16_t *)a->v, a->v_sb, a->v_sh,
-                                                          a->v_st, a->Hkv, a->T, nkb, v16, vexp);
+                                                          a->v_st, a->Hkv, a->T, nkb, v16, vexp,
+                                                          a->lengths);
   LA_LAUNCHED();
   PfKP p{};
   p.q = (const uint16_t *)a->q;
@@ -753,6 +768,7 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   p.sh_hkv = log2_or(a->Hkv);
   p.causal = a->causal;
   p.out_dt = a->out_dtype;
+  p.lens = a->lengths;
   const int64_t nwg = a->B * a->Hq * p.nqb;
   LA_REQUIRE(nwg < ((int64_t)1 << 31), "la_block_sparse_prefill: too many query blocks");
   prefill_kernel<<<dim3((unsigned)nwg), PF_NT, 0, st>>>(p);

@@ -33,6 +33,11 @@ struct TopkKParams {
   int64_t seg_len, nseg;
   // candidate rows: output index = cand_idx[row slot] instead of the position
   const int32_t *cand_idx;
+  // ragged batches (may be null): row t of batch item br / rows_per_b has no
+  // units at all once t * b_len_unit >= b_lens[item] (a row past the end of a
+  // shorter sequence: nothing selected, no sink, no own unit)
+  const int32_t *b_lens;
+  int64_t rows_per_b, b_len_unit;
 };
 
 // The row (group) a workgroup selects for, its valid prefix and forced unit.
@@ -60,6 +65,10 @@ __device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
   }
   if (p.n_valid_tab) n_v = min(p.n, (int64_t)p.n_valid_tab[r.t]);
   if (p.own_tab) own = (int64_t)p.own_tab[r.t];
+  if (p.b_lens && r.t * p.b_len_unit >= (int64_t)p.b_lens[r.br / p.rows_per_b]) {
+    n_v = 0;
+    own = -1;
+  }
   if (p.seg_len > 0) n_v = min(n_v - r.seg0, min(p.seg_len, p.n - r.seg0));
   r.n_v = max(n_v, (int64_t)0);
   r.own = own;

@@ -29,12 +29,27 @@ def _s3(t):
     return s[0], s[1], s[2]
 
 
+def _lengths(lengths: Optional[torch.Tensor], B: int) -> Optional[torch.Tensor]:
+    """Per-sequence lengths of a ragged batch: int32 (B,) on the device (values
+    are clamped to [0, T] by the kernels)."""
+    if lengths is None:
+        return None
+    if lengths.dtype != torch.int32 or lengths.shape != (B,):
+        raise ValueError(f"lengths must be int32 ({B},)")
+    return lengths.contiguous()
+
+
 def block_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 64, topk: int = 16,
-                     sink_blocks: int = 1, window_blocks: int = 4
+                     sink_blocks: int = 1, window_blocks: int = 4,
+                     lengths: Optional[torch.Tensor] = None
                      ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Key-block lists (B, Hq, n_qb, topk+sink+window) int32, ascending, -1
-    padded, and counts (B, Hq, n_qb).  q (B, Hq, T, D), k (B, Hkv, T, D)."""
-    dev = N.require_gpu(q, k, what="block_select_hip")
+    padded, and counts (B, Hq, n_qb).  q (B, Hq, T, D), k (B, Hkv, T, D).
+
+    ``lengths`` (int32 (B,), optional): a ragged batch padded to T; sequence
+    b's rows past lengths[b] are never read, its query blocks past the end get
+    empty lists, and its other lists equal a call on that sequence alone."""
+    dev = N.require_gpu(q, k, lengths, what="block_select_hip")
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
     if k.shape != (B, Hkv, T, D):
@@ -53,6 +68,8 @@ def block_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 64, topk:
     a.block, a.topk, a.sink_blocks, a.window_blocks, a.width = block, topk, sink_blocks, \
         window_blocks, width
     a.in_dtype = N.dtype_code(q.dtype)
+    lengths = _lengths(lengths, B)
+    a.lengths = N.ptr(lengths)
     L = N.load()
     ws_bytes = L.la_block_select_workspace(ctypes.byref(a))
     ws = N.workspace(ws_bytes, dev)
@@ -64,13 +81,16 @@ def block_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 64, topk:
 def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: torch.Tensor,
                          counts: Optional[torch.Tensor] = None, *, block_size: int = 64,
                          causal: bool = True, scale: Optional[float] = None,
-                         out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+                         out_dtype: Optional[torch.dtype] = None,
+                         lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Attention of every 64-query block over its listed 64-key blocks.
 
     q (B, Hq, T, 128), k/v (B, Hkv, T, 128) bf16; ids int32 (B, Hq, n_qb, W)
     (-1 entries read nothing); counts optional (B, Hq, n_qb).  Returns
-    (B, Hq, T, 128) in ``out_dtype`` (default q.dtype)."""
-    dev = N.require_gpu(q, k, v, ids, counts, what="block_sparse_prefill")
+    (B, Hq, T, 128) in ``out_dtype`` (default q.dtype).  ``lengths`` (int32
+    (B,), optional): a ragged batch; rows of sequence b at or past lengths[b]
+    are never read and come out as zeros."""
+    dev = N.require_gpu(q, k, v, ids, counts, lengths, what="block_sparse_prefill")
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
@@ -98,6 +118,8 @@ def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids:
     a.scale = float(scale if scale is not None else 1.0 / math.sqrt(D))
     a.causal = 1 if causal else 0
     a.out_dtype = N.dtype_code(out.dtype)
+    lengths = _lengths(lengths, B)
+    a.lengths = N.ptr(lengths)
     L = N.load()
     ws_bytes = L.la_block_sparse_prefill_workspace(ctypes.byref(a))
     ws = N.workspace(ws_bytes, dev)
@@ -109,11 +131,13 @@ def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids:
 
 def sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int = 64,
                    topk: int = 16, sink_blocks: int = 1, window_blocks: int = 4,
-                   out_dtype: Optional[torch.dtype] = None
+                   out_dtype: Optional[torch.dtype] = None,
+                   lengths: Optional[torch.Tensor] = None
                    ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Config-C3 prefill: block selection then MFMA attention.  Returns
-    (out, ids, counts)."""
+    (out, ids, counts).  ``lengths``: per-sequence lengths of a ragged batch."""
     ids, counts = block_select_hip(q, k, block=block, topk=topk, sink_blocks=sink_blocks,
-                                   window_blocks=window_blocks)
-    out = block_sparse_prefill(q, k, v, ids, counts, block_size=block, out_dtype=out_dtype)
+                                   window_blocks=window_blocks, lengths=lengths)
+    out = block_sparse_prefill(q, k, v, ids, counts, block_size=block, out_dtype=out_dtype,
+                               lengths=lengths)
     return out, ids, counts

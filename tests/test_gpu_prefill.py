@@ -205,3 +205,40 @@ def test_prefill_large_v_blocks(dev):
                                 out_dtype=torch.float32)
     assert N.device_status(dev) & N.LA_DEV_PREFILL_RANGE
     assert not torch.isfinite(out2[0, :2]).all()
+
+
+def test_ragged_batch_equals_one_call_per_sequence(dev):
+    """A ragged batch (lengths 1000, 517, 64 and 0, padded to 1000) gives, for
+    each sequence, the lists and outputs of a call on that sequence alone; its
+    query blocks past the end get empty lists and its padding rows come out
+    as zeros.  Padding rows hold NaN: reading any of them would show."""
+    Tm, hq, hkv = 1000, 4, 2
+    lens = [1000, 517, 64, 0]
+    B = len(lens)
+    q, k, v = c3_inputs(B, hq, hkv, Tm, 128, seed=11)
+    for b, L in enumerate(lens):
+        q[b, :, L:] = float("nan")
+        k[b, :, L:] = float("nan")
+        v[b, :, L:] = float("nan")
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    lengths = torch.tensor(lens, dtype=torch.int32, device=dev)
+    kw = dict(topk=3, sink_blocks=1, window_blocks=2)
+    out, ids, counts = sparse_prefill(q, k, v, out_dtype=torch.float32, lengths=lengths, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    nqb = (Tm + 63) // 64
+    for b, L in enumerate(lens):
+        nb = (L + 63) // 64
+        assert (counts[b, :, nb:] == 0).all() and (ids[b, :, nb:] == -1).all()
+        assert (out[b, :, L:] == 0).all()
+        if L == 0:
+            continue
+        o1, i1, c1 = sparse_prefill(q[b:b + 1, :, :L], k[b:b + 1, :, :L], v[b:b + 1, :, :L],
+                                    out_dtype=torch.float32, **kw)
+        assert torch.equal(ids[b:b + 1, :, :nb], i1), b
+        assert torch.equal(counts[b:b + 1, :, :nb], c1), b
+        assert torch.equal(out[b:b + 1, :, :L], o1), b
+    # the lists of the full-length sequence also match the CPU oracle
+    ref = oracle.block_select(q[:1].cpu(), k[:1].cpu(), block=64, **kw)
+    assert np.array_equal(ids[:1].cpu().numpy(), ref)
+    assert nqb == ids.shape[2]
