@@ -491,6 +491,13 @@ int la_xattn_select(const la_xattn_select_args *a, void *stream);
  * b's length L_b in [0, T]; q/k/v rows of sequence b at or past L_b are
  * padding and are never read, its output rows there are written as zeros,
  * and its other rows equal a call on sequence b alone with T = L_b.
+ * fp8 K/V (kv_dtype LA_FP8_E4M3): k/v hold OCP e4m3 codes (element strides in
+ * bytes, 8-byte aligned rows) with per-token fp32 scales k_scale/v_scale
+ * (B, Hkv, T) at strides s_sb/s_sh/s_st, the codec of kv/quant.py:76-109
+ * with group_size == head_dim.  K's codes are scored exactly (fp16 MFMA
+ * against q converted per row to fp16 with a power-of-two scale) and each
+ * score is multiplied by its key's scale; V is dequantized into the fp16
+ * copy.  Any other kv_dtype means bf16 K/V.
  */
 typedef struct {
   const void *q;
@@ -512,6 +519,11 @@ typedef struct {
   int32_t out_dtype;
   int32_t reserved;
   const int32_t *lengths; /* optional: per-sequence lengths (ragged batch) */
+  const float *k_scale;   /* fp8 K/V only: per-token scales */
+  const float *v_scale;
+  int64_t s_sb, s_sh, s_st;
+  int32_t kv_dtype; /* LA_FP8_E4M3, or bf16 K/V */
+  int32_t reserved2;
 } la_prefill_args;
 
 size_t la_block_sparse_prefill_workspace(const la_prefill_args *a);

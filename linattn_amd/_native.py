@@ -144,7 +144,9 @@ class LaPrefillArgs(ctypes.Structure):
                 ("k_st", _i64), ("v_sb", _i64), ("v_sh", _i64), ("v_st", _i64), ("o_sb", _i64),
                 ("o_sh", _i64), ("o_st", _i64), ("block", _i64), ("width", _i64),
                 ("scale", ctypes.c_float), ("causal", _i32), ("out_dtype", _i32),
-                ("reserved", _i32), ("lengths", _vp)]
+                ("reserved", _i32), ("lengths", _vp), ("k_scale", _vp), ("v_scale", _vp),
+                ("s_sb", _i64), ("s_sh", _i64), ("s_st", _i64), ("kv_dtype", _i32),
+                ("reserved2", _i32)]
 
 
 _LIB: Optional[ctypes.CDLL] = None

@@ -109,21 +109,26 @@ struct PfKP {
   float thr_gap;  // 8 / qscale: raw-score headroom above the reference maximum
   int32_t causal, out_dt;
   const int32_t *lens;  // ragged batch: rows of sequence b (clamped to [0, T]); null: T
+  const float *kscale;  // fp8 K: per-token scales, (B, Hkv, nkb * 64), zero past T
 };
 
 // Status bits this file's kernels raise on the current device (read through
 // la_device_status).
 __device__ uint32_t la_pf_status;
 
-// V (bf16, any strides with a unit stride over D) -> fp16, one workgroup per
-// 64-token block of one (b, KV head): e = min(7, max(0, E - 141)) for the
-// block's largest |v| with biased bf16 exponent E (so |v| * 2^-e < 2^15 when
-// E <= 148), then v16 = fp16(v * 2^-e), rounded to nearest even.  Rows past
-// T are not written.
-__global__ __launch_bounds__(256) void prefill_v16_kernel(const uint16_t *v, int64_t v_sb,
-                                                          int64_t v_sh, int64_t v_st, int64_t Hkv,
-                                                          int64_t T, int64_t nkb, uint16_t *v16,
-                                                          int32_t *vexp, const int32_t *lens) {
+// V (bf16 at any strides with a unit stride over D, or fp8 e4m3 codes with
+// per-token fp32 scales) -> fp16, one workgroup per 64-token block of one
+// (b, KV head): e = min(7, max(0, E - 141)) for the block's largest |v| with
+// biased exponent E (so |v| * 2^-e < 2^15 when E <= 148), then
+// v16 = fp16(v * 2^-e), rounded to nearest even (fp8: v = code * scale in
+// fp32, the product rounded once).  Rows past T (T_b) are not written.
+template <bool F8>
+__global__ __launch_bounds__(256) void prefill_v16_kernel(const void *v, const float *vs,
+                                                          int64_t s_sb, int64_t s_sh, int64_t s_st,
+                                                          int64_t v_sb, int64_t v_sh, int64_t v_st,
+                                                          int64_t Hkv, int64_t T, int64_t nkb,
+                                                          uint16_t *v16, int32_t *vexp,
+                                                          const int32_t *lens) {
   __shared__ uint32_t wmax[4];
   const int64_t blk = blockIdx.x;
   const int64_t kb = blk % nkb, bh = blk / nkb;
@@ -135,29 +140,48 @@ __global__ __launch_bounds__(256) void prefill_v16_kernel(const uint16_t *v, int
     if (tid == 0) vexp[blk] = 0;
     return;
   }
-  const uint16_t *src = v + b * v_sb + kvh * v_sh;
   uint16_t *dst = v16 + bh * Tfull * PF_D;
-  u32x4 x[4];
-  uint32_t mx = 0;
+  float x[4][8];
+  uint32_t mx = 0;  // largest |v| as fp32 bits (NaN above inf: e then saturates)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t row = kb * PF_BS + (tid >> 4) + 16 * i;
-    x[i] = row < T ? __builtin_nontemporal_load((const u32x4 *)(src + row * v_st + 8 * (tid & 15)))
-                   : u32x4{0u, 0u, 0u, 0u};
-    const uint32_t w[4] = {x[i][0], x[i][1], x[i][2], x[i][3]};
+    const int col = 8 * (tid & 15);
+    if (row < T) {
+      if constexpr (F8) {
+        const uint8_t *src = (const uint8_t *)v + b * v_sb + kvh * v_sh + row * v_st + col;
+        const uint2 c = *(const uint2 *)src;
+        const float sc = vs[b * s_sb + kvh * s_sh + row * s_st];
+        const float2 a0 = fp8x2_to_f32<false>(c.x), a1 = fp8x2_to_f32<true>(c.x);
+        const float2 a2 = fp8x2_to_f32<false>(c.y), a3 = fp8x2_to_f32<true>(c.y);
+        x[i][0] = a0.x * sc; x[i][1] = a0.y * sc; x[i][2] = a1.x * sc; x[i][3] = a1.y * sc;
+        x[i][4] = a2.x * sc; x[i][5] = a2.y * sc; x[i][6] = a3.x * sc; x[i][7] = a3.y * sc;
+      } else {
+        const uint16_t *src = (const uint16_t *)v + b * v_sb + kvh * v_sh + row * v_st + col;
+        const u32x4 w = __builtin_nontemporal_load((const u32x4 *)src);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) mx = max(mx, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
+        for (int e = 0; e < 4; ++e) {
+          x[i][2 * e] = bf16lo(w[e]);
+          x[i][2 * e + 1] = bf16hi(w[e]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[i][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = max(mx, __float_as_uint(x[i][e]) & 0x7fffffffu);
   }
-  // |v| bit patterns order like the values (NaN above inf: e then saturates)
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
   if ((tid & 63) == 0) wmax[tid >> 6] = mx;
   __syncthreads();
   mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
-  const int e = min(7, max(0, (int)(mx >> 7) - 141));
+  const int E = (int)(mx >> 23);
+  const int e = min(7, max(0, E - 141));
   if (tid == 0) {
     vexp[blk] = e;
-    if ((int)(mx >> 7) > 148 && mx < 0x7f80u)  // finite |v| >= 2^22 (inf and NaN pass through)
+    if (E > 148 && mx < 0x7f800000u)  // finite |v| >= 2^22 (inf and NaN pass through)
       __hip_atomic_fetch_or(&la_pf_status, (uint32_t)LA_DEV_PREFILL_RANGE, __ATOMIC_RELAXED,
                             __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -165,19 +189,69 @@ __global__ __launch_bounds__(256) void prefill_v16_kernel(const uint16_t *v, int
   for (int i = 0; i < 4; ++i) {
     const int64_t row = kb * PF_BS + (tid >> 4) + 16 * i;
     if (row >= T) continue;
-    const uint32_t w[4] = {x[i][0], x[i][1], x[i][2], x[i][3]};
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float lo = __builtin_amdgcn_ldexpf(bf16lo(w[j]), -e);
-      const float hi = __builtin_amdgcn_ldexpf(bf16hi(w[j]), -e);
+      const float lo = __builtin_amdgcn_ldexpf(x[i][2 * j], -e);
+      const float hi = __builtin_amdgcn_ldexpf(x[i][2 * j + 1], -e);
       o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
     }
     *(uint4 *)(dst + row * PF_D + 8 * (tid & 15)) = uint4{o[0], o[1], o[2], o[3]};
   }
 }
 
+// fp8 e4m3 K codes -> fp16 codes (exact: every e4m3 value is an fp16 value)
+// and the per-token scales into a padded row-major copy (zero past T), one
+// workgroup per 64-token block of one (b, KV head).  Output contiguous
+// (B, Hkv, T, 128) codes and (B, Hkv, nkb * 64) scales; rows past T (T_b) of
+// the codes are not written.
+__global__ __launch_bounds__(256) void prefill_kdeq_kernel(const uint8_t *k, const float *ks,
+                                                           int64_t s_sb, int64_t s_sh, int64_t s_st,
+                                                           int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                                           int64_t Hkv, int64_t T, int64_t nkb,
+                                                           uint16_t *kout, float *kscale,
+                                                           const int32_t *lens) {
+  const int64_t blk = blockIdx.x;
+  const int64_t kb = blk % nkb, bh = blk / nkb;
+  const int64_t b = bh / Hkv, kvh = bh % Hkv;
+  const int tid = threadIdx.x;
+  const int64_t Tfull = T;
+  if (lens) T = min(max((int64_t)lens[b], (int64_t)0), T);
+  if (tid < PF_BS) {
+    const int64_t row = kb * PF_BS + tid;
+    kscale[bh * nkb * PF_BS + row] = row < T ? ks[b * s_sb + kvh * s_sh + row * s_st] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = kb * PF_BS + (tid >> 4) + 16 * i;
+    if (row >= T) continue;
+    const int col = 8 * (tid & 15);
+    const uint2 c = *(const uint2 *)(k + b * k_sb + kvh * k_sh + row * k_st + col);
+    const float2 a[4] = {fp8x2_to_f32<false>(c.x), fp8x2_to_f32<true>(c.x),
+                         fp8x2_to_f32<false>(c.y), fp8x2_to_f32<true>(c.y)};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a[j].x, a[j].y}), f16x2));
+    *(uint4 *)(kout + (bh * Tfull + row) * PF_D + col) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// KF16 (fp8 K/V): K staged as its fp16 codes (exact) and q converted to fp16
+// per query row (scaled by 2^-eq, the power of two that puts the row's
+// largest |q| just below 2^15), scores by fp16 MFMA; each raw score is then
+// multiplied by its key's scale.  Scores are kept in "lane units" (the true
+// score times 2^-eq of the lane's query); qs = qscale * 2^eq turns lane units
+// into the exponent.  Without KF16, qs = qscale.
+template <bool KF16>
 __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
+  auto qk_mfma = [](const bf16x8 &a, const bf16x8 &b, f32x4 c) {
+    if constexpr (KF16)
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  };
   // K slots 0..1, V slots 2..3 (64 KiB: two workgroups per CU); after the
   // loop, the key-half merge area
   __shared__ __align__(16) uint16_t smem[4 * PF_BLK];
@@ -316,8 +390,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const bf16x8 a = *(const bf16x8 *)&sk[koffs[s] + 16 * kt2 * PF_D];
-        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[0][s], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[1][s], s1, 0, 0, 0);
+        s0 = qk_mfma(a, qreg[0][s], s0);
+        s1 = qk_mfma(a, qreg[1][s], s1);
       }
       st[0][kt2] = s0;
       st[1][kt2] = s1;
@@ -328,6 +402,28 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // per group; thr = m + thr_gap, the raw score above which m must be raised;
   // nmu = -m * qscale (0 while m = -inf), the exponent offset of the weights
   const float NEG_INF = __int_as_float(0xff800000);
+  float qs[2] = {p.qscale, p.qscale}, tg[2] = {p.thr_gap, p.thr_gap};  // KF16: per lane and group
+  auto QS = [&](int qg) {
+    if constexpr (KF16) return qs[qg]; else return p.qscale;
+  };
+  auto TG = [&](int qg) {
+    if constexpr (KF16) return tg[qg]; else return p.thr_gap;
+  };
+  // KF16: the scales of this lane's 8 keys (16 kt2 + 4 g + e of its key half)
+  // of the block scored in the current step (skc) and of the next one (skn)
+  f32x4 skc[2] = {}, skn[2] = {};
+  auto load_ks = [&](int kb, f32x4 (&dst)[2]) {
+    const uint32_t kbc = (uint32_t)kb < (uint32_t)nkb32 ? (uint32_t)kb : 0u;
+    const float *sp = p.kscale + ((b * p.Hkv + kvh) * p.nkb + kbc) * PF_BS + 32 * kh + 4 * g;
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2) dst[kt2] = *(const f32x4 *)(sp + 16 * kt2);
+  };
+  auto scale_scores = [&](f32x4 (&sc)[2][2], const f32x4 (&sk)[2]) {
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg)
+#pragma unroll
+      for (int kt2 = 0; kt2 < 2; ++kt2) sc[qg][kt2] *= sk[kt2];
+  };
   float m[2] = {NEG_INF, NEG_INF}, thr[2] = {NEG_INF, NEG_INF}, l[2] = {0.f, 0.f};
   float nmu[2] = {0.f, 0.f};
   f32x4 acc[2][8];
@@ -381,10 +477,10 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       if (__ballot(mx[qg] > thr[qg]) != 0) {
         const float cm = pf_pair32_max(pf_pair16_max(mx[qg]));
         const float mn = pf_max(m[qg], cm);
-        alpha[qg] = (m[qg] == NEG_INF) ? 0.f : fast_exp2((m[qg] - mn) * p.qscale);
+        alpha[qg] = (m[qg] == NEG_INF) ? 0.f : fast_exp2((m[qg] - mn) * QS(qg));
         m[qg] = mn;
-        thr[qg] = mn + p.thr_gap;
-        nmu[qg] = (mn == NEG_INF) ? 0.f : -mn * p.qscale;
+        thr[qg] = mn + TG(qg);
+        nmu[qg] = (mn == NEG_INF) ? 0.f : -mn * QS(qg);
         l[qg] *= alpha[qg];
         any = true;
       }
@@ -414,11 +510,46 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) qreg[qg][s] = __builtin_nontemporal_load((const bf16x8 *)(qp + 32 * s + 8 * g));
   }
+  f32x4 sk0[2] = {};
+  if constexpr (KF16) {
+    load_ks(kbj, sk0);
+    load_ks(kb1, skc);
+  }
   wait_vmcnt<0>();
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg)
 #pragma unroll
     for (int s = 0; s < 4; ++s) settle(qreg[qg][s]);  // q landed with the first blocks
+  if constexpr (KF16) {
+    // q row -> fp16 * 2^-eq (the row's 128 values are spread over the 4
+    // lanes c16 + 16 g: their largest |q| is taken across those lanes)
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      uint32_t mb = 0;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4 w = __builtin_bit_cast(u32x4, qreg[qg][s]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mb = max(mb, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
+      }
+      const float mf = pf_pair32_max(pf_pair16_max(__uint_as_float(mb << 16)));
+      const int eq = min(127, max(-100, (int)(__float_as_uint(mf) >> 23) - 141));
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4 w = __builtin_bit_cast(u32x4, qreg[qg][s]);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = __builtin_amdgcn_ldexpf(bf16lo(w[e]), -eq);
+          const float hi = __builtin_amdgcn_ldexpf(bf16hi(w[e]), -eq);
+          o[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+        }
+        qreg[qg][s] = __builtin_bit_cast(bf16x8, o);
+      }
+      qs[qg] = __builtin_amdgcn_ldexpf(p.qscale, eq);
+      tg[qg] = 8.f / qs[qg];
+    }
+  }
   lds_barrier();
   {
     const bool c0 = !whole_block(kbj), c1 = n > 1 && !whole_block(kb1);
@@ -432,6 +563,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // scores of blocks with even / odd list position
   f32x4 sA[2][2], sB[2][2];
   scores(0, sA);
+  if constexpr (KF16) scale_scores(sA, sk0);
   if (needs_mask(kbj)) apply_mask(kbj, sA);
   {
     float mx[2], alpha[2];
@@ -457,6 +589,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     const uint32_t kbe = (uint32_t)kbj < (uint32_t)nkb32 ? (uint32_t)kbj : 0u;
     sload2_i32(list + (FULL ? j + 2 : min(j + 2, n - 1)), vexp + kbe, kb2, ev);
     if (!FULL && j + 2 >= n) kb2 = 0;
+    if constexpr (KF16) load_ks(kb2, skn);  // scored in the next step; landed by its end
     if (FULL || j + 2 < n) dma_k(kb2, par);            // held block j (scored a step ago)
     if (FULL || j + 1 < n) dma_v(kb1, 2 + (par ^ 1));  // held block j-1 (multiplied)
     const uint16_t *sk = smem + (par ^ 1) * PF_BLK;
@@ -483,12 +616,13 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kt2][s], qreg[0][s], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kt2][s], qreg[1][s], s1, 0, 0, 0);
+        s0 = qk_mfma(ka[kt2][s], qreg[0][s], s0);
+        s1 = qk_mfma(ka[kt2][s], qreg[1][s], s1);
       }
       sn[0][kt2] = s0;
       sn[1][kt2] = s1;
     }
+    if constexpr (KF16) scale_scores(sn, skc);
     // P = 2^ev * exp2(s*qscale - m*qscale) in fp16 (round to nearest even; at
     // most 2^(8+ev) <= 2^15); l sums the rounded weights times 2^-ev (exact).
     // Column c16 is this lane's query; the positive scale commutes with the
@@ -504,8 +638,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pv[e] = fast_exp2(__builtin_fmaf(st[qg][0][e], p.qscale, c));
-        pv[4 + e] = fast_exp2(__builtin_fmaf(st[qg][1][e], p.qscale, c));
+        pv[e] = fast_exp2(__builtin_fmaf(st[qg][0][e], QS(qg), c));
+        pv[4 + e] = fast_exp2(__builtin_fmaf(st[qg][1][e], QS(qg), c));
       }
       f16x2 hw[4];
 #pragma unroll
@@ -546,6 +680,10 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       }
       float alpha[2];
       if (settle_max(mx, alpha)) rescale_acc(alpha);
+    }
+    if constexpr (KF16) {
+      skc[0] = skn[0];
+      skc[1] = skn[1];
     }
     // this wave's loads have landed and every wave is done with the slots
     // that the next step refills
@@ -624,8 +762,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
       const float M = pf_max(m[qg], m2[qg]);
-      const float a1 = (m[qg] == NEG_INF) ? 0.f : fast_exp2((m[qg] - M) * p.qscale);
-      const float a2 = (m2[qg] == NEG_INF) ? 0.f : fast_exp2((m2[qg] - M) * p.qscale);
+      const float a1 = (m[qg] == NEG_INF) ? 0.f : fast_exp2((m[qg] - M) * QS(qg));
+      const float a2 = (m2[qg] == NEG_INF) ? 0.f : fast_exp2((m2[qg] - M) * QS(qg));
       const float L = l[qg] * a1 + l2[qg] * a2;
       const float inv = L > 0.f ? 1.f / L : 0.f;
       const float b1 = a1 * inv, b2 = a2 * inv;
@@ -686,9 +824,16 @@ int prefill_status(uint32_t *bits, bool clear) {
 static int64_t pf_align(int64_t x) { return (x + 255) / 256 * 256; }
 
 // Workspace: the fp16 copy of V (B, Hkv, T, 128), then the block exponents.
+static bool prefill_fp8(const la_prefill_args *a) { return a->kv_dtype == LA_FP8_E4M3; }
+
+// Workspace: the fp16 copy of V (B, Hkv, T, 128) and its block exponents;
+// for fp8 K/V also the fp16 K codes (B, Hkv, T, 128) and the padded K scales
+// (B, Hkv, nkb * 64).
 static int64_t prefill_ws_bytes(const la_prefill_args *a) {
   const int64_t nkb = ceil_div(a->T, PF_BS);
-  return pf_align(a->B * a->Hkv * a->T * PF_D * 2) + pf_align(a->B * a->Hkv * nkb * 4);
+  const int64_t kv = pf_align(a->B * a->Hkv * a->T * PF_D * 2);
+  const int64_t ex = pf_align(a->B * a->Hkv * nkb * 4);
+  return kv + ex + (prefill_fp8(a) ? kv + pf_align(a->B * a->Hkv * nkb * PF_BS * 4) : 0);
 }
 
 static int prefill_validate(const la_prefill_args *a) {
@@ -701,12 +846,23 @@ static int prefill_validate(const la_prefill_args *a) {
   LA_REQUIRE(a->width >= 1, "la_block_sparse_prefill: list width");
   LA_REQUIRE(a->T < ((int64_t)1 << 30), "la_block_sparse_prefill: T must be below 2^30");
   LA_REQUIRE(a->scale > 0.f, "la_block_sparse_prefill: scale must be positive");
-  // 16-byte vector access of q/k/v rows and of the output
-  const bool al = ((uintptr_t)a->q % 16 == 0) && ((uintptr_t)a->k % 16 == 0) &&
-                  ((uintptr_t)a->v % 16 == 0) && ((uintptr_t)a->out % 16 == 0) &&
-                  a->q_sb % 8 == 0 && a->q_sh % 8 == 0 && a->q_st % 8 == 0 && a->k_sb % 8 == 0 &&
-                  a->k_sh % 8 == 0 && a->k_st % 8 == 0 && a->v_sb % 8 == 0 && a->v_sh % 8 == 0 &&
-                  a->v_st % 8 == 0 && a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_st % 4 == 0;
+  if (prefill_fp8(a)) {
+    LA_REQUIRE(a->k_scale && a->v_scale, "la_block_sparse_prefill: fp8 K/V need k_scale and v_scale");
+    // 8-byte code loads; element strides are bytes for fp8
+    const bool al8 = (uintptr_t)a->k % 8 == 0 && (uintptr_t)a->v % 8 == 0 && a->k_sb % 8 == 0 &&
+                     a->k_sh % 8 == 0 && a->k_st % 8 == 0 && a->v_sb % 8 == 0 && a->v_sh % 8 == 0 &&
+                     a->v_st % 8 == 0;
+    LA_REQUIRE(al8, "la_block_sparse_prefill: fp8 rows must be contiguous and 8-byte aligned");
+  } else {
+    const bool alk = (uintptr_t)a->k % 16 == 0 && (uintptr_t)a->v % 16 == 0 && a->k_sb % 8 == 0 &&
+                     a->k_sh % 8 == 0 && a->k_st % 8 == 0 && a->v_sb % 8 == 0 && a->v_sh % 8 == 0 &&
+                     a->v_st % 8 == 0;
+    LA_REQUIRE(alk, "la_block_sparse_prefill: rows must be contiguous and 16-byte aligned");
+  }
+  // 16-byte vector access of q rows and of the output
+  const bool al = ((uintptr_t)a->q % 16 == 0) && ((uintptr_t)a->out % 16 == 0) &&
+                  a->q_sb % 8 == 0 && a->q_sh % 8 == 0 && a->q_st % 8 == 0 &&
+                  a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_st % 4 == 0;
   LA_REQUIRE(al, "la_block_sparse_prefill: rows must be contiguous and 16-byte aligned");
   return LA_OK;
 }
@@ -733,13 +889,29 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   hipStream_t st = (hipStream_t)stream;
   const int64_t nvb = a->B * a->Hkv * nkb;
   LA_REQUIRE(nvb < ((int64_t)1 << 31), "la_block_sparse_prefill: too many key blocks");
-  prefill_v16_kernel<<<dim3((unsigned)nvb), 256, 0, st>>>((const uint16_t *)a->v, a->v_sb, a->v_sh,
-                                                          a->v_st, a->Hkv, a->T, nkb, v16, vexp,
-                                                          a->lengths);
+  const bool f8 = prefill_fp8(a);
+  if (f8)
+    prefill_v16_kernel<true><<<dim3((unsigned)nvb), 256, 0, st>>>(
+        a->v, a->v_scale, a->s_sb, a->s_sh, a->s_st, a->v_sb, a->v_sh, a->v_st, a->Hkv, a->T, nkb,
+        v16, vexp, a->lengths);
+  else
+    prefill_v16_kernel<false><<<dim3((unsigned)nvb), 256, 0, st>>>(
+        a->v, nullptr, 0, 0, 0, a->v_sb, a->v_sh, a->v_st, a->Hkv, a->T, nkb, v16, vexp, a->lengths);
   LA_LAUNCHED();
+  // fp8 K: dequantized once into fp16 with block exponents, staged like bf16 K
+  char *ws_k = (char *)a->workspace + pf_align(a->B * a->Hkv * a->T * PF_D * 2) +
+               pf_align(a->B * a->Hkv * nkb * 4);
+  uint16_t *kdq = f8 ? (uint16_t *)ws_k : nullptr;
+  float *kscale = f8 ? (float *)(ws_k + pf_align(a->B * a->Hkv * a->T * PF_D * 2)) : nullptr;
+  if (f8) {
+    prefill_kdeq_kernel<<<dim3((unsigned)nvb), 256, 0, st>>>(
+        (const uint8_t *)a->k, a->k_scale, a->s_sb, a->s_sh, a->s_st, a->k_sb, a->k_sh, a->k_st,
+        a->Hkv, a->T, nkb, kdq, kscale, a->lengths);
+    LA_LAUNCHED();
+  }
   PfKP p{};
   p.q = (const uint16_t *)a->q;
-  p.k = (const uint16_t *)a->k;
+  p.k = f8 ? kdq : (const uint16_t *)a->k;
   p.v = v16;
   p.vexp = vexp;
   p.out = a->out;
@@ -750,11 +922,15 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   p.Hkv = a->Hkv;
   p.T = a->T;
   p.q_sb = a->q_sb; p.q_sh = a->q_sh; p.q_st = a->q_st;
-  p.k_sb = a->k_sb; p.k_sh = a->k_sh; p.k_st = a->k_st;
+  if (f8) {
+    p.k_st = PF_D; p.k_sh = a->T * PF_D; p.k_sb = a->Hkv * a->T * PF_D;
+  } else {
+    p.k_sb = a->k_sb; p.k_sh = a->k_sh; p.k_st = a->k_st;
+  }
   p.v_st = PF_D; p.v_sh = a->T * PF_D; p.v_sb = a->Hkv * a->T * PF_D;
-  LA_REQUIRE(nkb * PF_BS * std::max<int64_t>(a->k_st, PF_D) < ((int64_t)1 << 31),
+  LA_REQUIRE(nkb * PF_BS * std::max<int64_t>(p.k_st, PF_D) < ((int64_t)1 << 31),
              "la_block_sparse_prefill: K rows of one head span >= 2^31 elements");
-  p.k_blk = (uint32_t)(PF_BS * a->k_st);
+  p.k_blk = (uint32_t)(PF_BS * p.k_st);
   p.v_blk = (uint32_t)(PF_BS * PF_D);
   p.o_sb = a->o_sb; p.o_sh = a->o_sh; p.o_st = a->o_st;
   p.width = a->width;
@@ -769,9 +945,13 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   p.causal = a->causal;
   p.out_dt = a->out_dtype;
   p.lens = a->lengths;
+  p.kscale = kscale;
   const int64_t nwg = a->B * a->Hq * p.nqb;
   LA_REQUIRE(nwg < ((int64_t)1 << 31), "la_block_sparse_prefill: too many query blocks");
-  prefill_kernel<<<dim3((unsigned)nwg), PF_NT, 0, st>>>(p);
+  if (f8)
+    prefill_kernel<true><<<dim3((unsigned)nwg), PF_NT, 0, st>>>(p);
+  else
+    prefill_kernel<false><<<dim3((unsigned)nwg), PF_NT, 0, st>>>(p);
   LA_LAUNCHED();
   return LA_OK;
 }

@@ -82,19 +82,33 @@ def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids:
                          counts: Optional[torch.Tensor] = None, *, block_size: int = 64,
                          causal: bool = True, scale: Optional[float] = None,
                          out_dtype: Optional[torch.dtype] = None,
-                         lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
+                         lengths: Optional[torch.Tensor] = None,
+                         k_scale: Optional[torch.Tensor] = None,
+                         v_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Attention of every 64-query block over its listed 64-key blocks.
 
-    q (B, Hq, T, 128), k/v (B, Hkv, T, 128) bf16; ids int32 (B, Hq, n_qb, W)
-    (-1 entries read nothing); counts optional (B, Hq, n_qb).  Returns
-    (B, Hq, T, 128) in ``out_dtype`` (default q.dtype).  ``lengths`` (int32
-    (B,), optional): a ragged batch; rows of sequence b at or past lengths[b]
-    are never read and come out as zeros."""
-    dev = N.require_gpu(q, k, v, ids, counts, lengths, what="block_sparse_prefill")
+    q (B, Hq, T, 128) bf16; k/v (B, Hkv, T, 128) bf16, or float8_e4m3fn codes
+    with per-token fp32 scales ``k_scale``/``v_scale`` (B, Hkv, T) (the codec
+    of kv/quant.py:76-109, see ``quantize_fp8_per_token``); ids int32
+    (B, Hq, n_qb, W) (-1 entries read nothing); counts optional (B, Hq, n_qb).
+    Returns (B, Hq, T, 128) in ``out_dtype`` (default q.dtype).  ``lengths``
+    (int32 (B,), optional): a ragged batch; rows of sequence b at or past
+    lengths[b] are never read and come out as zeros."""
+    dev = N.require_gpu(q, k, v, ids, counts, lengths, k_scale, v_scale,
+                        what="block_sparse_prefill")
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
-        raise ValueError("block_sparse_prefill runs bf16 q/k/v (MFMA bf16)")
+    fp8 = k.dtype == torch.float8_e4m3fn
+    if q.dtype != torch.bfloat16 or k.dtype != v.dtype or \
+            k.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+        raise ValueError("block_sparse_prefill runs bf16 q with bf16 or fp8 e4m3 k/v")
+    if fp8:
+        if k_scale is None or v_scale is None:
+            raise ValueError("fp8 k/v need k_scale and v_scale")
+        if k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32 or \
+                k_scale.shape != (B, Hkv, T) or v_scale.shape != (B, Hkv, T) or \
+                k_scale.stride() != v_scale.stride():
+            raise ValueError("k_scale/v_scale must be fp32 (B, Hkv, T) with equal strides")
     if k.shape != (B, Hkv, T, D) or v.shape != k.shape:
         raise ValueError("k/v must be (B, Hkv, T, D)")
     nqb = (T + block_size - 1) // block_size
@@ -120,6 +134,10 @@ def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids:
     a.out_dtype = N.dtype_code(out.dtype)
     lengths = _lengths(lengths, B)
     a.lengths = N.ptr(lengths)
+    if fp8:
+        a.kv_dtype = N.dtype_code(k.dtype)
+        a.k_scale, a.v_scale = k_scale.data_ptr(), v_scale.data_ptr()
+        a.s_sb, a.s_sh, a.s_st = _s3(k_scale)
     L = N.load()
     ws_bytes = L.la_block_sparse_prefill_workspace(ctypes.byref(a))
     ws = N.workspace(ws_bytes, dev)
