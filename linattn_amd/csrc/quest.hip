@@ -38,77 +38,128 @@ __global__ __launch_bounds__(256) void page_bounds_kernel(la_kv kv, int64_t Hkv,
   }
 }
 
-// Vector form: each thread reads 16-byte chunks of the page's key rows (LPR
-// lanes per row, all rows of the page in flight at once), keeps elementwise
-// min / max, and the row groups are folded through LDS.  Needs D % EPL == 0
-// and 16-byte aligned rows; min / max are exact, so the result equals the
-// scalar form bit for bit.
-template <int KT, int D>
-__global__ __launch_bounds__(256) void page_bounds_vec_kernel(la_kv kv, int64_t Hkv, int64_t ps,
-                                                              int64_t first_page, void *mn, void *mx,
-                                                              int64_t m_sb, int64_t m_sh,
-                                                              int64_t m_sp, int64_t m_sd, int meta_dt) {
+// Wave form: a workgroup (4 waves) covers PG consecutive pages of one
+// (b, KV head), a wave one page at a time.  A lane reads 16-byte chunks (LPR
+// lanes per key row, 64 / LPR rows per pass, U nontemporal loads in flight),
+// keeps elementwise min / max in registers, and the row groups are folded
+// with lane exchanges.  The page's bounds go to LDS; once every page is done
+// the workgroup writes them out row by row (for page-minor metadata, a
+// channel's PG pages are one contiguous run, written by adjacent lanes, in
+// place of scattered 2-byte stores).  Exact, so equal to the scalar form bit
+// for bit.
+template <int KT, int D, int PG>
+__global__ __launch_bounds__(256) void page_bounds_wave_kernel(la_kv kv, int64_t Hkv, int64_t ps,
+                                                               int64_t first_page, int64_t n_pages,
+                                                               void *mn, void *mx, int64_t m_sb,
+                                                               int64_t m_sh, int64_t m_sp,
+                                                               int64_t m_sd, int meta_dt, int quad) {
   constexpr int ESZ = KT == LA_BF16 ? 2 : 4;
   constexpr int EPL = 16 / ESZ;
-  constexpr int LPR = D / EPL;   // lanes per key row
-  constexpr int RPI = 256 / LPR; // rows per pass of the workgroup
-  constexpr int UN = 4;          // passes in flight
-  __shared__ float red[2][RPI][D];
-  const int64_t p = first_page + blockIdx.x;
-  const int64_t h = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  constexpr int LPR = D / EPL;  // lanes per key row
+  constexpr int RG = 64 / LPR;  // rows per pass of the wave
+  constexpr int U = 16;         // loads in flight per lane
+  __shared__ float sb[2][D][PG + 1];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t p0 = first_page + (int64_t)blockIdx.x * PG;
+  const int np = (int)min((int64_t)PG, n_pages - p0);  // pages of this workgroup
+  const int64_t h = blockIdx.y, b = blockIdx.z;
   const int64_t len = kv_length(kv, b);
-  const int64_t t0 = p * ps;
-  const int64_t n = max((int64_t)0, min(len, t0 + ps) - t0);
-  const int c = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
-  float lo[EPL], hi[EPL];
+  const int c = lane % LPR, rg = lane / LPR;
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  // a pool whose pages are the metadata pages resolves the physical page
+  // once; other pools go row by row
+  const bool direct = !kv.page_table || kv.page_size == ps;
+  for (int pp = w; pp < np; pp += 4) {
+    const int64_t p = p0 + pp;
+    const int64_t t0 = p * ps;
+    const int64_t n = max((int64_t)0, min(len, t0 + ps) - t0);
+    float lo[EPL], hi[EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    lo[e] = __int_as_float(0x7f800000);
-    hi[e] = __int_as_float(0xff800000);
-  }
-  const char *kb = (const char *)kv.k;
-  for (int64_t r = r0; r < n; r += RPI * UN) {
-    uint4 v[UN];
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const int64_t rr = r + u * RPI;
-      v[u] = rr < n ? *(const uint4 *)(kb + (kv_row(kv, b, h, t0 + rr, Hkv, D, false) + c * EPL) * ESZ)
-                    : uint4{0, 0, 0, 0};
+    for (int e = 0; e < EPL; ++e) {
+      lo[e] = __int_as_float(0x7f800000);
+      hi[e] = __int_as_float(0xff800000);
     }
+    int64_t base = 0, rs = 0;
+    if (kv.page_table) {
+      const int64_t phys = (direct && n > 0) ? kv.page_table[b * kv.pt_stride + p] : 0;
+      base = (phys * Hkv + h) * ps * D;
+      rs = D;
+    } else {
+      base = b * kv.k_sb + h * kv.k_sh + t0 * kv.k_st;
+      rs = kv.k_st;
+    }
+    const char *kb = (const char *)kv.k + (base + c * EPL) * ESZ;
+    for (int64_t r = rg; r < n; r += (int64_t)RG * U) {
+      v4u v[U];
 #pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      if (r + u * RPI >= n) break;
-      float x[EPL];
-      if constexpr (KT == LA_BF16) {
-        x[0] = bf16lo(v[u].x); x[1] = bf16hi(v[u].x); x[2] = bf16lo(v[u].y); x[3] = bf16hi(v[u].y);
-        x[4] = bf16lo(v[u].z); x[5] = bf16hi(v[u].z); x[6] = bf16lo(v[u].w); x[7] = bf16hi(v[u].w);
-      } else {
-        x[0] = __uint_as_float(v[u].x); x[1] = __uint_as_float(v[u].y);
-        x[2] = __uint_as_float(v[u].z); x[3] = __uint_as_float(v[u].w);
+      for (int u = 0; u < U; ++u) {
+        const int64_t rr = r + u * RG;
+        const char *src = direct ? kb + rr * rs * ESZ
+                                 : (const char *)kv.k +
+                                       (kv_row(kv, b, h, t0 + rr, Hkv, D, false) + c * EPL) * ESZ;
+        v[u] = rr < n ? __builtin_nontemporal_load((const v4u *)src) : v4u{0u, 0u, 0u, 0u};
       }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (r + u * RG >= n) break;
+        float x[EPL];
+        if constexpr (KT == LA_BF16) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[2 * e] = bf16lo(v[u][e]);
+            x[2 * e + 1] = bf16hi(v[u][e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(v[u][e]);
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          lo[e] = fminf(lo[e], x[e]);
+          hi[e] = fmaxf(hi[e], x[e]);
+        }
+      }
+    }
+    // fold the row groups (lanes c, c + LPR, c + 2 LPR, ...)
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1)
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
-        lo[e] = fminf(lo[e], x[e]);
-        hi[e] = fmaxf(hi[e], x[e]);
+        lo[e] = fminf(lo[e], __shfl_xor(lo[e], o, 64));
+        hi[e] = fmaxf(hi[e], __shfl_xor(hi[e], o, 64));
       }
-    }
-  }
+    if (rg == 0)
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    red[0][r0][c * EPL + e] = lo[e];
-    red[1][r0][c * EPL + e] = hi[e];
+      for (int e = 0; e < EPL; ++e) {
+        sb[0][c * EPL + e][pp] = lo[e];
+        sb[1][c * EPL + e][pp] = hi[e];
+      }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float a = red[0][0][d], z = red[1][0][d];
-    for (int i = 1; i < RPI; ++i) {
-      a = fminf(a, red[0][i][d]);
-      z = fmaxf(z, red[1][i][d]);
+  // channel rows out: item (which, d, page), or with `quad` (page-minor
+  // metadata whose runs of four pages are 4-element aligned, every page of
+  // the workgroup valid) item (which, d, four pages) as one store
+  if (quad && np == PG) {
+    for (int i = threadIdx.x; i < 2 * D * PG / 4; i += 256) {
+      const int pp = 4 * (i % (PG / 4)), d = (i / (PG / 4)) % D, which = i / (PG / 4 * D);
+      const int64_t o = b * m_sb + h * m_sh + (p0 + pp) + (int64_t)d * m_sd;
+      const float *x = &sb[which][d][pp];
+      void *dst = which ? mx : mn;
+      if (meta_dt == LA_F32) {
+        *(float4 *)((float *)dst + o) = float4{x[0], x[1], x[2], x[3]};
+      } else {
+        const uint32_t a = (uint32_t)f32_to_bf16_bits(x[0]) | ((uint32_t)f32_to_bf16_bits(x[1]) << 16);
+        const uint32_t z = (uint32_t)f32_to_bf16_bits(x[2]) | ((uint32_t)f32_to_bf16_bits(x[3]) << 16);
+        *(uint2 *)((uint16_t *)dst + o) = uint2{a, z};
+      }
     }
-    const int64_t o = b * m_sb + h * m_sh + p * m_sp + d * m_sd;
-    store_from_f32(mn, o, meta_dt, a);
-    store_from_f32(mx, o, meta_dt, z);
+    return;
+  }
+  for (int i = threadIdx.x; i < 2 * D * PG; i += 256) {
+    const int pp = i % PG, d = (i / PG) % D, which = i / (PG * D);
+    if (pp >= np) continue;
+    const int64_t o = b * m_sb + h * m_sh + (p0 + pp) * m_sp + (int64_t)d * m_sd;
+    store_from_f32(which ? mx : mn, o, meta_dt, sb[which][d][pp]);
   }
 }
 
@@ -407,9 +458,19 @@ extern "C" int la_quest_page_bounds(const la_kv *kv, int64_t B, int64_t Hkv, int
   if (!kv->page_table)
     vec = vec && (kv->k_sb * esz) % 16 == 0 && (kv->k_sh * esz) % 16 == 0 && (kv->k_st * esz) % 16 == 0;
   if (vec) {
-#define LA_PB(KT, DD)                                                                        \
-  page_bounds_vec_kernel<KT, DD><<<grid, 256, 0, st>>>(*kv, Hkv, page_size, first_page, page_min, \
-                                                       page_max, m_sb, m_sh, m_sp, m_sd, meta_dtype)
+    constexpr int PG = 32;  // pages per workgroup
+    // four pages per store: page-minor metadata (bf16 or fp32; f16 keys never
+    // reach here), every run of four pages aligned
+    const int64_t mes = meta_dtype == LA_F32 ? 4 : 2;
+    const int quad = m_sp == 1 && m_sd % 4 == 0 && m_sh % 4 == 0 && m_sb % 4 == 0 &&
+                     first_page % 4 == 0 && (uintptr_t)page_min % (4 * mes) == 0 &&
+                     (uintptr_t)page_max % (4 * mes) == 0 &&
+                     (meta_dtype == LA_F32 || meta_dtype == LA_BF16);
+    const dim3 wgrid((unsigned)ceil_div(n_pages - first_page, (int64_t)PG), (unsigned)Hkv, (unsigned)B);
+#define LA_PB(KT, DD)                                                                      \
+  page_bounds_wave_kernel<KT, DD, PG><<<wgrid, 256, 0, st>>>(*kv, Hkv, page_size, first_page, \
+                                                             n_pages, page_min, page_max, m_sb,  \
+                                                             m_sh, m_sp, m_sd, meta_dtype, quad)
     if (kv->dtype == LA_F32) {
       if (D == 64) LA_PB(LA_F32, 64); else if (D == 128) LA_PB(LA_F32, 128); else LA_PB(LA_F32, 256);
     } else {
