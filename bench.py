@@ -80,40 +80,206 @@ def setup_c4(dev, cfg):
     return q, pool_k, pool_v, pt, mins, maxs
 
 
-def cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg, n_seq, union):
-    """Time the CPU oracle (oracle/, C + numpy, one thread) on the first n_seq
-    sequences of the same inputs: page scores, top-k, attention."""
-    import numpy as np
+def cpu_info():
+    """CPU model (/proc/cpuinfo), os.cpu_count() and the cores this process
+    may run on."""
+    import os
+
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "cpu_count": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0))}
+
+
+def _timed_pool(tasks, threads, min_s):
+    """Run the independent tasks (callables; the oracle's C kernels and torch's
+    CPU ops release the GIL) over `threads` worker threads, one pass over all of
+    them at a time: one untimed pass, then passes until min_s seconds have gone
+    by.  Each worker holds torch's intra-op parallelism at one thread (the
+    setting is per calling thread), so that `threads` is the parallelism.
+    Returns (tasks per pass, best pass in s)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import torch
+
+    nt = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        with ThreadPoolExecutor(max_workers=threads,
+                                initializer=lambda: torch.set_num_threads(1)) as ex:
+            list(ex.map(lambda f: f(), tasks))  # warm-up
+            best, t_end = float("inf"), time.perf_counter() + min_s
+            while True:
+                t0 = time.perf_counter()
+                list(ex.map(lambda f: f(), tasks))
+                t1 = time.perf_counter()
+                best = min(best, t1 - t0)
+                if t1 >= t_end:
+                    return len(tasks), best
+    finally:
+        torch.set_num_threads(nt)
+
+
+def cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg, n_seq, union, keep):
+    """The CPU oracle (oracle/: C kernels + numpy, a from-scratch port of the
+    reference's semantics) on bounded samples of the same inputs, copied from
+    the device: C4 (Quest step), C2 (indexer top-k), C3 (blockwise prefill
+    over the selected blocks), C5 (indexer + top-k + fp8 attention).  Each leg
+    runs on every core this process may use and on 4 threads (the reference's
+    bench pins 4, bench/bench_decode.py:56); independent units (sequences,
+    query rows, query blocks) go to a thread pool.  `value` is the C4 leg on
+    every core."""
+    import numpy as np
 
     import oracle
 
+    info = cpu_info()
+    oracle.lib()
+    legs = {}
+    all_t = info["affinity"]
+
+    def run(name, tasks, units_per_task, unit, note, scale=1.0):
+        out = {"unit": unit, "sample": note}
+        for label, th in (("all", all_t), ("4", min(4, all_t))):
+            n, dt = _timed_pool(tasks, th, CPU_LEG_S)
+            out[f"value_{label}_threads"] = float(f"{n * units_per_task * scale / dt:.4g}")
+            out[f"threads_{label}"] = th
+        legs[name] = out
+
+    # C4: page scores, top-k and attention per sequence
     B, Hkv, T, D, ps = cfg["B"], cfg["Hkv"], cfg["T"], cfg["D"], cfg["page"]
     seqs = []
     for b in range(n_seq):
         kb = pool_k[pt[b].long()].permute(1, 0, 2, 3).reshape(1, Hkv, T, D).cpu()
         vb = pool_v[pt[b].long()].permute(1, 0, 2, 3).reshape(1, Hkv, T, D).cpu()
         seqs.append((q[b:b + 1].cpu(), kb, vb, mins[b:b + 1].cpu(), maxs[b:b + 1].cpu()))
-    oracle.lib()
-    # passes over the same sequences until at least MIN_CPU_S of CPU work
-    passes, t0 = 0, time.perf_counter()
-    while True:
-        for qb, kb, vb, mb, xb in seqs:
+
+    def c4_task(sq):
+        qb, kb, vb, mb, xb = sq
+        def f():
             ids = oracle.quest_select(qb, mb, xb, page_size=ps, topk=cfg["topk"], offset=T - 1,
                                       gqa_union=union)
             oracle.attend_lists(qb, kb, vb, ids, unit=ps, causal=True, offset=T - 1)
-        passes += 1
-        dt = time.perf_counter() - t0
-        if dt >= MIN_CPU_S:
-            break
-    return {"value": passes * n_seq / dt, "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"{passes} passes over {n_seq} of {B} sequences of config 4 (full step: "
-                      f"page scores, top-k, attention), {dt:.1f} s, CPU oracle (C, single "
-                      f"thread)"}
+        return f
+
+    run("c4", [c4_task(x) for x in seqs], 1, "tok/s",
+        f"{n_seq} of {B} sequences of config 4 (page scores, top-k, attention), one per task")
+    del seqs
+
+    # C2: 128 query rows spread evenly over [0, T) (their causal key counts
+    # average the full workload's), 2 rows per task
+    c2 = keep.get("c2")
+    if c2:
+        Tq = c2["q"].shape[1]
+        rows = np.linspace(0, Tq - 1, 128).astype(np.int64)
+        k2 = oracle.to_f64(c2["k"])  # converted once, as the GPU's keys are resident
+
+        def c2_task(r):
+            qr, wr = oracle.to_f64(c2["q"][:, r]), oracle.to_f64(c2["w"][:, r])
+            def f():
+                for i, t in enumerate(r):
+                    oracle.indexer_topk(qr[:, i:i + 1], k2[:, :t + 1], wr[:, i:i + 1],
+                                        c2["topk"], causal=True, offset=int(t))
+            return f
+
+        run("c2", [c2_task(rows[i:i + 2]) for i in range(0, 128, 2)], 2, "queries/s",
+            "128 query rows of config 2 evenly spaced over the 8192 positions (causal scores over "
+            "their key prefix, top-2048), 2 rows per task")
+
+    # C3: 64 (b, head, query block) items spread over the batch, heads and
+    # positions; a mask-free blockwise loop in torch fp32 (gather the selected
+    # key blocks, one causal 64 x 64 triangle on the diagonal block only),
+    # checked on its first item against the fp64 oracle
+    c3 = keep.get("c3")
+    if c3:
+        import torch
+
+        bs = c3["block"]
+        Bq, Hq, nqb = c3["ids"].shape[:3]
+        D3 = c3["q"].shape[-1]
+        G = Hq // c3["k"].shape[1]
+        rng = np.random.default_rng(0)
+        items = [(int(rng.integers(Bq)), int(rng.integers(Hq)), int(x))
+                 for x in np.linspace(0, nqb - 1, 64).astype(np.int64)]
+        pairs = sum(int(c3["counts"][b, h, qb]) for b, h, qb in items)
+        kv3 = {}  # fp32 K/V heads as (blocks, 64, D), made before timing
+        tri = torch.ones(bs, bs, dtype=torch.bool).tril()
+
+        def c3_item(it):
+            b, h, qb = it
+            key = (b, h // G)
+            if key not in kv3:
+                kv3[key] = tuple(c3[n][b, h // G].float().view(-1, bs, D3) for n in "kv")
+            kb, vb = kv3[key]
+            lst = c3["ids"][b, h, qb, :c3["counts"][b, h, qb]].long()
+            lst = lst[lst <= qb]  # causal: blocks past the query block hold no visible key
+            qq = c3["q"][b, h, qb * bs:(qb + 1) * bs].float() * (1.0 / math.sqrt(D3))
+            diag = lst == qb
+            def f():
+                s_ = (qq @ kb[lst].reshape(-1, D3).T).view(bs, -1, bs)
+                s_[:, diag] = s_[:, diag].masked_fill(~tri.unsqueeze(1), float("-inf"))
+                p_ = torch.softmax(s_.reshape(bs, -1), -1)
+                return p_ @ vb[lst].reshape(-1, D3)
+            return f
+
+        tasks = [c3_item(it) for it in items]
+        b, h, qb = items[0]
+        lst = c3["ids"][b, h, qb, :c3["counts"][b, h, qb]].numpy()
+        want = oracle.attend_lists(c3["q"][b:b + 1, h:h + 1, qb * bs:(qb + 1) * bs],
+                                   c3["k"][b:b + 1, h // G:h // G + 1],
+                                   c3["v"][b:b + 1, h // G:h // G + 1],
+                                   np.broadcast_to(lst, (1, 1, bs, len(lst))), unit=bs,
+                                   causal=True, offset=qb * bs)[0, 0]
+        err = float(np.abs(tasks[0]().double().numpy() - want).max())
+        flop_per_pair = bs * bs * D3 * 2 * 2
+        run("c3", tasks, pairs / len(items), "TFLOP/s",
+            "64 (b, head, query block) items of config 3 evenly spaced over the query blocks; "
+            "mask-free blockwise loop in torch fp32 over the GPU-selected key blocks (the "
+            "selection not timed); useful FLOPs as on the GPU", scale=flop_per_pair / 1e12)
+        legs["c3"]["max_abs_err_vs_oracle_item0"] = float(f"{err:.3g}")
+
+    # C5: per sequence, indexer over all 131072 keys, top-4096, fp8 attention
+    c5 = keep.get("c5")
+    if c5:
+        T5, k5 = c5["T"], c5["topk"]
+
+        for sq in c5["seqs"]:  # indexer operands converted once, as on the GPU they are resident
+            for n in ("q_idx", "k_idx", "w"):
+                sq[n] = oracle.to_f64(sq[n])
+
+        def c5_task(sq):
+            def f():
+                _, idx = oracle.indexer_topk(sq["q_idx"], sq["k_idx"], sq["w"], k5, causal=True,
+                                             offset=T5 - 1)
+                ids = np.broadcast_to(idx.reshape(1, 1, 1, -1),
+                                      (1, sq["kc"].shape[1], 1, idx.shape[-1]))
+                oracle.attend_lists(sq["q"], sq["kc"], sq["vc"], ids, unit=1, causal=True,
+                                    offset=T5 - 1, k_scale=sq["ks"], v_scale=sq["vs"])
+            return f
+
+        run("c5", [c5_task(sq) for sq in c5["seqs"]], 1, "tok/s",
+            f"{len(c5['seqs'])} of 16 sequences of config 5 (indexer over 131072 keys, top-4096, "
+            "fp8 attention of 32 heads), one per task")
+
+    c4 = legs["c4"]
+    return {"value": c4["value_all_threads"], "unit": "tok/s", "cores": c4["threads_all"],
+            "kind": "port",
+            "sample": f"config 4 leg: {c4['sample']}; one warm-up pass, then the best pass of "
+                      f"{CPU_LEG_S:.0f}+ s of passes per leg and thread count; CPU oracle (C + "
+                      f"numpy) on {c4['threads_all']} threads",
+            "cpu": info, "legs": legs}
 
 
 FP64_VALU_PEAK_TFLOPS = 78.6  # MI355X fp64 vector, AMD public spec
-MIN_CPU_S = 10.0  # CPU work timed for the baseline
+CPU_LEG_S = 3.0  # CPU work timed per baseline leg and thread count
+C5_CPU_SEQ = 16  # C5 sequences copied to the host for its CPU leg (all of them)
 
 
 def time_cuda(fn, steps, warmup):
@@ -131,8 +297,9 @@ def time_cuda(fn, steps, warmup):
     return s.elapsed_time(e) / steps
 
 
-def bench_c2(dev, steps, warmup):
-    """Config 2: fused indexer + causal top-2048, bf16, B=1, T=8192, 4x64 heads."""
+def bench_c2(dev, steps, warmup, keep=None):
+    """Config 2: fused indexer + causal top-2048, bf16, B=1, T=8192, 4x64 heads.
+    ``keep`` (a dict) receives host copies of the inputs for the CPU leg."""
     import torch
 
     from linattn_amd.kernels.fused_indexer import indexer_topk
@@ -143,6 +310,8 @@ def bench_c2(dev, steps, warmup):
     k = torch.randn(1, T, HI, d, generator=g, device=dev).bfloat16()
     w = torch.rand(1, T, HI, generator=g, device=dev)
     ms = time_cuda(lambda: indexer_topk(q, k, w, kk, causal=True), steps, warmup)
+    if keep is not None:
+        keep["c2"] = {"q": q.cpu(), "k": k.cpu(), "w": w.cpu(), "topk": kk}
     pairs = T * (T + 1) // 2
     flops = pairs * HI * d * 2  # exact fp64 q.k products
     tflops = flops / (ms * 1e-3) / 1e12
@@ -155,7 +324,7 @@ def bench_c2(dev, steps, warmup):
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, AMD public spec
 
 
-def bench_c3(dev, steps, warmup):
+def bench_c3(dev, steps, warmup, keep=None):
     """Config 3: block-sparse causal prefill, bf16, B=2, T=32768, 32/8 heads,
     D=128, 64x64 blocks, sink + 4-block window + top-16 by pooled scores."""
     import torch
@@ -179,6 +348,9 @@ def bench_c3(dev, steps, warmup):
     pairs = int(counts.sum())
     flops = pairs * bs * bs * D * 2 * 2  # QK^T and PV, diagonal blocks counted whole
     tflops = flops / (ms * 1e-3) / 1e12
+    if keep is not None:
+        keep["c3"] = {"q": q.cpu(), "k": k.cpu(), "v": v.cpu(), "ids": ids.cpu(),
+                      "counts": counts.cpu(), "block": bs}
     # the same lists over an fp8 e4m3 cache (per-token scales, kv/quant.py:76-109)
     from linattn_amd.kernels.paged_decode import quantize_fp8_per_token
     kc, ks = quantize_fp8_per_token(k.float())
@@ -197,7 +369,7 @@ def bench_c3(dev, steps, warmup):
                     "(K codes scored by fp16 MFMA, per-key scales, V dequantized)"}
 
 
-def bench_c5(dev, steps, warmup):
+def bench_c5(dev, steps, warmup, keep=None):
     """Config 5: fp8 e4m3 KV (per-token fp32 scales) sparse decode, batch 16,
     context 131072 in 64-token pages, 32/8 heads, D=128; the indexer (4 x 64,
     bf16) picks 4096 tokens per sequence."""
@@ -229,6 +401,18 @@ def bench_c5(dev, steps, warmup):
                                    page_size=ps, k_scale=ks, v_scale=vs)
 
     ms = time_cuda(step, steps, warmup)
+    if keep is not None:  # host copies of the first C5_CPU_SEQ sequences (contiguous K/V)
+        seqs = []
+        for b in range(C5_CPU_SEQ):
+            rows = pt[b].long()
+            seqs.append({
+                "q": q[b:b + 1].cpu(), "q_idx": q_idx[b:b + 1].cpu(), "k_idx": k_idx[b:b + 1].cpu(),
+                "w": w[b:b + 1].cpu(),
+                "kc": kc[rows].permute(1, 0, 2, 3).reshape(1, Hkv, T, D).cpu(),
+                "vc": vc[rows].permute(1, 0, 2, 3).reshape(1, Hkv, T, D).cpu(),
+                "ks": ks[rows].permute(1, 0, 2).reshape(1, Hkv, T).cpu(),
+                "vs": vs[rows].permute(1, 0, 2).reshape(1, Hkv, T).cpu()})
+        keep["c5"] = {"seqs": seqs, "topk": topk, "T": T}
     bytes_step = (B * T * HI * d * 2            # indexer keys
                   + B * Hkv * topk * D * 2       # fp8 K and V of the kept tokens
                   + B * Hkv * topk * 2 * 4       # their scales
@@ -541,16 +725,24 @@ def main() -> int:
     }
     # side configurations: a few untimed calls first (clocks settle)
     sub, sub_w = max(3, args.steps // 4), 10
+    keep = None if args.no_cpu_baseline else {}
     result["page_bounds"] = bench_page_bounds(dev, pool_k, pt, mins, maxs, cfg, sub, sub_w)
-    result["indexer"] = bench_c2(dev, sub, sub_w)
-    result["prefill"] = bench_c3(dev, sub, sub_w)
-    result["fp8_decode"] = bench_c5(dev, sub, sub_w)
+    result["indexer"] = bench_c2(dev, sub, sub_w, keep)
+    result["prefill"] = bench_c3(dev, sub, sub_w, keep)
+    result["fp8_decode"] = bench_c5(dev, sub, sub_w, keep)
     result["moba_decode"] = bench_moba(dev, sub, sub_w)
     result["xattn_select"] = bench_xattn(dev, max(3, args.steps // 10), 3)
     result["serving"] = bench_serving(dev, q, pool_k, pool_v, pt, mins, maxs, cfg, sub, sub_w)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg,
-                                              args.cpu_sample, union)
+        cb = cpu_baseline(q, pool_k, pool_v, pt, mins, maxs, cfg, args.cpu_sample, union, keep)
+        # achieved GB/s of the decode legs, at the GPU step's algorithmic bytes per token
+        for leg, per_tok in (("c4", step_bytes / B),
+                             ("c5", result["fp8_decode"]["bytes_per_step"] / 16)):
+            if leg in cb["legs"]:
+                for lab in ("all", "4"):
+                    v = cb["legs"][leg][f"value_{lab}_threads"]
+                    cb["legs"][leg][f"GBps_{lab}_threads"] = round(v * per_tok / 1e9, 3)
+        result["cpu_baseline"] = cb
     print(json.dumps(result))
     return 0
 
