@@ -255,6 +255,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // K slots 0..1, V slots 2..3 (64 KiB: two workgroups per CU); after the
   // loop, the key-half merge area
   __shared__ __align__(16) uint16_t smem[4 * PF_BLK];
+  // KF16: the per-key scales of the K block in each K slot (copied with it)
+  __shared__ __align__(16) float sscale[KF16 ? 2 * PF_BS : 4];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
@@ -409,16 +411,27 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   auto TG = [&](int qg) {
     if constexpr (KF16) return tg[qg]; else return p.thr_gap;
   };
-  // KF16: the scales of this lane's 8 keys (16 kt2 + 4 g + e of its key half)
-  // of the block scored in the current step (skc) and of the next one (skn)
-  f32x4 skc[2] = {}, skn[2] = {};
-  auto load_ks = [&](int kb, f32x4 (&dst)[2]) {
-    const uint32_t kbc = (uint32_t)kb < (uint32_t)nkb32 ? (uint32_t)kb : 0u;
-    const float *sp = p.kscale + ((b * p.Hkv + kvh) * p.nkb + kbc) * PF_BS + 32 * kh + 4 * g;
-#pragma unroll
-    for (int kt2 = 0; kt2 < 2; ++kt2) dst[kt2] = *(const f32x4 *)(sp + 16 * kt2);
+  // KF16: the 64 scales of K block kb go to LDS with its codes (wave 0: one
+  // 4-byte LDS-DMA load per lane, counted and waited for like the block
+  // copies; an empty or out-of-range entry copies block 0's, never used)
+  auto dma_ks = [&](int kb, int slot) {
+    if constexpr (KF16) {
+      if (wu == 0) {
+        const uint32_t kbc = (uint32_t)kb < (uint32_t)nkb32 ? (uint32_t)kb : 0u;
+        const float *sp = p.kscale + ((b * p.Hkv + kvh) * p.nkb + kbc) * PF_BS + lane;
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+            (uint32_t)(uintptr_t)(lds_void_t *)(sscale + slot * PF_BS));
+        asm volatile("global_load_lds_dword %0, off" ::"v"(sp), "{m0}"(m0) : "memory");
+      }
+    }
   };
-  auto scale_scores = [&](f32x4 (&sc)[2][2], const f32x4 (&sk)[2]) {
+  // the scores of this lane's 8 keys (16 kt2 + 4 g + e of its key half) of
+  // the K block in `slot`, times their scales
+  auto scale_scores = [&](f32x4 (&sc)[2][2], int slot) {
+    const float *sp = sscale + slot * PF_BS + 32 * kh + 4 * g;
+    f32x4 sk[2];
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2) sk[kt2] = *(const f32x4 *)(sp + 16 * kt2);
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg)
 #pragma unroll
@@ -510,11 +523,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) qreg[qg][s] = __builtin_nontemporal_load((const bf16x8 *)(qp + 32 * s + 8 * g));
   }
-  f32x4 sk0[2] = {};
-  if constexpr (KF16) {
-    load_ks(kbj, sk0);
-    load_ks(kb1, skc);
-  }
+  dma_ks(kbj, 0);
+  if (n > 1) dma_ks(kb1, 1);
   wait_vmcnt<0>();
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg)
@@ -563,7 +573,7 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // scores of blocks with even / odd list position
   f32x4 sA[2][2], sB[2][2];
   scores(0, sA);
-  if constexpr (KF16) scale_scores(sA, sk0);
+  if constexpr (KF16) scale_scores(sA, 0);
   if (needs_mask(kbj)) apply_mask(kbj, sA);
   {
     float mx[2], alpha[2];
@@ -589,8 +599,10 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     const uint32_t kbe = (uint32_t)kbj < (uint32_t)nkb32 ? (uint32_t)kbj : 0u;
     sload2_i32(list + (FULL ? j + 2 : min(j + 2, n - 1)), vexp + kbe, kb2, ev);
     if (!FULL && j + 2 >= n) kb2 = 0;
-    if constexpr (KF16) load_ks(kb2, skn);  // scored in the next step; landed by its end
-    if (FULL || j + 2 < n) dma_k(kb2, par);            // held block j (scored a step ago)
+    if (FULL || j + 2 < n) {  // the slot held block j (scored a step ago)
+      dma_k(kb2, par);
+      dma_ks(kb2, par);
+    }
     if (FULL || j + 1 < n) dma_v(kb1, 2 + (par ^ 1));  // held block j-1 (multiplied)
     const uint16_t *sk = smem + (par ^ 1) * PF_BLK;
     const uint16_t *sv = smem + (2 + par) * PF_BLK;
@@ -622,7 +634,6 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       sn[0][kt2] = s0;
       sn[1][kt2] = s1;
     }
-    if constexpr (KF16) scale_scores(sn, skc);
     // P = 2^ev * exp2(s*qscale - m*qscale) in fp16 (round to nearest even; at
     // most 2^(8+ev) <= 2^15); l sums the rounded weights times 2^-ev (exact).
     // Column c16 is this lane's query; the positive scale commutes with the
@@ -657,6 +668,10 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg)
         acc[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], ph[qg], acc[qg][dt], 0, 0, 0);
+    // KF16: the key scales of block j+1, applied with its maxima (its scores
+    // are ready by then; applied right after the score products, the
+    // multiplies would wait for the matrix core)
+    if constexpr (KF16) scale_scores(sn, par ^ 1);
     float mx[2];
     lane_max(sn, mx);
     // order within the block: the 24 LDS reads, then the 16 score MFMAs each
@@ -680,10 +695,6 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       }
       float alpha[2];
       if (settle_max(mx, alpha)) rescale_acc(alpha);
-    }
-    if constexpr (KF16) {
-      skc[0] = skn[0];
-      skc[1] = skn[1];
     }
     // this wave's loads have landed and every wave is done with the slots
     // that the next step refills
