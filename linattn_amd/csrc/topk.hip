@@ -20,6 +20,12 @@
 namespace la {
 
 constexpr int TK_BATCH = 8;  // keys read per thread before they are used
+// bucket ranking of the sorted form: TKB_N key buckets (+ forced and tie
+// buckets), scanned TKB_PT per thread; TKB_MAX survivors per bucket at most
+constexpr int TKB_BITS = 11, TKB_N = 1 << TKB_BITS, TKB_PT = 9, TKB_S = TKB_PT * 256;
+constexpr int TKB_MAX = 256;
+// undecided keys the bitwise search copies to LDS once that few remain
+constexpr int TK_CAND_CAP = 512;
 
 struct TkShared {
   uint32_t hist[256];
@@ -402,12 +408,18 @@ __device__ __forceinline__ void tk_bitonic_desc(uint64_t (&c)[E], int tid, uint6
 // (key desc, index asc) with a bitonic network over E registers per thread:
 // partners in the same thread are swapped in place, in other lanes of the
 // wave they are exchanged by shuffles, in other waves through LDS.
+// Sorted rows of the longest kind (KPT 32: the indexer's) are held to three
+// waves per SIMD (168 registers, two of them spilled): their steps are short
+// and barrier-bound, so a third resident workgroup per CU pays.
 template <int KPT, int E, bool BITMAP>
-__global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
+__global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 3 : 1) void topk_reg_kernel(TopkKParams p) {
   constexpr int P = TK_NT * E;  // sort width (sorted form)
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ TkRegShared<KPT> sr;
   __shared__ uint32_t s_fill, s_first_pad;
+  __shared__ uint32_t s_bins[BITMAP ? 1 : TKB_S + 1];  // sorted form: bucket counts / starts
+  __shared__ uint64_t s_red2[TK_NW], s_red3[TK_NW];
+  __shared__ uint32_t s_tie[BITMAP ? 1 : 2 * 256];  // sorted form: tie-bucket index bits, prefixes
 
   const int tid = threadIdx.x, lane = tid & 63;
   const uint64_t lt = lanemask_lt(lane);
@@ -456,30 +468,223 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
         if (take) atomicOr(&bm[i >> 5], 1u << (i & 31));
       });
     } else {
-      tk_reg_select_bits<KPT>(u, n_v, K, sr, [&](int j, int32_t i, bool take) {
+      static_assert(KPT <= 32, "take flags in one word");
+      uint32_t takem = 0;  // bit j: slot j selected
+      tk_reg_select_bits<KPT>(
+          u, n_v, K, sr, [&](int j, int32_t, bool take) { takem |= take ? (1u << j) : 0u; },
+          skey, (uint32_t)min(P, TK_CAND_CAP));
+      // the selected keys to skey / sidx[0, K): one place reservation per wave
+      uint32_t wcnt = 0;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) wcnt += (uint32_t)__popcll(__ballot((takem >> j) & 1u));
+      uint32_t base = 0;
+      if (lane == 0 && wcnt) base = atomicAdd(&s_fill, wcnt);
+      base = __shfl(base, 0, 64);
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const bool take = (takem >> j) & 1u;
         const uint64_t tm = __ballot(take);
-        uint32_t base = 0;
-        if (lane == 0 && tm) base = atomicAdd(&s_fill, (uint32_t)__popcll(tm));
-        base = __shfl(base, 0, 64);
         if (take) {
-          const uint32_t pos = base + (uint32_t)__popcll(tm & lt);
-          skey[pos] = u[j];
-          sidx[pos] = i;
+          const uint32_t q = base + (uint32_t)__popcll(tm & lt);
+          skey[q] = u[j];
+          sidx[q] = tid + TK_NT * j;
         }
-      });
+        base += (uint32_t)__popcll(tm);
+      }
+      __syncthreads();
     }
   }
   if constexpr (BITMAP) {
     tk_emit_bitmap(p, bm, rw, sr.wtmp[1]);
   } else {
-    // sorted form (one row per workgroup).  The K survivors are first sorted
-    // as single 64-bit composites: the key with its low 13 bits replaced by
-    // 8191 - index (rows hold at most 8192 units), so one unsigned compare
-    // orders them by (key desc, index asc) unless two keys differ only in
-    // their low 13 bits.  The result is then checked with the full keys
-    // (re-read from the row) and, if any neighbouring pair is out of order,
-    // sorted again on (key, index).
+    static_assert(BITMAP || KPT <= 32, "sorted form: row indices below 8192 (tie bits)");
+    // Sorted form (one row per workgroup): the K selected keys (skey / sidx,
+    // in any order) are ranked by (key desc, index asc).  A counting pass
+    // spreads them over buckets of their key range -- bucket 0 for a forced
+    // key, then TKB_N buckets of equal key width from the largest other key
+    // down to the smallest key above the minimum, and a last bucket for the
+    // keys equal to the minimum (ties such as zero scores) -- and copies them
+    // back in bucket order; each then counts the keys of its own bucket that
+    // precede it, and the ranked (index, value) pairs leave through LDS in
+    // order.  Order keys grow with the score's exponent as well as its
+    // mantissa, so scores spread over many binades still fill many buckets.
+    // When the range holds both signs, the buckets are laid over a signed
+    // magnitude image instead (exponent and mantissa bits, clamped 24 binades
+    // below the largest magnitude), so that the 2000 binades of tiny
+    // magnitudes around zero take no buckets.  A row whose largest bucket
+    // still holds more than TKB_MAX keys takes the bitonic sort below.
     const int32_t K = (int32_t)rw.K;
+    const int w = tid >> 6;
+    const int32_t *cand = p.cand_idx ? p.cand_idx + ((rw.br / p.Tq) * p.G * p.Tq + rw.tl) * p.row_stride + rw.seg0 : nullptr;
+    int32_t *oi = p.out_idx + rw.orow * p.width;
+    if (tid == 0) s_first_pad = (uint32_t)K;
+    // magnitude bits (exponent, mantissa) of the score behind an order key
+    constexpr uint64_t MAG = 0x7fffffffffffffffull;
+    auto mag = [](uint64_t k) -> uint64_t { return (k >> 63) ? (k & MAG) : (~k & MAG); };
+    uint64_t bkey[E];
+    int32_t bidx[E];
+    uint64_t mx = 0, mn = ~0ull;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = tid + TK_NT * e;
+      bkey[e] = i < K ? skey[i] : 0ull;
+      bidx[e] = i < K ? sidx[i] : -1;
+      if (bidx[e] >= 0) {
+        if (bkey[e] != KEY_FORCED) mx = max(mx, bkey[e]);
+        mn = min(mn, bkey[e]);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      mx = max(mx, (uint64_t)__shfl_xor(mx, off, 64));
+      mn = min(mn, (uint64_t)__shfl_xor(mn, off, 64));
+    }
+    if (lane == 0) {
+      sr.red[0][w] = mx;
+      sr.red[1][w] = mn;
+    }
+    for (int b = tid; b <= TKB_S; b += TK_NT) s_bins[b] = 0u;
+    s_tie[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int x = 0; x < TK_NW; ++x) {
+      mx = max(mx, sr.red[0][x]);
+      mn = min(mn, sr.red[1][x]);
+    }
+    // over the keys above the minimum (other than a forced key): the smallest
+    // one and the largest magnitude
+    uint64_t mn2 = ~0ull, emax = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (bidx[e] >= 0 && bkey[e] > mn && bkey[e] != KEY_FORCED) {
+        mn2 = min(mn2, bkey[e]);
+        emax = max(emax, mag(bkey[e]));
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      mn2 = min(mn2, (uint64_t)__shfl_xor(mn2, off, 64));
+      emax = max(emax, (uint64_t)__shfl_xor(emax, off, 64));
+    }
+    if (lane == 0) {
+      s_red2[w] = mn2;
+      s_red3[w] = emax;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int x = 0; x < TK_NW; ++x) {
+      mn2 = min(mn2, s_red2[x]);
+      emax = max(emax, s_red3[x]);
+    }
+    // the bucket image: the key itself, or over a range of both signs the
+    // signed magnitude above a floor 24 binades below the largest
+    const bool mixed = mn2 <= mx && ((mn2 ^ mx) >> 63) != 0;
+    const uint64_t floor_m = (emax >> 52) >= 24 ? ((emax >> 52) - 24) << 52 : 0ull;
+    auto img = [&](uint64_t k) -> uint64_t {
+      if (!mixed) return k;
+      const uint64_t dm = max(mag(k), floor_m) - floor_m;
+      return (k >> 63) ? (0x8000000000000000ull + dm) : (0x8000000000000000ull - dm);
+    };
+    const uint64_t tmx = img(mx);
+    const uint64_t range = mn2 <= mx ? tmx - img(mn2) : 0ull;
+    const int nbits = range ? 64 - __clzll((long long)range) : 0;
+    const int shift = nbits > TKB_BITS ? nbits - TKB_BITS : 0;
+    uint32_t bk[E], slot[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (bidx[e] >= 0) {
+        const uint64_t k = bkey[e];
+        bk[e] = k == KEY_FORCED ? 0u : k == mn ? (uint32_t)TKB_N + 1u : 1u + (uint32_t)((tmx - img(k)) >> shift);
+        slot[e] = atomicAdd(&s_bins[bk[e]], 1u);
+        if (bk[e] == (uint32_t)TKB_N + 1u) atomicOr(&s_tie[bidx[e] >> 5], 1u << (bidx[e] & 31));
+      }
+    }
+    __syncthreads();
+    // keys tied at the minimum rank by index: prefix counts of the tie bits
+    {
+      const uint32_t wbits = s_tie[tid];
+      uint32_t tot_t;
+      const uint32_t pc = (uint32_t)__popc(wbits);
+      s_tie[256 + tid] = tk_block_incl_scan(pc, sr.wtmp[0], tot_t) - pc;
+    }
+    // bucket starts (exclusive scan, TKB_PT bins per thread) and the largest bucket
+    uint32_t c9[TKB_PT], loc = 0, big = 0;
+#pragma unroll
+    for (int i = 0; i < TKB_PT; ++i) {
+      c9[i] = s_bins[TKB_PT * tid + i];
+      loc += c9[i];
+      if (TKB_PT * tid + i != TKB_N + 1) big = max(big, c9[i]);  // (the tie bucket: by index)
+    }
+    uint32_t tot_b;
+    uint32_t run = tk_block_incl_scan(loc, sr.wtmp[0], tot_b) - loc;
+#pragma unroll
+    for (int i = 0; i < TKB_PT; ++i) {
+      s_bins[TKB_PT * tid + i] = run;
+      run += c9[i];
+    }
+    if (tid == 0) s_bins[TKB_S] = (uint32_t)K;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) big = max(big, (uint32_t)__shfl_xor(big, off, 64));
+    if (lane == 0) sr.wtmp[1][w] = big;
+    __syncthreads();
+#pragma unroll
+    for (int x = 0; x < TK_NW; ++x) big = max(big, sr.wtmp[1][x]);
+    if (big <= (uint32_t)TKB_MAX) {
+      // bucket order in skey / sidx, then the rank within the bucket
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if (bidx[e] >= 0) {
+          const uint32_t j = s_bins[bk[e]] + slot[e];
+          skey[j] = bkey[e];
+          sidx[j] = bidx[e];
+        }
+      }
+      __syncthreads();
+      uint32_t pos[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if (bidx[e] < 0) continue;
+        const uint32_t b0 = s_bins[bk[e]], b1 = s_bins[bk[e] + 1];
+        uint32_t r = 0;
+        if (bk[e] == (uint32_t)TKB_N + 1u) {
+          const int32_t ix = bidx[e];
+          r = s_tie[256 + (ix >> 5)] + (uint32_t)__popc(s_tie[ix >> 5] & ((1u << (ix & 31)) - 1u));
+        } else {
+          for (uint32_t j = b0; j < b1; ++j) r += tk_precedes(skey[j], sidx[j], bkey[e], bidx[e]) ? 1u : 0u;
+        }
+        pos[e] = b0 + r;
+      }
+      __syncthreads();  // every bucket is read before the ranked pairs overwrite it
+      // (output index, value bits) at each rank in skey, then written out in order
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if (bidx[e] < 0) continue;
+        const int32_t s0 = bidx[e];
+        const int32_t id = cand ? cand[s0] : s0;
+        const bool pad = cand && id < 0;
+        if (pad) atomicMin(&s_first_pad, pos[e]);
+        const float v = pad ? __int_as_float(0xff800000)
+                            : (rw.force && s0 == own) ? __int_as_float(0x7f800000)
+                                                       : (float)key_to_double(bkey[e]);
+        skey[pos[e]] = (uint64_t)(uint32_t)id | ((uint64_t)__float_as_uint(v) << 32);
+      }
+      __syncthreads();
+      const int64_t kw = min((int64_t)K, p.width);
+      for (int64_t jj = tid; jj < p.width; jj += TK_NT) {
+        const uint64_t x = jj < kw ? skey[jj] : 0xff800000ffffffffull;  // -1, -inf past K
+        oi[jj] = (int32_t)(uint32_t)x;
+        if (p.out_val) p.out_val[rw.orow * p.width + jj] = __uint_as_float((uint32_t)(x >> 32));
+      }
+      __syncthreads();
+      if (p.out_count && tid == 0) p.out_count[rw.orow] = (int32_t)s_first_pad;
+      return;
+    }
+    // Bitonic fallback.  The K survivors are first sorted as single 64-bit
+    // composites: the key with its low 13 bits replaced by 8191 - index (rows
+    // hold at most 8192 units), so one unsigned compare orders them by (key
+    // desc, index asc) unless two keys differ only in their low 13 bits.  The
+    // result is then checked with the full keys (re-read from the row) and,
+    // if any neighbouring pair is out of order, sorted again on (key, index).
     for (int32_t i = K + tid; i < P; i += TK_NT) {
       skey[i] = 0;
       sidx[i] = -1;
@@ -572,8 +777,6 @@ __global__ __launch_bounds__(TK_NT) void topk_reg_kernel(TopkKParams p) {
         }
       }
     }
-    const int32_t *cand = p.cand_idx ? p.cand_idx + ((rw.br / p.Tq) * p.G * p.Tq + rw.tl) * p.row_stride + rw.seg0 : nullptr;
-    int32_t *oi = p.out_idx + rw.orow * p.width;
     int32_t id[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) id[e] = (cand && idx[e] >= 0) ? cand[idx[e]] : idx[e];

@@ -8,6 +8,7 @@
 namespace la {
 
 constexpr int TK_NT = 256;  // threads of a selecting workgroup
+constexpr int TK_CAND_REGS = 8;  // keys per lane of the one-wave finish
 constexpr int TK_NW = TK_NT / 64;
 
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) {
@@ -43,6 +44,7 @@ struct TkRegShared {
   uint64_t red[2][TK_NW];
   uint32_t wtmp[2][TK_NW];
   uint32_t bin, above, cnt;
+  uint32_t cfill;  // candidates copied by tk_reg_select_bits
 };
 
 // Top K of the keys u[j] of units t + 256*j (t = thread), j < KPT, among the
@@ -170,9 +172,14 @@ __device__ __forceinline__ void tk_reg_select(const uint64_t (&u)[KPT], int32_t 
 // It stops when exactly K do; else T is the K-th largest key and its ties
 // are taken lowest index first.  emit(j, i, take) as in tk_reg_select.
 // The keys of units past n_v are set to 0 in u (no candidate reaches 0).
+// With `cand` (LDS for `cap` <= 64 * TK_CAND_REGS keys, not otherwise used
+// until emit), once at most `cap` keys lie between T and the lowest key known
+// to be selected whole (the undecided window), they are copied there and one
+// wave finishes the search over them in registers, with no barrier per bit.
 template <int KPT, class Emit>
 __device__ __forceinline__ void tk_reg_select_bits(uint64_t (&u)[KPT], int32_t n_v, uint32_t K,
-                                                   TkRegShared<KPT> &sh, Emit emit) {
+                                                   TkRegShared<KPT> &sh, Emit emit,
+                                                   uint64_t *cand = nullptr, uint32_t cap = 0) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   uint32_t *cnt = sh.wtmp[0];  // [2][TK_NW] counts, alternating steps
 #pragma unroll
@@ -214,7 +221,69 @@ __device__ __forceinline__ void tk_reg_select_bits(uint64_t (&u)[KPT], int32_t n
   uint64_t T = top >= 0 ? a & ~((2ull << top) - 1ull) : a;  // 2ull << 63 wraps to 0
   bool exact = false;
   int step = 0;
-  for (int bit = top; bit >= 0; --bit, ++step) {
+  // keys >= U (when has_u) are selected whole: `above` of them; `tot_t`
+  // keys are >= T, so tot_t - above lie in the undecided window [T, U)
+  uint64_t U = 0;
+  bool has_u = false;
+  uint32_t above = 0, tot_t = (uint32_t)n_v;
+  int bit = top;
+  for (; bit >= 0; --bit, ++step) {
+    if (cand && tot_t - above <= cap && step > 0) {
+      // copy the window's keys (workgroup-uniform decision) ...
+      uint32_t *fill = &sh.cfill;
+      if (tid == 0) fill[0] = 0;
+      __syncthreads();
+      const uint64_t lt = lanemask_lt(lane);
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const bool inw = u[j] >= T && (!has_u || u[j] < U) && tid + TK_NT * j < n_v;
+        const uint64_t m = __ballot(inw);
+        if (m) {
+          uint32_t base = 0;
+          if (lane == 0) base = atomicAdd(fill, (uint32_t)__popcll(m));
+          base = __shfl(base, 0, 64);
+          if (inw) cand[base + (uint32_t)__popcll(m & lt)] = u[j];
+        }
+      }
+      const uint32_t n_c = tot_t - above;
+      __syncthreads();
+      // ... and let one wave finish the search over them in registers,
+      // without barriers
+      if (w == 0) {
+        uint64_t cr[TK_CAND_REGS];
+#pragma unroll
+        for (int m = 0; m < TK_CAND_REGS; ++m) {
+          const uint32_t i = lane + 64 * m;
+          cr[m] = i < n_c ? cand[i] : 0ull;  // 0 never reaches a candidate threshold
+        }
+        for (; bit >= 0; --bit) {
+          const uint64_t T2 = T | (1ull << bit);
+          uint32_t c = above;
+#pragma unroll
+          for (int m = 0; m < TK_CAND_REGS; ++m)
+            c += (uint32_t)__popcll(__ballot(cr[m] >= T2 && (!has_u || cr[m] < U)));
+          if (c >= K) {
+            T = T2;
+            if (c == K) {
+              exact = true;
+              break;
+            }
+          } else {
+            U = T2;
+            has_u = true;
+            above = c;
+          }
+        }
+        if (lane == 0) {
+          sh.red[0][0] = T;
+          sh.cfill = exact ? 1u : 0u;
+        }
+      }
+      __syncthreads();
+      T = sh.red[0][0];
+      exact = sh.cfill != 0;
+      break;
+    }
     const uint64_t T2 = T | (1ull << bit);
     uint32_t c = 0;
 #pragma unroll
@@ -227,10 +296,15 @@ __device__ __forceinline__ void tk_reg_select_bits(uint64_t (&u)[KPT], int32_t n
     for (int x = 0; x < TK_NW; ++x) tot += slot[x];
     if (tot >= K) {
       T = T2;
+      tot_t = tot;
       if (tot == K) {
         exact = true;
         break;
       }
+    } else {
+      U = T2;
+      has_u = true;
+      above = tot;
     }
   }
   if (exact) {

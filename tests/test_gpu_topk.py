@@ -134,6 +134,55 @@ def test_topk_sorted_keys_differing_in_low_bits(dev):
     assert np.array_equal(vals[0, 0].cpu().numpy(), rv.astype(np.float32))
 
 
+def _spread_rows(n, seed):
+    """Rows for the sorted form's bucket ranking: ReLU sums with exact zeros
+    (ties at the minimum), both signs, far outliers, scores over many
+    binades and few distinct values."""
+    g = torch.Generator().manual_seed(seed)
+    relu = (torch.randn(n, 4, generator=g, dtype=torch.float64).clamp(min=0)
+            * torch.rand(4, generator=g, dtype=torch.float64)).sum(1)
+    rows = [relu, relu.clone(), torch.randn(n, generator=g, dtype=torch.float64) * 3.0,
+            torch.randn(n, generator=g, dtype=torch.float64),
+            torch.exp(torch.randn(n, generator=g, dtype=torch.float64) * 20.0),
+            torch.randint(0, 5, (n,), generator=g).double() * 0.5]
+    rows[3][17], rows[3][n // 2] = 1e300, -1e300
+    return torch.stack(rows).view(1, 1, len(rows), n)
+
+
+@pytest.mark.parametrize("n,k", [(8192, 2048), (5000, 4096), (3000, 512)])
+def test_topk_sorted_bucket_rank_rows(dev, n, k):
+    """Sorted selections whose survivors stress the bucket ranking: ties at
+    the minimum, mixed signs, far outliers (the bitonic fallback), many
+    binades; prefixes shorter and longer than k."""
+    sc = _spread_rows(n, n + k)
+    Tq = sc.shape[2]
+    nv = torch.tensor([n, k + 60, n, n, n, n - 1], dtype=torch.int32)[:Tq]
+    ids, counts, vals = _topk(sc.to(dev), k=k, width=k, group=1, order=0, pos_offset=0,
+                              pos_unit=0, force_own=False, with_values=True,
+                              n_valid=nv.to(dev))
+    ri, rv = oracle.topk_rows(sc[0, 0].numpy(), k, n_valid=nv.numpy())
+    assert np.array_equal(ids[0, 0].cpu().numpy(), ri)
+    assert np.array_equal(vals[0, 0].cpu().numpy(), rv.astype(np.float32))
+    assert np.array_equal(counts[0, 0].cpu().numpy(), np.minimum(k, nv.numpy()))
+
+
+def test_topk_sorted_forced_own(dev):
+    """A forced own unit ranks first (value +inf) above every bucket."""
+    n, k = 6000, 1024
+    sc = _spread_rows(n, 3)
+    Tq = sc.shape[2]
+    pos_offset = n - Tq - 500  # rows see n - Tq - 499 + t keys; own = the last visible
+    ids, counts, vals = _topk(sc.to(dev), k=k, width=k, group=1, order=0,
+                              pos_offset=pos_offset, pos_unit=1, force_own=True,
+                              with_values=True)
+    t = np.arange(Tq)
+    nv = np.minimum(n, pos_offset + t + 1)
+    ri, rv = oracle.topk_rows(sc[0, 0].numpy(), k, n_valid=nv, own=nv - 1, force_own=True)
+    assert np.array_equal(ids[0, 0].cpu().numpy(), ri)
+    assert (ids[0, 0, :, 0].cpu().numpy() == nv - 1).all()
+    assert np.array_equal(vals[0, 0, :, 1:].cpu().numpy(), rv[:, 1:].astype(np.float32))
+
+
 @pytest.mark.parametrize("n,group", [(60, 1), (500, 2), (1024, 4), (3000, 2)])
 def test_topk_union_sink_window(dev, n, group):
     """Bitmap form (one wave per row for short rows, register form for long):
