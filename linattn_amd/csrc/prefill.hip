@@ -510,9 +510,15 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // j+1 while the weights of block j are formed, then block j's PV product
   // while the maxima of block j+1 are taken.  K block x lives in slot x % 2
   // and V block x in slot 2 + x % 2; both are fetched one step ahead (K of
-  // block j+2 and V of block j+1 during step j).  List entries and V block
-  // exponents come through the scalar cache (see sload_i32).
+  // block j+2 and V of block j+1 during step j).  bf16 K/V: lists of up to
+  // 64 entries sit in VGPR lanes (entry i in lane i, with the exponent of its
+  // V block) and are read per step by v_readlane; longer lists, and every
+  // list of the fp8 form (which has no registers to spare), come through the
+  // scalar cache (see sload_i32).
   if (n <= 1) kb1 = 0;
+  const bool lanes = !KF16 && n <= 64;
+  int lv = 0, evv = 0;
+  if (lanes) lv = list[min(lane, n - 1)];
   dma_k(kbj, 0);
   dma_v(kbj, 2);
   if (n > 1) dma_k(kb1, 1);
@@ -530,6 +536,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   for (int qg = 0; qg < 2; ++qg)
 #pragma unroll
     for (int s = 0; s < 4; ++s) settle(qreg[qg][s]);  // q landed with the first blocks
+  settle(lv);
+  if (lanes) evv = vexp[(uint32_t)lv < (uint32_t)nkb32 ? (uint32_t)lv : 0u];
   if constexpr (KF16) {
     // q row -> fp16 * 2^-eq (the row's 128 values are spread over the 4
     // lanes c16 + 16 g: their largest |q| is taken across those lanes)
@@ -596,8 +604,13 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     // list entry j+2 and the exponent of V block j (V block j holds v * 2^-ev;
     // an empty or out-of-range entry reads exponent 0 from block 0)
     int kb2, ev;
-    const uint32_t kbe = (uint32_t)kbj < (uint32_t)nkb32 ? (uint32_t)kbj : 0u;
-    sload2_i32(list + (FULL ? j + 2 : min(j + 2, n - 1)), vexp + kbe, kb2, ev);
+    if (lanes) {
+      kb2 = __builtin_amdgcn_readlane(lv, FULL ? j + 2 : min(j + 2, n - 1));
+      ev = __builtin_amdgcn_readlane(evv, j);
+    } else {
+      const uint32_t kbe = (uint32_t)kbj < (uint32_t)nkb32 ? (uint32_t)kbj : 0u;
+      sload2_i32(list + (FULL ? j + 2 : min(j + 2, n - 1)), vexp + kbe, kb2, ev);
+    }
     if (!FULL && j + 2 >= n) kb2 = 0;
     if (FULL || j + 2 < n) {  // the slot held block j (scored a step ago)
       dma_k(kb2, par);
