@@ -479,37 +479,57 @@ def bench_serving(dev, q, pool_k, pool_v, pt, mins, maxs, cfg, steps, warmup):
 def bench_moba(dev, steps, warmup):
     """MoBA decode (selection.py:610-640; the same routing is NSA's selection
     branch): B=16, 32/8 heads, D=128, T=16384 bf16, 64-token blocks, top-16
-    blocks + own block per query head.  The routing pools K every step, as
-    the reference does (no cached block means)."""
+    blocks + own block per query head.  The step keeps the fp64 block means
+    of K (as hip_moba's state does): it re-pools only the block of the newest
+    key, routes on the cached means and attends.  ``ms_route_repool`` is the
+    routing that pools every key per call, as the reference does."""
     import torch
 
     from linattn_amd.kernels.block_sparse import sparse_attention
-    from linattn_amd.kernels.routing import gate_select_hip
+    from linattn_amd.kernels.routing import block_means_hip, gate_select_hip
 
     B, Hq, Hkv, T, D, bs, topk = 16, 32, 8, 16384, 128, 64, 16
     g = torch.Generator(device=dev).manual_seed(3)
     q = torch.randn(B, Hq, 1, D, generator=g, device=dev).to(torch.bfloat16)
     k = torch.randn(B, Hkv, T, D, generator=g, device=dev).to(torch.bfloat16)
     v = torch.randn(B, Hkv, T, D, generator=g, device=dev).to(torch.bfloat16)
+    kbar = block_means_hip(k, block=bs)
+    newest = torch.full((B,), T - 1, dtype=torch.int32, device=dev)
+
+    def refresh():  # the block the step's key joined
+        block_means_hip(k, block=bs, out=kbar, positions=newest)
 
     def route():
+        return gate_select_hip(q, k, block=bs, topk=topk, offset=T - 1, kbar=kbar)
+
+    def route_repool():
         return gate_select_hip(q, k, block=bs, topk=topk, offset=T - 1)
 
     ids, counts = route()
+    ids0, counts0 = route_repool()
+    same = bool(torch.equal(ids, ids0) and torch.equal(counts, counts0))
 
     def step():
+        refresh()
         i, c = route()
         sparse_attention(q, k, v, i, unit=bs, counts=c, causal=True, offset=T - 1)
 
+    ms_refresh = time_cuda(refresh, steps, warmup)
     ms_route = time_cuda(route, steps, warmup)
+    ms_repool = time_cuda(route_repool, steps, warmup)
     ms_step = time_cuda(step, steps, warmup)
     pool_bytes = B * Hkv * T * D * 2
+    mean_bytes = kbar.numel() * 8
     att_bytes = int(counts.sum()) * bs * D * 2 * 2
     return {"workload": "MoBA decode, B=16, T=16384, 32/8 heads, D=128, bf16, block 64, top-16",
-            "ms_route": round(ms_route, 4), "ms_step": round(ms_step, 4),
-            "tok_per_s": round(B / (ms_step * 1e-3), 1),
-            "route_GBps": round(pool_bytes / (ms_route * 1e-3) / 1e9, 1),
-            "attend_bytes": att_bytes}
+            "ms_step": round(ms_step, 4), "tok_per_s": round(B / (ms_step * 1e-3), 1),
+            "ms_refresh_means": round(ms_refresh, 4), "ms_route": round(ms_route, 4),
+            "route_GBps": round(mean_bytes / (ms_route * 1e-3) / 1e9, 1),
+            "ms_route_repool": round(ms_repool, 4),
+            "repool_GBps": round(pool_bytes / (ms_repool * 1e-3) / 1e9, 1),
+            "lists_equal_repool": same, "attend_bytes": att_bytes,
+            "note": "block means (fp64, 33.5 MB) kept on append; the refresh re-pools the newest "
+                    "key's block of every (b, KV head)"}
 
 
 def bench_xattn(dev, steps, warmup):

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 8
+#define LA_ABI_VERSION 9
 
 /* element types */
 enum {
@@ -412,7 +412,10 @@ int la_block_select(const la_block_select_args *a, void *stream);
  * KV head h / (Hq/Hkv).  Output: out_idx[((b*Hq + h)*Tq + t)*width + i]
  * ascending, -1 padded (width >= min(topk, blocks) + 1), out_count the number
  * kept.  Workspace: la_gate_select_workspace bytes (fp64 q, pooled keys and
- * the gate rows).
+ * the gate rows).  kbar (optional): the block means of k, (B, Hkv, n_kb, D)
+ * fp64 contiguous as la_block_means writes them; given, k is not read and
+ * not pooled (the per-step pooling of selection.py:620-624 is replaced by
+ * means kept up to date on append).
  */
 typedef struct {
   const void *q;
@@ -427,10 +430,41 @@ typedef struct {
   int64_t block, topk, offset, width;
   int32_t in_dtype;
   int32_t reserved;
+  const double *kbar;
 } la_gate_select_args;
 
 size_t la_gate_select_workspace(const la_gate_select_args *a);
 int la_gate_select(const la_gate_select_args *a, void *stream);
+
+/*
+ * Block means of keys for the gate routing, kept across decode steps.
+ * Replaces the block_reduce pooling that MoBAAttention.select repeats over
+ * every key at every call (variants/selection.py:620-624; core.py:102-120):
+ * a decode step re-pools only the block its new key landed in.  Block j of
+ * (b, h) is written as la_gate_select pools it: fp64, rows j*block ..
+ * j*block + block - 1 added in order and the sum divided by `block`, rows
+ * at or past T_b repeating row T_b - 1 (T_b = lengths[b] clamped to [0, T]
+ * when given, else T; a sequence without rows gets zeros).  Blocks pooled:
+ * first_block .. first_block + n_blocks - 1 of every (b, h), or, with
+ * `positions` (int32 (B,)), only block positions[b] / block of sequence b
+ * (entries outside [0, n_kb) pool nothing).  k: (B, H, T, D) at element
+ * strides, unit stride over D; out: (B, H, n_kb, D) fp64 contiguous,
+ * n_kb = ceil(T / block); blocks not pooled keep their contents.  No
+ * workspace.
+ */
+typedef struct {
+  const void *k;
+  double *out;
+  const int32_t *positions;
+  const int32_t *lengths;
+  int64_t B, H, T, D;
+  int64_t k_sb, k_sh, k_st;
+  int64_t block, first_block, n_blocks;
+  int32_t in_dtype;
+  int32_t reserved;
+} la_block_means_args;
+
+int la_block_means(const la_block_means_args *a, void *stream);
 
 /*
  * XAttention block selection: XAttention.antidiagonal_scores / select

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -41,6 +41,7 @@ EXPORTED = (
     "la_paged_kv_append",
     "la_gate_select_workspace",
     "la_gate_select",
+    "la_block_means",
     "la_xattn_select",
     "la_device_status",
 )
@@ -124,7 +125,15 @@ class LaGateSelectArgs(ctypes.Structure):
                 ("ws_bytes", _i64), ("B", _i64), ("Hq", _i64), ("Hkv", _i64), ("Tq", _i64),
                 ("T", _i64), ("D", _i64), ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64),
                 ("k_sb", _i64), ("k_sh", _i64), ("k_st", _i64), ("block", _i64), ("topk", _i64),
-                ("offset", _i64), ("width", _i64), ("in_dtype", _i32), ("reserved", _i32)]
+                ("offset", _i64), ("width", _i64), ("in_dtype", _i32), ("reserved", _i32),
+                ("kbar", _vp)]
+
+
+class LaBlockMeansArgs(ctypes.Structure):
+    _fields_ = [("k", _vp), ("out", _vp), ("positions", _vp), ("lengths", _vp), ("B", _i64),
+                ("H", _i64), ("T", _i64), ("D", _i64), ("k_sb", _i64), ("k_sh", _i64),
+                ("k_st", _i64), ("block", _i64), ("first_block", _i64), ("n_blocks", _i64),
+                ("in_dtype", _i32), ("reserved", _i32)]
 
 
 class LaXattnSelectArgs(ctypes.Structure):
@@ -193,6 +202,7 @@ def load() -> ctypes.CDLL:
     L.la_gate_select_workspace.argtypes = [P(LaGateSelectArgs)]
     L.la_gate_select_workspace.restype = ctypes.c_size_t
     L.la_gate_select.argtypes = [P(LaGateSelectArgs), _vp]
+    L.la_block_means.argtypes = [P(LaBlockMeansArgs), _vp]
     L.la_xattn_select.argtypes = [P(LaXattnSelectArgs), _vp]
     L.la_xattn_select.restype = ctypes.c_int
     L.la_device_status.argtypes = [ctypes.POINTER(ctypes.c_uint32), _i32, _vp]

@@ -23,13 +23,25 @@ __device__ __forceinline__ int64_t seq_rows(const int32_t *lens, int64_t b, int6
   return lens ? min(max((int64_t)lens[b], (int64_t)0), T) : T;
 }
 
+// The block a pooling workgroup writes: blk0 + blockIdx.x, or, with per-
+// sequence positions, the block of positions[b] (-1 when outside [0, nb)).
+__device__ __forceinline__ int64_t pool_block(int64_t blk0, const int32_t *pos, int64_t b,
+                                              int64_t bs, int64_t nb) {
+  if (!pos) return blk0 + blockIdx.x;
+  const int64_t p = pos[b];
+  return (p >= 0 && p / bs < nb) ? p / bs : -1;
+}
+
 // qbar/kbar[b][h][blk][d] = (sum_{i<bs} x[b][h][min(blk*bs+i, T_b-1)][d]) / bs
 // (T_b = seq_rows; a sequence without rows pools zeros, which no list reads)
 __global__ __launch_bounds__(128) void mean_pool_kernel(const void *x, int dt, int64_t T, int64_t D,
                                                         int64_t sb, int64_t sh, int64_t st,
                                                         int64_t bs, int64_t H, int64_t nb,
-                                                        double *out, const int32_t *lens) {
-  const int64_t blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+                                                        double *out, const int32_t *lens,
+                                                        int64_t blk0, const int32_t *pos) {
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int64_t blk = pool_block(blk0, pos, b, bs, nb);
+  if (blk < 0) return;
   const int64_t base = b * sb + h * sh;
   T = seq_rows(lens, b, T);
   if (T == 0) {
@@ -55,10 +67,13 @@ __global__ __launch_bounds__(NT) void mean_pool_vec_kernel(const void *x, int dt
                                                             int64_t D, int64_t sb, int64_t sh,
                                                             int64_t st, int64_t bs, int64_t H,
                                                             int64_t nb, double *out,
-                                                            const int32_t *lens) {
+                                                            const int32_t *lens, int64_t blk0,
+                                                            const int32_t *pos) {
   extern __shared__ __align__(16) unsigned char rows[];  // bs rows of D * ESZ bytes
   constexpr int CH = 64 * 512 / 16 / NT;                  // chunks per thread (max)
-  const int64_t blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int64_t blk = pool_block(blk0, pos, b, bs, nb);
+  if (blk < 0) return;  // (workgroup-uniform)
   const int tid = threadIdx.x;
   T = seq_rows(lens, b, T);
   if (T == 0) {  // (workgroup-uniform)
@@ -100,89 +115,117 @@ __global__ __launch_bounds__(NT) void mean_pool_vec_kernel(const void *x, int dt
   }
 }
 
-constexpr int BS_TQ = 64, BS_TK = 64, BS_DC = 32, BS_NT = 256;
+constexpr int BS_DC = 32, BS_NT = 256;
 
 // scores[(b*Hq+h)*nqb + i][j] = sum_d fl(qbar[b,h,i,d] * kbar[b,h/G,j,d]) for
-// the 64x64 tile (i, j).  Row i sits at position pos0 + i*qunit and column j
-// starts at j*kunit; tiles whose every column starts past every row's
-// position are skipped (causal: their scores are never read).
+// the TQ x TK tile (i, j), TK = (256 / (TQ / RQ)) * RK: each thread holds
+// RQ x RK scores.  Row i sits at position pos0 + i*qunit and column j starts
+// at j*kunit; tiles whose every column starts past every row's position are
+// skipped (causal: their scores are never read).  TQ = 64 (4 x 4 per thread)
+// for prefill rows; TQ = 4 (one score per thread, 64 columns) for decode,
+// where a 64-row tile would compute 63 empty rows per query.
+template <int TQ, int RQ, int RK>
 __global__ __launch_bounds__(BS_NT) void block_score_kernel(const double *qbar, const double *kbar,
                                                             int64_t Hq, int64_t Hkv, int64_t nqb,
                                                             int64_t nkb, int64_t D, int64_t pos0,
                                                             int64_t qunit, int64_t kunit,
                                                             double *scores) {
-  __shared__ double sq[BS_DC][BS_TQ + 2];
-  __shared__ double sk[BS_DC][BS_TK + 2];
+  constexpr int TY = TQ / RQ, TX = BS_NT / TY, TK = TX * RK;
+  static_assert(TY * TX == BS_NT, "tile shape");
+  __shared__ double sq[BS_DC][TQ + 2];
+  __shared__ double sk[BS_DC][TK + 2];
   const int tid = threadIdx.x;
-  const int tq = tid >> 4, tk = tid & 15;  // rows 4*tq.., cols 4*tk..
-  const int64_t i0 = (int64_t)blockIdx.y * BS_TQ, j0 = (int64_t)blockIdx.x * BS_TK;
+  const int tq = tid / TX, tk = tid % TX;  // rows RQ*tq.., cols RK*tk..
+  const int64_t i0 = (int64_t)blockIdx.y * TQ, j0 = (int64_t)blockIdx.x * TK;
   const int64_t bh = blockIdx.z;
   const int64_t b = bh / Hq, h = bh % Hq;
-  if (j0 * kunit > pos0 + min(i0 + BS_TQ - 1, nqb - 1) * qunit) return;  // all in the future
+  if (j0 * kunit > pos0 + min(i0 + TQ - 1, nqb - 1) * qunit) return;  // all in the future
   const double *qb = qbar + bh * nqb * D;
   const double *kb = kbar + (b * Hkv + h / (Hq / Hkv)) * nkb * D;
-  double acc[4][4];
+  double acc[RQ][RK];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < RQ; ++a)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[a][c] = 0.0;
+    for (int c = 0; c < RK; ++c) acc[a][c] = 0.0;
   for (int64_t d0 = 0; d0 < D; d0 += BS_DC) {
     const int dn = (int)min((int64_t)BS_DC, D - d0);
     __syncthreads();
-    for (int x = tid; x < BS_TQ * BS_DC; x += BS_NT) {
+    for (int x = tid; x < TQ * BS_DC; x += BS_NT) {
       const int r = x / BS_DC, dd = x % BS_DC;
       sq[dd][r] = (dd < dn && i0 + r < nqb) ? qb[(i0 + r) * D + d0 + dd] : 0.0;
+    }
+    for (int x = tid; x < TK * BS_DC; x += BS_NT) {
+      const int r = x / BS_DC, dd = x % BS_DC;
       sk[dd][r] = (dd < dn && j0 + r < nkb) ? kb[(j0 + r) * D + d0 + dd] : 0.0;
     }
     __syncthreads();
     for (int dd = 0; dd < dn; ++dd) {
-      double qv[4], kv[4];
+      double qv[RQ], kv[RK];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        qv[a] = sq[dd][4 * tq + a];
-        kv[a] = sk[dd][4 * tk + a];
-      }
+      for (int a = 0; a < RQ; ++a) qv[a] = sq[dd][RQ * tq + a];
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+      for (int c = 0; c < RK; ++c) kv[c] = sk[dd][RK * tk + c];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[a][c] = add_product(acc[a][c], qv[a], kv[c]);
+      for (int a = 0; a < RQ; ++a)
+#pragma unroll
+        for (int c = 0; c < RK; ++c) acc[a][c] = add_product(acc[a][c], qv[a], kv[c]);
     }
   }
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int64_t i = i0 + 4 * tq + a;
+  for (int a = 0; a < RQ; ++a) {
+    const int64_t i = i0 + RQ * tq + a;
     if (i >= nqb) continue;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int64_t j = j0 + 4 * tk + c;
+    for (int c = 0; c < RK; ++c) {
+      const int64_t j = j0 + RK * tk + c;
       if (j < nkb) scores[(bh * nqb + i) * nkb + j] = acc[a][c];
     }
   }
 }
 
+// Scores of every (row, column) tile of (B * Hq) heads; the tile shape
+// follows the number of rows.
+static void block_scores(const double *qbar, const double *kbar, int64_t B, int64_t Hq,
+                         int64_t Hkv, int64_t nqb, int64_t nkb, int64_t D, int64_t pos0,
+                         int64_t qunit, int64_t kunit, double *scores, hipStream_t st) {
+  if (nqb <= 4)
+    block_score_kernel<4, 1, 1><<<dim3((unsigned)ceil_div(nkb, 64), (unsigned)ceil_div(nqb, 4),
+                                       (unsigned)(B * Hq)),
+                                  BS_NT, 0, st>>>(qbar, kbar, Hq, Hkv, nqb, nkb, D, pos0, qunit,
+                                                  kunit, scores);
+  else
+    block_score_kernel<64, 4, 4><<<dim3((unsigned)ceil_div(nkb, 64), (unsigned)ceil_div(nqb, 64),
+                                        (unsigned)(B * Hq)),
+                                   BS_NT, 0, st>>>(qbar, kbar, Hq, Hkv, nqb, nkb, D, pos0, qunit,
+                                                   kunit, scores);
+}
+
 // Mean of every `bs` rows of x[b][h] (rows past T_b repeat row T_b-1) into
 // out[b][h][blk][d] in fp64; bs = 1 is the exact widening to fp64.  T_b is
-// lens[b] (ragged batch) or T.
+// lens[b] (ragged batch) or T.  Blocks blk0 .. blk0 + npool - 1 (all nb by
+// default), or the block of pos[b] for each sequence b (npool = 1).
 static void pool_rows(const void *x, int dt, int64_t B, int64_t H, int64_t T, int64_t D, int64_t sb,
                       int64_t sh, int64_t s_t, int64_t bs, int64_t nb, double *out,
-                      hipStream_t st, const int32_t *lens = nullptr) {
+                      hipStream_t st, const int32_t *lens = nullptr, int64_t blk0 = 0,
+                      int64_t npool = -1, const int32_t *pos = nullptr) {
   const int64_t esz = dt == LA_F32 ? 4 : 2;
-  const dim3 grid((unsigned)nb, (unsigned)H, (unsigned)B);
+  if (npool < 0) npool = nb;
+  const dim3 grid((unsigned)npool, (unsigned)H, (unsigned)B);
   const bool vec = bs <= 64 && (D * esz) % 16 == 0 && D * esz <= 512 && (uintptr_t)x % 16 == 0 &&
                    (sb * esz) % 16 == 0 && (sh * esz) % 16 == 0 && (s_t * esz) % 16 == 0;
   const size_t lds = (size_t)(bs * D * esz);
   // 128 threads when one thread per d covers the row (the block stays in LDS
   // only while it is summed, so several blocks per CU overlap)
   if (vec && esz == 4 && D <= 128)
-    mean_pool_vec_kernel<4, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
+    mean_pool_vec_kernel<4, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens, blk0, pos);
   else if (vec && esz == 4)
-    mean_pool_vec_kernel<4, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
+    mean_pool_vec_kernel<4, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens, blk0, pos);
   else if (vec && D <= 128)
-    mean_pool_vec_kernel<2, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
+    mean_pool_vec_kernel<2, 128><<<grid, 128, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens, blk0, pos);
   else if (vec)
-    mean_pool_vec_kernel<2, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
+    mean_pool_vec_kernel<2, 256><<<grid, 256, lds, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens, blk0, pos);
   else
-    mean_pool_kernel<<<grid, 128, 0, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens);
+    mean_pool_kernel<<<grid, 128, 0, st>>>(x, dt, T, D, sb, sh, s_t, bs, H, nb, out, lens, blk0, pos);
 }
 
 struct BsLayout {
@@ -240,9 +283,7 @@ extern "C" int la_block_select(const la_block_select_args *a, void *stream) {
   pool_rows(a->k, a->in_dtype, a->B, a->Hkv, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block, L.nkb,
             kbar, st, a->lengths);
   LA_LAUNCHED();
-  block_score_kernel<<<dim3((unsigned)ceil_div(L.nkb, BS_TK), (unsigned)ceil_div(L.nqb, BS_TQ),
-                            (unsigned)(a->B * a->Hq)),
-                       BS_NT, 0, st>>>(qbar, kbar, a->Hq, a->Hkv, L.nqb, L.nkb, a->D, 0, 1, 1, sc);
+  block_scores(qbar, kbar, a->B, a->Hq, a->Hkv, L.nqb, L.nkb, a->D, 0, 1, 1, sc, st);
   LA_LAUNCHED();
   TopkKParams tp{};
   tp.scores = sc;
@@ -286,12 +327,13 @@ static GsLayout gs_layout(const la_gate_select_args *a) {
   L.nkb = ceil_div(a->T, a->block);
   L.qbar_off = 0;
   L.kbar_off = L.qbar_off + a->B * a->Hq * a->Tq * a->D * 8;
-  L.sc_off = L.kbar_off + a->B * a->Hkv * L.nkb * a->D * 8;
+  // (no pooled keys when the caller keeps them)
+  L.sc_off = L.kbar_off + (a->kbar ? 0 : a->B * a->Hkv * L.nkb * a->D * 8);
   L.bytes = L.sc_off + a->B * a->Hq * a->Tq * L.nkb * 8;
   return L;
 }
 static int gs_validate(const la_gate_select_args *a) {
-  LA_REQUIRE(a && a->q && a->k && a->out_idx, "la_gate_select: null pointer");
+  LA_REQUIRE(a && a->q && (a->k || a->kbar) && a->out_idx, "la_gate_select: null pointer");
   LA_REQUIRE(a->B > 0 && a->Hq > 0 && a->Hkv > 0 && a->Tq > 0 && a->T > 0 && a->D > 0 &&
                  a->block > 0,
              "la_gate_select: bad shape");
@@ -326,13 +368,15 @@ extern "C" int la_gate_select(const la_gate_select_args *a, void *stream) {
   pool_rows(a->q, a->in_dtype, a->B, a->Hq, a->Tq, a->D, a->q_sb, a->q_sh, a->q_st, 1, a->Tq, qbar,
             st);  // q widened to fp64
   LA_LAUNCHED();
-  pool_rows(a->k, a->in_dtype, a->B, a->Hkv, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block,
-            L.nkb, kbar, st);
-  LA_LAUNCHED();
-  block_score_kernel<<<dim3((unsigned)ceil_div(L.nkb, BS_TK), (unsigned)ceil_div(a->Tq, BS_TQ),
-                            (unsigned)(a->B * a->Hq)),
-                       BS_NT, 0, st>>>(qbar, kbar, a->Hq, a->Hkv, a->Tq, L.nkb, a->D, a->offset, 1,
-                                       a->block, sc);
+  if (a->kbar) {  // block means kept by the caller (la_block_means)
+    kbar = const_cast<double *>(a->kbar);
+  } else {
+    pool_rows(a->k, a->in_dtype, a->B, a->Hkv, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block,
+              L.nkb, kbar, st);
+    LA_LAUNCHED();
+  }
+  block_scores(qbar, kbar, a->B, a->Hq, a->Hkv, a->Tq, L.nkb, a->D, a->offset, 1, a->block, sc,
+               st);
   LA_LAUNCHED();
   TopkKParams tp{};
   tp.scores = sc;
@@ -353,4 +397,35 @@ extern "C" int la_gate_select(const la_gate_select_args *a, void *stream) {
   tp.out_idx = a->out_idx;
   tp.out_count = a->out_count;
   return topk_launch(tp, st);
+}
+
+// ------------------------------------------------------------ block means --
+namespace la {
+static int bm_validate(const la_block_means_args *a) {
+  LA_REQUIRE(a && a->k && a->out, "la_block_means: null pointer");
+  LA_REQUIRE(a->B > 0 && a->H > 0 && a->T > 0 && a->D > 0 && a->block > 0,
+             "la_block_means: bad shape");
+  LA_REQUIRE(a->in_dtype == LA_F32 || a->in_dtype == LA_BF16 || a->in_dtype == LA_F16,
+             "la_block_means: k dtype");
+  const int64_t nkb = ceil_div(a->T, a->block);
+  if (!a->positions)
+    LA_REQUIRE(a->first_block >= 0 && a->n_blocks >= 0 && a->first_block + a->n_blocks <= nkb,
+               "la_block_means: blocks [%lld, %lld) outside [0, %lld)", (long long)a->first_block,
+               (long long)(a->first_block + a->n_blocks), (long long)nkb);
+  LA_REQUIRE(nkb < ((int64_t)1 << 31) && a->B < 65536 && a->H < 65536, "la_block_means: grid");
+  return LA_OK;
+}
+}  // namespace la
+
+extern "C" int la_block_means(const la_block_means_args *a, void *stream) {
+  const int rc = bm_validate(a);
+  if (rc != LA_OK) return rc;
+  const int64_t nkb = ceil_div(a->T, a->block);
+  const int64_t npool = a->positions ? 1 : a->n_blocks;
+  if (npool == 0) return LA_OK;
+  pool_rows(a->k, a->in_dtype, a->B, a->H, a->T, a->D, a->k_sb, a->k_sh, a->k_st, a->block, nkb,
+            a->out, (hipStream_t)stream, a->lengths, a->positions ? 0 : a->first_block, npool,
+            a->positions);
+  LA_LAUNCHED();
+  return LA_OK;
 }

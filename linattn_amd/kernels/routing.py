@@ -21,16 +21,66 @@ import torch
 
 from linattn_amd import _native as N
 
-__all__ = ["gate_select_hip", "nsa_selection_hip", "xattn_select_hip"]
+__all__ = ["block_means_hip", "gate_select_hip", "nsa_selection_hip", "xattn_select_hip"]
+
+
+def block_means_hip(k: torch.Tensor, *, block: int, out: Optional[torch.Tensor] = None,
+                    first_block: int = 0, n_blocks: Optional[int] = None,
+                    positions: Optional[torch.Tensor] = None,
+                    lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block means of k (B, H, T, D) as ``gate_select_hip`` pools them:
+    (B, H, ceil(T/block), D) fp64, each block's rows added in order and
+    divided by ``block``, the tail block repeating the last row
+    (block_reduce, core.py:102-120).  Pools blocks ``first_block`` ..
+    ``first_block + n_blocks - 1`` (all by default) into ``out`` (allocated
+    when None; other blocks keep their values), or, with ``positions``
+    (int32 (B,)), only the block holding positions[b] in sequence b: a decode
+    step re-pools just the block its new key joined, instead of the per-call
+    pooling of every key in MoBAAttention.select (selection.py:620-624).
+    ``lengths`` (int32 (B,)): rows of each sequence (the tail repeats row
+    lengths[b] - 1)."""
+    dev = N.require_gpu(k, positions, lengths, what="block_means_hip")
+    if k.dim() != 4 or k.stride(3) != 1:
+        raise ValueError("k must be (B, H, T, D) with contiguous rows")
+    if k.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError("k must be fp32, bf16 or fp16")
+    B, H, T, D = k.shape
+    if block <= 0 or T == 0:
+        raise ValueError("block > 0 and T > 0 required")
+    nkb = (T + block - 1) // block
+    if out is None:
+        out = torch.empty(B, H, nkb, D, dtype=torch.float64, device=dev)
+    elif out.shape != (B, H, nkb, D) or out.dtype != torch.float64 or not out.is_contiguous() \
+            or out.device != dev:
+        raise ValueError(f"out must be a contiguous fp64 ({B}, {H}, {nkb}, {D}) tensor on {dev}")
+    for name, t in (("positions", positions), ("lengths", lengths)):
+        if t is not None and (t.dtype != torch.int32 or t.shape != (B,)):
+            raise ValueError(f"{name} must be int32 ({B},)")
+    a = N.LaBlockMeansArgs()
+    a.k, a.out = k.data_ptr(), out.data_ptr()
+    positions = positions.contiguous() if positions is not None else None
+    lengths = lengths.contiguous() if lengths is not None else None
+    a.positions, a.lengths = N.ptr(positions), N.ptr(lengths)
+    a.B, a.H, a.T, a.D = B, H, T, D
+    a.k_sb, a.k_sh, a.k_st = k.stride(0), k.stride(1), k.stride(2)
+    a.block = block
+    a.first_block = first_block
+    a.n_blocks = nkb - first_block if n_blocks is None else n_blocks
+    a.in_dtype = N.dtype_code(k.dtype)
+    N.check(N.load().la_block_means(ctypes.byref(a), N.stream_handle(dev)), "block_means_hip")
+    return out
 
 
 def gate_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int, topk: int,
-                    offset: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+                    offset: int = 0, kbar: Optional[torch.Tensor] = None
+                    ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Block lists (B, Hq, Tq, min(topk, n_blocks) + 1), ascending, -1 padded,
     and counts (B, Hq, Tq).  q (B, Hq, Tq, D) at positions offset + t; k
     (B, Hkv, T, D) with Hq a multiple of Hkv (query head h reads KV head
-    h // (Hq/Hkv), repeat_kv of selection.py:623)."""
-    dev = N.require_gpu(q, k, what="gate_select_hip")
+    h // (Hq/Hkv), repeat_kv of selection.py:623).  ``kbar``: the block
+    means of k kept by the caller (``block_means_hip``); given, k is not
+    read (only its shape is used)."""
+    dev = N.require_gpu(q, k, kbar, what="gate_select_hip")
     if q.dim() != 4 or k.dim() != 4 or q.shape[0] != k.shape[0] or q.shape[3] != k.shape[3]:
         raise ValueError("q (B, Hq, Tq, D) and k (B, Hkv, T, D) expected")
     if q.dtype != k.dtype:
@@ -44,10 +94,14 @@ def gate_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int, topk: int,
     if block <= 0 or topk < 1 or offset < 0:
         raise ValueError("block > 0, topk >= 1 and offset >= 0 required")
     n_kb = (T + block - 1) // block
+    if kbar is not None and (kbar.shape != (B, Hkv, n_kb, D) or kbar.dtype != torch.float64
+                             or not kbar.is_contiguous()):
+        raise ValueError(f"kbar must be a contiguous fp64 ({B}, {Hkv}, {n_kb}, {D}) tensor")
     width = min(topk, n_kb) + 1
     ids = torch.empty(B, Hq, Tq, width, dtype=torch.int32, device=dev)
     counts = torch.empty(B, Hq, Tq, dtype=torch.int32, device=dev)
     a = N.LaGateSelectArgs()
+    a.kbar = N.ptr(kbar)
     a.q, a.k, a.out_idx, a.out_count = q.data_ptr(), k.data_ptr(), ids.data_ptr(), counts.data_ptr()
     a.B, a.Hq, a.Hkv, a.Tq, a.T, a.D = B, Hq, Hkv, Tq, T, D
     a.q_sb, a.q_sh, a.q_st = q.stride(0), q.stride(1), q.stride(2)

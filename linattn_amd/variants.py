@@ -33,7 +33,7 @@ from linattn_amd.kernels.block_sparse import sparse_attention
 from linattn_amd.kernels.fused_indexer import indexer_topk
 from linattn_amd.kernels.quest_pages import alloc_page_meta, page_update_hip, quest_select_hip
 from linattn_amd.kernels.prefill import block_sparse_prefill
-from linattn_amd.kernels.routing import gate_select_hip, xattn_select_hip
+from linattn_amd.kernels.routing import block_means_hip, gate_select_hip, xattn_select_hip
 
 __all__ = ["HipAttention", "HipQuest", "HipDSA", "HipMoBA", "HipXAttention", "HipSlidingWindow",
            "HipStreamingSink", "SUPPORTED"]
@@ -310,10 +310,41 @@ class HipMoBA(HipAttention):
 
     reference = "moba"
 
+    def prepare_state(self, batch, device, dtype):
+        state = super().prepare_state(batch, device, dtype)
+        state["block_means"] = None
+        return state
+
+    def push_kv(self, state, k, v):
+        """Append the keys and re-pool only the blocks they touched: the
+        state keeps the fp64 block means the gate reads (``block_means_hip``),
+        where the reference pools every key at every call
+        (selection.py:620-624)."""
+        start = state["k"].shape[-2]
+        state = super().push_kv(state, k, v)
+        kk = state["k"]
+        B, Hkv, t, D = kk.shape
+        if t == 0:
+            return state
+        bs = self.cfg.block_size
+        nkb = (t + bs - 1) // bs
+        first = start // bs
+        old = state.get("block_means")
+        if old is not None and old.shape == (B, Hkv, nkb, D) and old.device == kk.device:
+            means = old  # the new keys stayed in the known blocks: refresh in place
+        else:
+            means = torch.empty(B, Hkv, nkb, D, dtype=torch.float64, device=kk.device)
+            if old is not None and first > 0:
+                means[:, :, :first].copy_(old[:, :, :first])
+        block_means_hip(kk, block=bs, out=means, first_block=first, n_blocks=nkb - first)
+        state["block_means"] = means
+        return state
+
     def attend(self, q, state, offset: int = 0):
         k, v = state["k"], state["v"]
         bs = self.cfg.block_size
-        ids, counts = gate_select_hip(q, k, block=bs, topk=self.cfg.topk_blocks, offset=offset)
+        ids, counts = gate_select_hip(q, k, block=bs, topk=self.cfg.topk_blocks, offset=offset,
+                                      kbar=state.get("block_means"))
         out = sparse_attention(q, k, v, ids, unit=bs, counts=counts, causal=True, offset=offset,
                                out_dtype=q.dtype)
         self._extra = {"blocks_per_query": float(counts.to(torch.float64).mean()),

@@ -34,6 +34,7 @@ __all__ = [
     "repeat_kv",
     "causal_mask",
     "block_reduce",
+    "block_means",
     "dense_attention",
     "block_sparse_attention",
     "attend_lists",
@@ -502,6 +503,25 @@ def block_select(q, k, *, block: int, topk: int, sink_blocks: int = 1,
 
 
 # ------------------------------------------------------ per-query routing --
+def block_means(k, block: int) -> np.ndarray:
+    """The pooled keys the gate reads: block_reduce (core.py:102-120; the tail
+    block repeats the last row) of k (B, H, T, D) in fp64 with each block's
+    rows added in order and the sum divided by ``block`` (or_mean_pool, the
+    pooling of gate_select).  Returns (B, H, ceil(T / block), D)."""
+    k = to_f64(k)
+    B, H, T, D = k.shape
+    nkb = (T + block - 1) // block
+    L = lib()
+    out = np.zeros((B, H, nkb, D))
+    for b in range(B):
+        for h in range(H):
+            x = np.ascontiguousarray(k[b, h])
+            o = np.zeros((nkb, D))
+            L.or_mean_pool(_p(x, _D), T, D, block, _p(o, _D))
+            out[b, h] = o
+    return out
+
+
 def gate_select(q, k, *, block: int, topk: int, offset: int = 0) -> np.ndarray:
     """MoBA's gate routing (selection.py:610-640), also NSA's blockwise
     selection (native_sparse.py:78-93): for query t at position offset + t,

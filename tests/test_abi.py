@@ -26,6 +26,7 @@ STRUCTS = {
     "la_prefill_args": N.LaPrefillArgs,
     "la_kv_append_args": N.LaKvAppendArgs,
     "la_gate_select_args": N.LaGateSelectArgs,
+    "la_block_means_args": N.LaBlockMeansArgs,
     "la_xattn_select_args": N.LaXattnSelectArgs,
 }
 

@@ -194,6 +194,71 @@ def test_gate_select_bit_exact(dev, dtype, hq, hkv, T):
     assert np.array_equal(ids1.cpu().numpy(), ref1)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_block_means_cache(dev, dtype):
+    """Block means kept on append: a full pooling equals the oracle's bit for
+    bit (tail block padded with the last row); re-pooling only the block of
+    each appended key, one token at a time (and ragged, per-sequence
+    positions and lengths), leaves the cache equal to a fresh pooling; the
+    routing reads the cache instead of k and returns the same lists."""
+    from linattn_amd.kernels.routing import block_means_hip, gate_select_hip
+
+    B, Hq, Hkv, T, D, bs = 2, 8, 2, 150, 64, 16
+    q, k, _ = inputs(B, Hq, Hkv, T, D, seed=9)
+    q, k = q.to(dtype).to(dev), k.to(dtype).to(dev)
+    full = block_means_hip(k, block=bs)
+    assert np.array_equal(full.cpu().numpy(), oracle.block_means(k.cpu(), bs))
+    # decode: keys appended one at a time from 120 rows, only the new key's block re-pooled
+    t0 = 120
+    means = block_means_hip(k[:, :, :t0], block=bs)
+    for t in range(t0 + 1, T + 1):
+        nkb = (t + bs - 1) // bs
+        if means.shape[2] != nkb:
+            grown = torch.zeros(B, Hkv, nkb, D, dtype=torch.float64, device=dev)
+            grown[:, :, :means.shape[2]] = means
+            means = grown
+        pos = torch.full((B,), t - 1, dtype=torch.int32, device=dev)
+        block_means_hip(k[:, :, :t], block=bs, out=means, positions=pos)
+    assert np.array_equal(means.cpu().numpy(), full.cpu().numpy())
+    # ragged: sequence b holds lengths[b] rows; its last block re-pooled alone
+    lens = torch.tensor([T, 97], dtype=torch.int32, device=dev)
+    rag = full.clone()
+    block_means_hip(k, block=bs, out=rag, positions=lens - 1, lengths=lens)
+    ref1 = oracle.block_means(k[1:, :, :97].cpu(), bs)
+    assert np.array_equal(rag[1, :, (97 - 1) // bs].cpu().numpy(), ref1[0, :, -1])
+    assert np.array_equal(rag[0].cpu().numpy(), full[0].cpu().numpy())
+    # the gate reads the cache: same lists as pooling k, and as the oracle
+    for off, qq in ((0, q), (T - 1, q[:, :, -1:])):
+        ids, counts = gate_select_hip(qq, k, block=bs, topk=3, offset=off, kbar=full)
+        ids0, counts0 = gate_select_hip(qq, k, block=bs, topk=3, offset=off)
+        assert torch.equal(ids, ids0) and torch.equal(counts, counts0)
+        assert np.array_equal(ids.cpu().numpy(),
+                              oracle.gate_select(qq.cpu(), k.cpu(), block=bs, topk=3, offset=off))
+
+
+def test_hip_moba_decode_keeps_block_means(dev):
+    """hip_moba's state carries the block means across decode steps (refreshed
+    for the touched blocks only); after a prefill and 40 single-token steps
+    they equal a fresh pooling of the cache, and each step's output matches
+    the oracle's."""
+    from linattn_amd.kernels.routing import block_means_hip
+
+    c = cfg()
+    q, k, v = inputs(1, 4, 2, 160, 64, seed=10)
+    var = build("hip_moba", c)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    _, state = var.forward(qd[:, :, :120], kd[:, :, :120], vd[:, :, :120], chunk=120)
+    for t in range(120, 160):
+        out, state = var.forward(qd[:, :, t:t + 1], kd[:, :, t:t + 1], vd[:, :, t:t + 1],
+                                 state=state, chunk=1)
+        ids = oracle.gate_select(q[:, :, t:t + 1], k[:, :, :t + 1], block=c.block_size,
+                                 topk=c.topk_blocks, offset=t)
+        ref = oracle.attend_lists(q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1], ids,
+                                  unit=c.block_size, causal=True, offset=t)
+        assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
+    assert torch.equal(state["block_means"], block_means_hip(state["k"], block=c.block_size))
+
+
 @pytest.mark.parametrize("chunk", [160, 48])
 def test_hip_moba_matches_oracle(dev, chunk):
     c = cfg()

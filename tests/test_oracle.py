@@ -523,6 +523,28 @@ def test_gate_select_ranking_bruteforce():
             assert set(s) == set(top) | {own}
 
 
+def test_block_means_pins():
+    """The gate's pooled keys (block_reduce, core.py:102-120): on small
+    integers every summation order is exact, so they equal numpy's mean of the
+    tail-padded blocks bit for bit; the tail block of a hand-made input is
+    (sum of its rows + copies of the last row) / block; on normal data they
+    agree with numpy's (pairwise) mean to rounding."""
+    r = rng(21)
+    x = r.integers(-50, 50, size=(2, 3, 37, 5)).astype(np.float64)
+    bs = 8
+    m = oracle.block_means(x, bs)
+    nkb = (37 + bs - 1) // bs
+    pad = np.concatenate([x, np.repeat(x[:, :, -1:], nkb * bs - 37, axis=2)], axis=2)
+    assert np.array_equal(m, pad.reshape(2, 3, nkb, bs, 5).mean(3))
+    y = np.array([[1.0, 2.0], [3.0, 5.0], [7.0, 11.0]]).reshape(1, 1, 3, 2)
+    assert np.array_equal(oracle.block_means(y, 2)[0, 0],
+                          np.array([[2.0, 3.5], [7.0, 11.0]]))
+    assert np.array_equal(oracle.block_means(y, 4)[0, 0], np.array([[(1 + 3 + 7 + 7) / 4.0,
+                                                                       (2 + 5 + 11 + 11) / 4.0]]))
+    z = r.standard_normal((1, 2, 100, 16))
+    assert np.allclose(oracle.block_means(z, 16), oracle.block_reduce(z, 16), rtol=0, atol=1e-15)
+
+
 def test_gate_select_full_budget_recovers_dense():
     """test_budgets.py:64-81 for MoBA: with every block routed the output is
     dense causal attention; with an offset (decode) as well."""
