@@ -10,10 +10,12 @@
 // increasing h as fl(acc + fl(w*r)) -- never fused.  The CPU oracle computes
 // the same expression, so selections match bit for bit.
 //
-// Two score kernels, both VALU fp64 (matrix-core accumulation order is not
-// specified, so MFMA cannot reproduce these bits):
-//  - tiled (prefill): a 64-query x 128-key tile per workgroup, 8x4 register
-//    tile per thread, q/k slices staged in LDS as fp32 (exact for bf16);
+// Score kernels:
+//  - matrix-core tiles (prefill, 2-byte q and k): 64 queries x 64 keys per
+//    workgroup on v_mfma_f64_16x16x4f64, whose in-order accumulation keeps
+//    the sequential sum's bits (products of 2-byte values are exact);
+//  - VALU tiles (fp32 or unaligned inputs): a 64-query x 128-key tile per
+//    workgroup, 8x4 register tile per thread, q/k slices staged in LDS;
 //  - per-key (decode, few queries): 64 keys per workgroup, one thread per
 //    (key, head) reading the key row from LDS.
 // Scores of a chunk of queries go to the workspace and the shared row top-k
@@ -129,19 +131,10 @@ __global__ __launch_bounds__(IT_NT) void indexer_tile_kernel(IdxKP p) {
   }
 }
 
-// Tiled scores for 2-byte q/k whose (head, d) rows are 16-byte aligned, the
-// shape of config C2.  Same 64-query x 128-key tile and fp64 arithmetic as
-// indexer_tile_kernel, restaged for throughput:
-//  - a (head, 64-d) slice is loaded with coalesced 16-byte loads (8 lanes per
-//    row), the next slice's loads in flight while the current one is
-//    computed; q goes to LDS as fp64 and k as fp32, both row-major;
-//  - thread (tq, tk) owns queries 8 tq .. 8 tq + 7 and keys tk + 32 c
-//    (c < 4): each k read of a wave covers 32 consecutive rows (no bank
-//    conflicts), the q reads are broadcasts, and only k is converted in the
-//    inner loop (each k value feeds 8 FMAs);
-//  - the head weights of the tile's queries are staged once.
+// 2-byte q/k whose (head, d) rows are 16-byte aligned (the shape of config
+// C2) are loaded as (head, 64-d) slices with coalesced 16-byte loads (8 lanes
+// per row) and widened to fp32 (exact) for LDS.
 constexpr int IT16_D = 64;  // d slice
-constexpr int IT16_QS = IT16_D + 2, IT16_KS = IT16_D + 4;  // LDS row strides (fp64, fp32)
 
 template <bool BF>
 __device__ __forceinline__ void widen8(const uint4 &v, float (&x)[8]) {
@@ -158,79 +151,89 @@ __device__ __forceinline__ void widen8(const uint4 &v, float (&x)[8]) {
   }
 }
 
+// The score tile on the fp64 matrix cores (2-byte q and k): a workgroup
+// covers 64 queries x 64 keys, wave w keys [k0 + 32 (w % 2), +32) x
+// queries [q0 + 32 (w / 2), +32) as 2 x 2 tiles of v_mfma_f64_16x16x4f64
+// (A = key rows, B = query columns, one fp64 value per lane each); three
+// workgroups per CU.  gfx950 accumulates that instruction as a chain in k
+// order, c = fl(fl(fl(fl(c + a0 b0) + a1 b1) + a2 b2) + a3 b3), and a product
+// of two 2-byte values is exact in fp64, so chaining the instructions over d
+// in increasing order yields the bits of the sequential sum (tests pin this
+// on the device).  Lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]
+// (d = 4 s + l / 16 of chunk s) and receives D[4 e + l / 16][l % 16], e < 4.
+// q and k slices are staged in LDS as fp32 (exact) with rows padded to 68
+// floats, so the 16 rows x 4 columns a fragment read touches fall in
+// distinct banks; the next slice is loaded into registers during this one.
+constexpr int IM_S = 68;   // LDS row stride (fp32)
+constexpr int IM_K = 64;   // keys per workgroup (queries: IT_Q)
+constexpr int IM_NT = 256;
+
 template <bool BF>
-__global__ __launch_bounds__(IT_NT, 2) void indexer_tile16_kernel(IdxKP p) {
-  __shared__ __align__(16) double sq[IT_Q][IT16_QS];
-  __shared__ __align__(16) float sk[IT_K][IT16_KS];
+__global__ __launch_bounds__(IM_NT, 3) void indexer_mfma_kernel(IdxKP p) {
+  typedef double f64x4 __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) float sq[IT_Q][IM_S];
+  __shared__ __align__(16) float sk[IM_K][IM_S];
   __shared__ float sw[IT_Q][8];
-  const int tid = threadIdx.x;
-  const int tq = tid >> 5, tk = tid & 31;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r16 = lane & 15, kq = lane >> 4;
   const int64_t b = blockIdx.z;
   const int64_t q0 = (int64_t)blockIdx.y * IT_Q;  // within the chunk
-  const int64_t k0 = (int64_t)blockIdx.x * IT_K;
+  const int64_t k0 = (int64_t)blockIdx.x * IM_K;
   if (q0 >= p.tn) return;
   if (p.causal) {
     const int64_t last_q = p.offset + p.t0 + min(q0 + IT_Q, p.tn) - 1;
     if (k0 * p.unit > last_q) return;
   }
   const int HI = (int)p.HI, d = (int)p.d;
-  for (int i = tid; i < IT_Q * HI; i += IT_NT) {
+  for (int i = tid; i < IT_Q * HI; i += IM_NT) {
     const int r = i / HI, h = i % HI;
     const int64_t t = p.t0 + min(q0 + r, p.tn - 1);
     sw[r][h] = p.w[b * p.w_sb + t * p.w_st + h * p.w_sh];
   }
   const uint16_t *qb = (const uint16_t *)p.q + b * p.q_sb;
   const uint16_t *kb = (const uint16_t *)p.k + b * p.k_sb;
-  // slice loads: chunk c of q (c < 512) is row c/8, d-chunk c%8; k likewise
-  // (c < 1024).  Rows past the chunk / key range read a clamped row.
-  uint4 lq[2], lk[4];
+  // slice loads: chunk c (c < 512) of q is row c/8, d-chunk c%8; k likewise.
+  // Rows past the chunk / key range read a clamped row.
+  uint4 lq[2], lk[2];
   auto fetch = [&](int h, int d0) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int c = tid + u * IT_NT, r = c >> 3, dc = c & 7;
+      const int c = tid + u * IM_NT, r = c >> 3, dc = c & 7;
       const int64_t t = p.t0 + min(q0 + r, p.tn - 1);
-      const int dd = min(d0 + dc * 8, d - 8);
-      lq[u] = *(const uint4 *)(qb + t * p.q_st + h * p.q_sh + dd);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = tid + u * IT_NT, r = c >> 3, dc = c & 7;
       const int64_t s = min(k0 + r, p.Tk - 1);
       const int dd = min(d0 + dc * 8, d - 8);
+      lq[u] = *(const uint4 *)(qb + t * p.q_st + h * p.q_sh + dd);
       lk[u] = *(const uint4 *)(kb + s * p.k_st + h * p.k_sh + dd);
     }
   };
   auto stage = [&]() {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int c = tid + u * IT_NT, r = c >> 3, dc = c & 7;
+      const int c = tid + u * IM_NT, r = c >> 3, dc = c & 7;
       float x[8];
       widen8<BF>(lq[u], x);
-#pragma unroll
-      for (int e = 0; e < 8; e += 2)
-        *(double2 *)&sq[r][dc * 8 + e] = double2{(double)x[e], (double)x[e + 1]};
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = tid + u * IT_NT, r = c >> 3, dc = c & 7;
-      float x[8];
+      *(float4 *)&sq[r][dc * 8] = float4{x[0], x[1], x[2], x[3]};
+      *(float4 *)&sq[r][dc * 8 + 4] = float4{x[4], x[5], x[6], x[7]};
       widen8<BF>(lk[u], x);
       *(float4 *)&sk[r][dc * 8] = float4{x[0], x[1], x[2], x[3]};
       *(float4 *)&sk[r][dc * 8 + 4] = float4{x[4], x[5], x[6], x[7]};
     }
   };
-  double score[8][4];
+  const int kw = w & 1, qw = w >> 1;
+  f64x4 score[2][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) score[i][c] = 0.0;
+    for (int jb = 0; jb < 2; ++jb) score[ib][jb] = f64x4{0.0, 0.0, 0.0, 0.0};
+  const float *ka = &sk[32 * kw + r16][kq];
+  const float *qa = &sq[32 * qw + r16][kq];
   fetch(0, 0);
   for (int h = 0; h < HI; ++h) {
-    double dot[8][4];
+    f64x4 dot[2][2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dot[i][c] = 0.0;
+      for (int jb = 0; jb < 2; ++jb) dot[ib][jb] = f64x4{0.0, 0.0, 0.0, 0.0};
     for (int d0 = 0; d0 < d; d0 += IT16_D) {
       const int dn = min(IT16_D, d - d0);
       __syncthreads();  // the previous slice is consumed
@@ -241,45 +244,51 @@ __global__ __launch_bounds__(IT_NT, 2) void indexer_tile16_kernel(IdxKP p) {
         const int nh = last_d ? h + 1 : h, nd = last_d ? 0 : d0 + IT16_D;
         fetch(min(nh, HI - 1), nd);
       }
-      for (int dd = 0; dd < dn; dd += 4) {
-        float4 k4[4];
+      auto chunk = [&](int dd) {
+        double a[2], bq[2];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) k4[c] = *(const float4 *)&sk[tk + 32 * c][dd];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          double kv[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) kv[c] = (double)(e == 0 ? k4[c].x : e == 1 ? k4[c].y : e == 2 ? k4[c].z : k4[c].w);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const double qv = sq[8 * tq + i][dd + e];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) dot[i][c] = __builtin_fma(qv, kv[c], dot[i][c]);
-          }
+        for (int i = 0; i < 2; ++i) {
+          a[i] = (double)ka[16 * i * IM_S + dd];
+          bq[i] = (double)qa[16 * i * IM_S + dd];
         }
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb)
+            dot[ib][jb] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[ib], bq[jb], dot[ib][jb], 0, 0, 0);
+      };
+      if (dn == IT16_D) {
+#pragma unroll
+        for (int dd = 0; dd < IT16_D; dd += 4) chunk(dd);
+      } else {
+        for (int dd = 0; dd < dn; dd += 4) chunk(dd);
       }
     }
     // head epilogue: score += fl(w * relu(dot)), heads in increasing order
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const double wv = (double)sw[8 * tq + i][h];
+    for (int jb = 0; jb < 2; ++jb) {
+      const double wv = (double)sw[32 * qw + 16 * jb + r16][h];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const double r = dot[i][c] > 0.0 ? dot[i][c] : 0.0;
-        score[i][c] = add_product(score[i][c], wv, r);
-      }
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const double x = dot[ib][jb][e];
+          score[ib][jb][e] = add_product(score[ib][jb][e], wv, x > 0.0 ? x : 0.0);
+        }
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t ql = q0 + 8 * tq + i;
+  for (int jb = 0; jb < 2; ++jb) {
+    const int64_t ql = q0 + 32 * qw + 16 * jb + r16;
     if (ql >= p.tn) continue;
     double *row = p.scores + (b * p.tn + ql) * p.Tk;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int64_t s = k0 + tk + 32 * c;
-      if (s < p.Tk) row[s] = score[i][c];
-    }
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t s = k0 + 32 * kw + 16 * ib + 4 * e + kq;
+        if (s < p.Tk) row[s] = score[ib][jb][e];
+      }
   }
 }
 
@@ -658,10 +667,12 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
                               st>>>(p);
     } else {
       const dim3 grid((unsigned)ceil_div(a->Tk, IT_K), (unsigned)ceil_div(p.tn, IT_Q), (unsigned)a->B);
+      const dim3 grid_m((unsigned)ceil_div(a->Tk, IM_K), (unsigned)ceil_div(p.tn, IT_Q),
+                        (unsigned)a->B);
       if (tile16 && a->in_dtype == LA_BF16)
-        indexer_tile16_kernel<true><<<grid, IT_NT, 0, st>>>(p);
+        indexer_mfma_kernel<true><<<grid_m, IM_NT, 0, st>>>(p);
       else if (tile16)
-        indexer_tile16_kernel<false><<<grid, IT_NT, 0, st>>>(p);
+        indexer_mfma_kernel<false><<<grid_m, IM_NT, 0, st>>>(p);
       else
         indexer_tile_kernel<<<grid, IT_NT, 0, st>>>(p);
     }

@@ -94,6 +94,38 @@ def test_indexer_decode_form(dev, tq, hi, d, dtype):
     check(q, k, w, 512, dev, causal=True, offset=5000 - tq)
 
 
+def test_indexer_summation_order_is_sequential(dev):
+    """The tiled score kernel adds q.k products over d in increasing order
+    (the matrix-core form relies on gfx950's in-order fp64 accumulation).
+    Each key row is a shuffle of +-2^60 pairs and small integers, so its
+    fp64 sum depends on the order (a small value added to a +-2^60 partial
+    sum is absorbed); with q = 1 and w = 1 the score is relu(sum).  The
+    ranking of every key and the values equal the oracle's sequential sums;
+    an unordered or pairwise sum would change them."""
+    r = np.random.default_rng(7)
+    Tq, Tk, d = 64, 256, 64
+    big = np.ldexp(1.0, 60)
+    rows = []
+    for _ in range(Tk):
+        vals = np.concatenate([[big, -big, big, -big], r.integers(1, 100, size=d - 4)])
+        rows.append(r.permutation(vals))
+    k = torch.tensor(np.array(rows), dtype=torch.float64).to(torch.bfloat16).view(1, Tk, 1, d)
+    q = torch.ones(1, Tq, 1, d, dtype=torch.bfloat16)
+    w = torch.ones(1, Tq, 1)
+    seq = [0.0] * Tk
+    for j, row in enumerate(k[0, :, 0].double().numpy()):
+        acc = 0.0
+        for x in row:
+            acc = acc + x
+        seq[j] = max(acc, 0.0)
+    assert len(set(seq)) > 20  # the order matters for these rows
+    check(q, k, w, Tk, dev)
+    val, _ = indexer_topk(q.to(dev), k.to(dev), w.to(dev), Tk)
+    want = np.sort(np.array(seq))[::-1].astype(np.float32)
+    assert np.array_equal(val[0, 0].cpu().numpy(), want)
+    assert np.array_equal(val[0, -1].cpu().numpy(), want)
+
+
 def test_config2_indexer_full_size(dev):
     """C2: B=1, T=8192, 4 heads of dim 64, bf16 q/k, w ~ U(0,1), causal top-2048,
     int32 indices.  Every row is checked for structure; 48 rows (both ends and
