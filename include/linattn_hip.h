@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 9
+#define LA_ABI_VERSION 10
 
 /* element types */
 enum {
@@ -490,7 +490,14 @@ int la_block_means(const la_block_means_args *a, void *stream);
  * *width + i] ascending, -1 padded, width >= n_kb (mode 0) or
  * min(topk, n_kb) + 1 (mode 1); out_count[(b*Hq + h)*n_qb + qb].  Limits:
  * block <= 64, n_kb <= 4096, LDS block*D*4 + n_kb*n_slots*8 <= 120 KiB.
- * No workspace.
+ * Workspace (optional): with workspace >= la_xattn_select_workspace() bytes,
+ * shapes with stride == block >= 2, 2-byte q/k and 16-byte aligned rows
+ * (D a multiple of 8) score on the fp64 matrix cores first (for stride ==
+ * block the antidiagonal entries pair query rows i mod block with key rows
+ * -i mod block: block dense gram products per head, in-order fp64
+ * accumulation over d, the same bits) and the selection reads the slots from
+ * the workspace; otherwise the selection kernel scores every slot itself.
+ * la_xattn_select_workspace() returns 0 when no workspace is used.
  */
 typedef struct {
   const void *q;
@@ -505,8 +512,11 @@ typedef struct {
   double inv_sqrt_d;
   int32_t mode;
   int32_t in_dtype;
+  void *workspace;
+  int64_t ws_bytes;
 } la_xattn_select_args;
 
+size_t la_xattn_select_workspace(const la_xattn_select_args *a);
 int la_xattn_select(const la_xattn_select_args *a, void *stream);
 
 /*

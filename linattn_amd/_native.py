@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -42,6 +42,7 @@ EXPORTED = (
     "la_gate_select_workspace",
     "la_gate_select",
     "la_block_means",
+    "la_xattn_select_workspace",
     "la_xattn_select",
     "la_device_status",
 )
@@ -142,7 +143,7 @@ class LaXattnSelectArgs(ctypes.Structure):
                 ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64), ("k_sb", _i64), ("k_sh", _i64),
                 ("k_st", _i64), ("block", _i64), ("stride", _i64), ("offset", _i64),
                 ("topk", _i64), ("width", _i64), ("inv_sqrt_d", ctypes.c_double),
-                ("mode", _i32), ("in_dtype", _i32)]
+                ("mode", _i32), ("in_dtype", _i32), ("workspace", _vp), ("ws_bytes", _i64)]
 
 
 class LaPrefillArgs(ctypes.Structure):
@@ -203,6 +204,8 @@ def load() -> ctypes.CDLL:
     L.la_gate_select_workspace.restype = ctypes.c_size_t
     L.la_gate_select.argtypes = [P(LaGateSelectArgs), _vp]
     L.la_block_means.argtypes = [P(LaBlockMeansArgs), _vp]
+    L.la_xattn_select_workspace.argtypes = [P(LaXattnSelectArgs)]
+    L.la_xattn_select_workspace.restype = ctypes.c_size_t
     L.la_xattn_select.argtypes = [P(LaXattnSelectArgs), _vp]
     L.la_xattn_select.restype = ctypes.c_int
     L.la_device_status.argtypes = [ctypes.POINTER(ctypes.c_uint32), _i32, _vp]

@@ -69,6 +69,7 @@ struct XaKP {
   const void *q, *k;
   int32_t *out_idx, *out_count;
   const double *alpha;  // per query head (threshold mode)
+  double *slots;        // optional: [b][h][qb][kb][slot] scored by xattn_slots_mfma_kernel
   int64_t B, Hq, Hkv, Tq, T, D;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st;
   int64_t blk, r, n_slots, offset, n_qb, n_kb, topk, width;
@@ -105,6 +106,162 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t *red) {
   return t;
 }
 
+// Slot scores on the fp64 matrix cores when stride == block (>= 2): slot 0
+// of (qb, kb) is entry (0, 0) and slot 1 the entries (i, block - i),
+// i = 1 .. block-1, so query row qb*block + i only meets key rows kb*block +
+// ((block - i) mod block): for each residue i the entries of every (qb, kb)
+// form one dense gram product G_i = Q_i K_i^T (Q_i the query rows i mod
+// block, K_i the key rows -i mod block).  slot0 = (0 + G_0) * inv_sqrt_d and
+// slot1 = (((0 + G_1) + G_2) + ... + G_{block-1}) * inv_sqrt_d, the oracle's
+// order.  A workgroup covers 64 query blocks x 64 key blocks of one (b, h);
+// wave w computes key blocks [kb0 + 32 (w % 2), +32) x query blocks
+// [qb0 + 32 (w / 2), +32) as 2 x 2 tiles of v_mfma_f64_16x16x4f64 (A = key
+// rows, B = query rows, one value per lane; lane l supplies d = 4 c + l / 16
+// of chunk c and receives D[4 e + l / 16][l % 16]).  The instruction
+// accumulates in k order and a product of 2-byte values is exact in fp64,
+// so the entries carry the bits of the sequential sum over d.  Rows past Tq
+// or T are zero rows (F.pad).  Slices of 64 dims are staged in LDS as fp32
+// (rows padded to 68 floats: conflict-free fragment reads), the next slice
+// loaded into registers during this one.  Tiles wholly past causality are
+// skipped.
+constexpr int XM_T = 64, XM_D = 64, XM_S = XM_D + 4, XM_NT = 256;
+
+template <bool BF>
+__device__ __forceinline__ void xm_widen8(const uint4 &v, float (&x)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (BF) {
+      x[2 * e] = bf16lo(w[e]);
+      x[2 * e + 1] = bf16hi(w[e]);
+    } else {
+      x[2 * e] = __half2float(__ushort_as_half((uint16_t)(w[e] & 0xffffu)));
+      x[2 * e + 1] = __half2float(__ushort_as_half((uint16_t)(w[e] >> 16)));
+    }
+  }
+}
+
+template <bool BF>
+__global__ __launch_bounds__(XM_NT, 2) void xattn_slots_mfma_kernel(XaKP p) {
+  typedef double f64x4 __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) float sq[XM_T][XM_S];
+  __shared__ __align__(16) float sk[XM_T][XM_S];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int64_t kb0 = (int64_t)blockIdx.x * XM_T, qb0 = (int64_t)blockIdx.y * XM_T;
+  const int64_t bh = blockIdx.z, b = bh / p.Hq, h = bh % p.Hq, kvh = h / (p.Hq / p.Hkv);
+  const int64_t blk = p.blk;
+  const int D = (int)p.D;
+  if (qb0 >= p.n_qb) return;
+  const int64_t qlast = min(qb0 + XM_T, p.n_qb) - 1;
+  if (kb0 * blk > qlast * blk + p.offset) return;  // every key block past causality
+  const uint16_t *qbase = (const uint16_t *)p.q + b * p.q_sb + h * p.q_sh;
+  const uint16_t *kbase = (const uint16_t *)p.k + b * p.k_sb + kvh * p.k_sh;
+  // slice loads: chunk c (< 512) is row c / 8, 16-byte chunk c % 8, for the
+  // query rows (qb0 + row) * blk + i and the key rows (kb0 + row) * blk + j
+  uint4 lq[2], lk[2];
+  auto fetch = [&](int64_t i, int d0) {
+    const int64_t j = (blk - i) % blk;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + u * XM_NT, r = c >> 3, dc = c & 7;
+      const int dd = min(d0 + dc * 8, D - 8);
+      const int64_t t = (qb0 + r) * blk + i, s = (kb0 + r) * blk + j;
+      lq[u] = (qb0 + r < p.n_qb && t < p.Tq) ? *(const uint4 *)(qbase + t * p.q_st + dd)
+                                              : uint4{0u, 0u, 0u, 0u};
+      lk[u] = (kb0 + r < p.n_kb && s < p.T) ? *(const uint4 *)(kbase + s * p.k_st + dd)
+                                             : uint4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + u * XM_NT, r = c >> 3, dc = c & 7;
+      float x[8];
+      xm_widen8<BF>(lq[u], x);
+      *(float4 *)&sq[r][dc * 8] = float4{x[0], x[1], x[2], x[3]};
+      *(float4 *)&sq[r][dc * 8 + 4] = float4{x[4], x[5], x[6], x[7]};
+      xm_widen8<BF>(lk[u], x);
+      *(float4 *)&sk[r][dc * 8] = float4{x[0], x[1], x[2], x[3]};
+      *(float4 *)&sk[r][dc * 8 + 4] = float4{x[4], x[5], x[6], x[7]};
+    }
+  };
+  const int kw = w & 1, qw = w >> 1;
+  const float *ka = &sk[32 * kw + r16][kq];
+  const float *qa = &sq[32 * qw + r16][kq];
+  // output slot of this lane's element (ib, jb, e): key block kb0 + 32 kw +
+  // 16 ib + 4 e + kq, query block qb0 + 32 qw + 16 jb + r16
+  auto store = [&](const f64x4 (&v)[2][2], int slot) {  // slot 0: (0 + entry) * inv_sqrt_d
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
+      const int64_t qb = qb0 + 32 * qw + 16 * jb + r16;
+      if (qb >= p.n_qb) continue;
+      double *rowp = p.slots + ((bh * p.n_qb + qb) * p.n_kb) * p.n_slots + slot;
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t kb = kb0 + 32 * kw + 16 * ib + 4 * e + kq;
+          if (kb < p.n_kb)
+            rowp[kb * p.n_slots] = (slot == 0 ? 0.0 + v[ib][jb][e] : v[ib][jb][e]) * p.inv_sqrt_d;
+        }
+    }
+  };
+  f64x4 slot1[2][2];
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) slot1[ib][jb] = f64x4{0.0, 0.0, 0.0, 0.0};
+  fetch(0, 0);
+  for (int64_t i = 0; i < blk; ++i) {
+    f64x4 dot[2][2];
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) dot[ib][jb] = f64x4{0.0, 0.0, 0.0, 0.0};
+    for (int d0 = 0; d0 < D; d0 += XM_D) {
+      const int dn = min(XM_D, D - d0);
+      __syncthreads();  // the previous slice is consumed
+      stage();
+      __syncthreads();
+      {  // next slice in flight during this one
+        const bool last_d = d0 + XM_D >= D;
+        fetch(last_d ? min(i + 1, blk - 1) : i, last_d ? 0 : d0 + XM_D);
+      }
+      auto chunk = [&](int dd) {
+        double a[2], bq[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          a[x] = (double)ka[16 * x * XM_S + dd];
+          bq[x] = (double)qa[16 * x * XM_S + dd];
+        }
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb)
+            dot[ib][jb] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[ib], bq[jb], dot[ib][jb], 0, 0, 0);
+      };
+      if (dn == XM_D) {
+#pragma unroll
+        for (int dd = 0; dd < XM_D; dd += 4) chunk(dd);
+      } else {
+        for (int dd = 0; dd < dn; dd += 4) chunk(dd);
+      }
+    }
+    if (i == 0) {
+      store(dot, 0);
+    } else {
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) slot1[ib][jb][e] = slot1[ib][jb][e] + dot[ib][jb][e];
+    }
+  }
+  store(slot1, 1);
+}
+
 template <int KPT>
 __global__ __launch_bounds__(TK_NT) void xattn_select_kernel(XaKP p) {
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -124,21 +281,26 @@ __global__ __launch_bounds__(TK_NT) void xattn_select_kernel(XaKP p) {
   double *ss = (double *)(dyn + xa_align16(blk * D * 4));  // [n_kb][NS]
   uint32_t *bm = (uint32_t *)(ss + n_kb * NS);    // bitmap of kept blocks
 
-  for (int64_t x = tid; x < blk * D; x += TK_NT) {
-    const int64_t i = x / D, d = x % D, t = qb * blk + i;
-    sq[x] = t < p.Tq ? load_as_f32(p.q, b * p.q_sb + h * p.q_sh + t * p.q_st + d, p.in_dt) : 0.f;
-  }
-  for (int64_t x = tid; x < (n_kb + 31) / 32; x += TK_NT) bm[x] = 0u;
-  __syncthreads();
-
   // visible key blocks: kb*blk <= qb*blk + offset
   const int64_t pos0 = qb * blk + p.offset;
   const int64_t lim = min(pos0 / blk, n_kb - 1);
   const int64_t n_vis = lim + 1;
   const int64_t kbase = b * p.k_sb + kvh * p.k_sh;
 
+  if (p.slots) {  // scored on the matrix cores: the row's visible slots
+    const double *src = p.slots + row * n_kb * NS;
+    for (int64_t x = tid; x < n_vis * NS; x += TK_NT) ss[x] = src[x];
+  } else {
+    for (int64_t x = tid; x < blk * D; x += TK_NT) {
+      const int64_t i = x / D, d = x % D, t = qb * blk + i;
+      sq[x] = t < p.Tq ? load_as_f32(p.q, b * p.q_sb + h * p.q_sh + t * p.q_st + d, p.in_dt) : 0.f;
+    }
+  }
+  for (int64_t x = tid; x < (n_kb + 31) / 32; x += TK_NT) bm[x] = 0u;
+  __syncthreads();
+
   // slot scores of the visible blocks, one block per thread
-  for (int64_t kb = tid; kb < n_vis; kb += TK_NT) {
+  for (int64_t kb = p.slots ? n_vis : tid; kb < n_vis; kb += TK_NT) {
     for (int64_t s = 0; s < NS; ++s) {
       const int64_t o = s * p.r;
       double acc = 0.0;
@@ -307,6 +469,28 @@ static int xattn_lds(const la_xattn_select_args *a, int64_t n_kb, int64_t ns, si
   return bytes <= 120 * 1024 ? LA_OK : LA_ERR_UNSUPPORTED;
 }
 
+// Slots on the matrix cores: stride == block >= 2, 2-byte q and k, 16-byte
+// aligned rows with D a multiple of 8.
+static bool xattn_mfma_shape(const la_xattn_select_args *a) {
+  const bool two = a->in_dtype == LA_BF16 || a->in_dtype == LA_F16;
+  return two && a->block >= 2 && a->stride == a->block && a->D % 8 == 0 &&
+         (uintptr_t)a->q % 16 == 0 && (uintptr_t)a->k % 16 == 0 && a->q_sb % 8 == 0 &&
+         a->q_sh % 8 == 0 && a->q_st % 8 == 0 && a->k_sb % 8 == 0 && a->k_sh % 8 == 0 &&
+         a->k_st % 8 == 0;
+}
+
+static int64_t xattn_slot_bytes(const la_xattn_select_args *a) {
+  const int64_t n_kb = ceil_div(a->T, a->block), n_qb = ceil_div(a->Tq, a->block);
+  const int64_t ns = (2 * a->block - 2) / a->stride + 1;
+  return a->B * a->Hq * n_qb * n_kb * ns * 8;
+}
+
+extern "C" size_t la_xattn_select_workspace(const la_xattn_select_args *a) {
+  if (!a || a->B <= 0 || a->Hq <= 0 || a->Tq <= 0 || a->T <= 0 || a->block < 1 || a->stride < 1)
+    return 0;
+  return xattn_mfma_shape(a) ? (size_t)xattn_slot_bytes(a) : 0;
+}
+
 extern "C" int la_xattn_select(const la_xattn_select_args *a, void *stream) {
   LA_REQUIRE(a && a->q && a->k && a->out_idx && a->out_count, "la_xattn_select: null pointer");
   LA_REQUIRE(a->B > 0 && a->Hq > 0 && a->Hkv > 0 && a->Tq > 0 && a->T > 0 && a->D > 0,
@@ -350,6 +534,17 @@ extern "C" int la_xattn_select(const la_xattn_select_args *a, void *stream) {
   const int64_t nwg = a->B * a->Hq * n_qb;
   LA_REQUIRE(nwg < ((int64_t)1 << 31), "la_xattn_select: too many rows");
   hipStream_t st = (hipStream_t)stream;
+  if (a->workspace && xattn_mfma_shape(a) && a->ws_bytes >= xattn_slot_bytes(a)) {
+    p.slots = (double *)a->workspace;
+    LA_REQUIRE(a->B * a->Hq < 65536, "la_xattn_select: B * Hq >= 65536");
+    const dim3 grid((unsigned)ceil_div(n_kb, XM_T), (unsigned)ceil_div(n_qb, XM_T),
+                    (unsigned)(a->B * a->Hq));
+    if (a->in_dtype == LA_BF16)
+      xattn_slots_mfma_kernel<true><<<grid, XM_NT, 0, st>>>(p);
+    else
+      xattn_slots_mfma_kernel<false><<<grid, XM_NT, 0, st>>>(p);
+    LA_LAUNCHED();
+  }
   const int kpt = (int)ceil_div(n_kb, TK_NT);
   auto launch = [&](auto kern) -> int {
     if (lds > 64 * 1024)

@@ -196,5 +196,9 @@ def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride
     a.inv_sqrt_d = 1.0 / math.sqrt(D)
     a.mode = 0 if topk is None else 1
     a.in_dtype = N.dtype_code(q.dtype)
-    N.check(N.load().la_xattn_select(ctypes.byref(a), N.stream_handle(dev)), "xattn_select_hip")
+    L = N.load()
+    ws_bytes = L.la_xattn_select_workspace(ctypes.byref(a))
+    ws = N.workspace(ws_bytes, dev) if ws_bytes else None
+    a.workspace, a.ws_bytes = N.ptr(ws), ws_bytes
+    N.check(L.la_xattn_select(ctypes.byref(a), N.stream_handle(dev)), "xattn_select_hip")
     return ids, counts

@@ -66,6 +66,34 @@ def test_xattn_select_topk_and_offset(dev, t, tq, block, topk):
     check_lists(ids, counts, ref_ids, ref_counts)
 
 
+def test_xattn_slots_summation_order(dev):
+    """Slot entries are fp64 sums over d in increasing order (the matrix-core
+    scorer for stride == block relies on the in-order fp64 accumulation).
+    With q = 1 every entry is its key row's sum; each key row shuffles +-2^60
+    pairs with small integers, so that sum depends on the order (a small value
+    added to a +-2^60 partial sum is absorbed) and so do the slots, masses and
+    lists, which equal the oracle's."""
+    r = np.random.default_rng(9)
+    T, D = 256, 64
+    big = np.ldexp(1.0, 60)
+    rows = [r.permutation(np.concatenate([[big, -big, big, -big], r.integers(1, 60, size=D - 4)]))
+            for _ in range(T)]
+    k = torch.tensor(np.array(rows)).to(torch.bfloat16).view(1, 1, T, D)
+    q = torch.ones(1, 1, T, D, dtype=torch.bfloat16)
+    seq = []
+    for row in k[0, 0].double().numpy():
+        acc = 0.0
+        for x in row:
+            acc = acc + x
+        seq.append(acc)
+    pair = [float(np.sum(row)) for row in k[0, 0].double().numpy()]
+    assert sum(a != b for a, b in zip(seq, pair)) > T // 2  # the order matters
+    for thr in (0.5, 0.9):
+        ids, counts = xattn_select_hip(q.to(dev), k.to(dev), block=8, stride=8, threshold=thr)
+        ref_ids, ref_counts = oracle.xattn_select(q, k, block=8, stride=8, threshold=thr)
+        check_lists(ids, counts, ref_ids, ref_counts)
+
+
 def cfg(**kw):
     base = dict(n_heads=4, n_kv_heads=2, head_dim=64, block_size=16, topk_blocks=4)
     base.update(kw)
