@@ -424,6 +424,30 @@ def bench_c5(dev, steps, warmup, keep=None):
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def bench_fused_c4(dev, q, pool_k, pool_v, pt, mins, maxs, cfg, ids, counts, step_bytes,
+                   steps, warmup):
+    """The C4 step as one kernel (``quest_decode_fused``: selection and
+    attention per (b, KV head) workgroup), beside the two-launch step of the
+    headline; its lists must equal the headline's."""
+    import torch
+
+    from linattn_amd.kernels.paged_decode import quest_decode_fused
+
+    ps, T = cfg["page"], cfg["T"]
+
+    def step():
+        return quest_decode_fused(q, pool_k, pool_v, pt, mins, maxs, page_size=ps,
+                                  topk=cfg["topk"], pos=T - 1)
+
+    _, fids, fcounts = step()
+    same = bool(torch.equal(fids, ids) and torch.equal(fcounts, counts))
+    ms = time_cuda(step, steps, warmup)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    return {"workload": "C4 step as one kernel (quest_decode_fused)", "ms": round(ms, 4),
+            "tok_per_s": round(cfg["B"] / (ms * 1e-3), 1), "GBps": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "lists_equal_two_kernel": same}
+
+
 def bench_page_bounds(dev, pool_k, pt, mins, maxs, cfg, steps, warmup):
     """Quest metadata built from scratch over the whole C4 key pool (64 x 1024
     pages of 8 KV heads): channel min/max of every page (quest_pages.py:38-48),
@@ -746,6 +770,9 @@ def main() -> int:
     # side configurations: a few untimed calls first (clocks settle)
     sub, sub_w = max(3, args.steps // 4), 10
     keep = None if args.no_cpu_baseline else {}
+    if union:
+        result["fused_step"] = bench_fused_c4(dev, q, pool_k, pool_v, pt, mins, maxs, cfg, ids,
+                                              counts, step_bytes, sub, sub_w)
     result["page_bounds"] = bench_page_bounds(dev, pool_k, pt, mins, maxs, cfg, sub, sub_w)
     result["indexer"] = bench_c2(dev, sub, sub_w, keep)
     result["prefill"] = bench_c3(dev, sub, sub_w, keep)

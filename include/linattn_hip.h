@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 10
+#define LA_ABI_VERSION 11
 
 /* element types */
 enum {
@@ -224,6 +224,34 @@ typedef struct {
 } la_quest_select_args;
 
 int la_quest_select(const la_quest_select_args *a, void *stream);
+
+/*
+ * Fused Quest decode: page selection and attention in one kernel, the
+ * fusion of selector and decode kernel that docs/kernels.md:89-93 describes
+ * (FFD) beyond the fused top-k of quest_pages.py:110-113: the selected page
+ * list never leaves the chip before it is attended.  Replaces
+ * la_quest_select followed by la_sparse_attention for one decode query per
+ * sequence.  One workgroup of 512 threads per (b, KV head): the
+ * la_quest_select union selection of the G = Hq/Hkv query heads (select.Tq
+ * == 1; the list is also written to select.out_idx / out_count exactly as
+ * la_quest_select writes it; G in {2, 4}), then the matrix-core attention of the G heads
+ * over those pages of the paged pool `kv` (bf16 K/V, page_table, page_size a
+ * multiple of 16 and equal to select.page_size, head_dim 128, bf16 q),
+ * causal at the query's position (select.pos_offset, or select.positions[b])
+ * and within kv.kv_len, scale times q.k, output (B, Hq, 1, 128) at the o_*
+ * element strides in out_dtype (LA_F32, LA_BF16 or LA_F16).  Other shapes
+ * return LA_ERR_UNSUPPORTED with nothing launched.  No workspace.
+ */
+typedef struct {
+  la_quest_select_args select;
+  la_kv kv;
+  void *out;
+  int64_t o_sb, o_sh, o_st;
+  float scale;
+  int32_t out_dtype;
+} la_quest_decode_args;
+
+int la_quest_decode_fused(const la_quest_decode_args *a, void *stream);
 
 /*
  * Paged KV append with Quest page bounds maintained in the same pass.

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -30,6 +30,7 @@ EXPORTED = (
     "la_quest_page_bounds",
     "la_quest_scores",
     "la_quest_select",
+    "la_quest_decode_fused",
     "la_topk_rows_workspace",
     "la_topk_rows",
     "la_indexer_topk_workspace",
@@ -90,6 +91,11 @@ class LaQuestSelectArgs(ctypes.Structure):
                 ("m_sb", _i64), ("m_sh", _i64), ("m_sp", _i64), ("m_sd", _i64),
                 ("page_size", _i64), ("pos_offset", _i64), ("k", _i64), ("q_dtype", _i32),
                 ("meta_dtype", _i32), ("positions", _vp)]
+
+
+class LaQuestDecodeArgs(ctypes.Structure):
+    _fields_ = [("select", LaQuestSelectArgs), ("kv", LaKV), ("out", _vp), ("o_sb", _i64),
+                ("o_sh", _i64), ("o_st", _i64), ("scale", ctypes.c_float), ("out_dtype", _i32)]
 
 
 class LaKvAppendArgs(ctypes.Structure):
@@ -187,6 +193,7 @@ def load() -> ctypes.CDLL:
     L.la_quest_scores.argtypes = [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp,
                                   _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]
     L.la_quest_select.argtypes = [P(LaQuestSelectArgs), _vp]
+    L.la_quest_decode_fused.argtypes = [P(LaQuestDecodeArgs), _vp]
     L.la_topk_rows_workspace.argtypes = [P(LaTopkArgs)]
     L.la_topk_rows_workspace.restype = ctypes.c_size_t
     L.la_topk_rows.argtypes = [P(LaTopkArgs), _vp]

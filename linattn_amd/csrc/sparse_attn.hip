@@ -21,6 +21,7 @@
 
 #include "common.h"
 #include "kv_access.h"
+#include "quest_select.h"
 
 namespace la {
 
@@ -191,20 +192,19 @@ __device__ __forceinline__ bool token_rows(const AttnKP &p, const RowCtx &rc, co
 
 // Merges the per-wave softmax states (s_m, s_l, s_acc, filled by every wave
 // before a barrier) and writes the output row, or this split's partial state.
-template <int G, int D>
-__device__ __forceinline__ void finish_row(const AttnKP &p, const RowCtx &rc,
-                                           const float (*s_acc)[G][D], const float (*s_m)[G],
-                                           const float (*s_l)[G]) {
-  const int64_t r = blockIdx.y, split = blockIdx.x;
-  for (int i = threadIdx.x; i < G * D; i += SA_NT) {
+template <int G, int D, int NW = SA_NW>
+__device__ __forceinline__ void finish_row(const AttnKP &p, const RowCtx &rc, int64_t r,
+                                           int64_t split, const float (*s_acc)[G][D],
+                                           const float (*s_m)[G], const float (*s_l)[G]) {
+  for (int i = threadIdx.x; i < G * D; i += 64 * NW) {
     const int g = i / D, d = i % D;
     float M = __int_as_float(0xff800000);
 #pragma unroll
-    for (int x = 0; x < SA_NW; ++x) M = fmaxf(M, s_m[x][g]);
+    for (int x = 0; x < NW; ++x) M = fmaxf(M, s_m[x][g]);
     const float Mu = (M == __int_as_float(0xff800000)) ? 0.f : M;
     float L = 0.f, A = 0.f;
 #pragma unroll
-    for (int x = 0; x < SA_NW; ++x) {
+    for (int x = 0; x < NW; ++x) {
       const float sc = fast_exp2(s_m[x][g] - Mu);
       L += s_l[x][g] * sc;
       A += s_acc[x][g][d] * sc;
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(SA_NT) void sparse_attn_kernel(AttnKP p) {
     }
   }
   __syncthreads();
-  finish_row<G, D>(p, rc, s_acc, s_m, s_l);
+  finish_row<G, D>(p, rc, blockIdx.y, blockIdx.x, s_acc, s_m, s_l);
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -430,27 +430,41 @@ __device__ __forceinline__ float row_max16(float x) {
 // round and keeps q to ~2^-8 relative; the per-token K scale multiplies the
 // fp32 scores, and each V row is decoded in registers with its scale folded
 // into the token's weight.
-template <int KT, int G, bool PAGED, bool U16>
-__global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel(AttnKP p) {
+// LDS of the matrix-core attention body for NW waves (G heads, D = 128).
+template <int KT, int G, int NW>
+struct MfmaLds {
+  static constexpr int NRG = (G + 3) / 4;
+  float acc[NW][G][128];
+  float m[NW][G], l[NW][G];
+  __attribute__((aligned(16))) float p[NW][16][4 * NRG];
+  long q8[KT == LA_FP8_E4M3 ? 2 * 4 * 64 : 1];  // fp8: [term][s][lane] q codes
+  float sq;                                     // fp8: their scale
+};
+
+// The attention of one row by NW waves over the entries staged in s_tok0 /
+// s_phys (the caller synchronises after staging, before the body reads
+// them): every wave leaves its softmax state (m, l, acc) in L and the body
+// ends with a workgroup barrier, so finish_row can merge them.
+template <int KT, int G, bool PAGED, bool U16, int NW>
+__device__ __forceinline__ void mfma_attend(const AttnKP &p, const RowCtx &rc,
+                                            const int32_t *s_tok0, const int32_t *s_phys,
+                                            MfmaLds<KT, G, NW> &L) {
   constexpr bool F8 = KT == LA_FP8_E4M3;
   constexpr int ESZ = F8 ? 1 : 2;  // bytes per K/V element
   constexpr int D = 128;
   constexpr int RT = 16;            // tokens per wave round
   constexpr int NRG = (G + 3) / 4;  // DPP rows holding heads
   static_assert(G >= 1 && G <= 8, "group of at most 8 heads");
-
-  __shared__ int32_t s_tok0[SA_MAX_EPS];
-  __shared__ int32_t s_phys[PAGED ? SA_MAX_EPS : 1];
-  __shared__ float s_acc[SA_NW][G][D];
-  __shared__ float s_m[SA_NW][G], s_l[SA_NW][G];
-  __shared__ __align__(16) float s_p[SA_NW][RT][4 * NRG];
-  __shared__ long s_q8[F8 ? 2 * 4 * 64 : 1];  // fp8: [term][s][lane] q codes
-  __shared__ float s_sq;                      // fp8: their scale
+  auto &s_acc = L.acc;
+  auto &s_m = L.m;
+  auto &s_l = L.l;
+  auto &s_p = L.p;
+  long *s_q8 = L.q8;
+  float &s_sq = L.sq;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = lane & 15;     // V: 8-dim chunk; K: token of the round
   const int slot = lane >> 4;  // V: token slot; K: 8-dim group within 32
-  const RowCtx rc = stage_row<G, PAGED>(p, s_tok0, s_phys);
   const int32_t lim32 = (int32_t)min(rc.lim, (int64_t)0x7fffffff);
 
   // A operand: q row c (head c < G), dims 32s + 8*slot .. +8, raw bf16 bits
@@ -521,7 +535,7 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
   const int32_t F = (int32_t)(rc.ne * p.unit);
   const char *kbase = (const char *)p.kv.k;
   const char *vbase = (const char *)p.kv.v;
-  constexpr int32_t STEP = SA_NW * RT;
+  constexpr int32_t STEP = NW * RT;
   // One set of K/V registers, refilled as it is consumed: the next round's K
   // loads are issued once the current K is in the matrix core, and each V
   // row of the next round once the current one has been accumulated.
@@ -739,7 +753,112 @@ __global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel
     }
   }
   __syncthreads();
-  finish_row<G, D>(p, rc, s_acc, s_m, s_l);
+}
+
+template <int KT, int G, bool PAGED, bool U16>
+__global__ __launch_bounds__(SA_NT, G <= 4 ? 4 : 2) void sparse_attn_mfma_kernel(AttnKP p) {
+  __shared__ int32_t s_tok0[SA_MAX_EPS];
+  __shared__ int32_t s_phys[PAGED ? SA_MAX_EPS : 1];
+  __shared__ MfmaLds<KT, G, SA_NW> L;
+  const RowCtx rc = stage_row<G, PAGED>(p, s_tok0, s_phys);
+  mfma_attend<KT, G, PAGED, U16, SA_NW>(p, rc, s_tok0, s_phys, L);
+  finish_row<G, 128, SA_NW>(p, rc, blockIdx.y, blockIdx.x, L.acc, L.m, L.l);
+}
+
+
+// ---------------------------------------------- fused Quest decode ----
+// One workgroup of eight waves per (b, KV head) with one query per sequence:
+// the union page selection of the G heads (quest_select_union, as in
+// la_quest_select), the ascending list staged in LDS (first token and pool
+// row of every page) and written out for the caller, then the matrix-core
+// attention of the G heads over it by the eight waves and the merge of their
+// softmax states.  The selection's page keys and widened q are dead once the
+// list is staged, so the attention state reuses their LDS.
+constexpr int QD_NW = 8, QD_NT = 64 * QD_NW;
+
+template <int MT, int G, int KPT>
+struct QuestDecodeLds {
+  union {
+    struct {
+      uint64_t keys[G * TK_NT * KPT];
+      double qd[G * 256];
+    } sel;
+    MfmaLds<LA_BF16, G, QD_NW> att;
+  } u;
+  uint32_t bm[TK_NT * KPT / 32];
+  int32_t tok0[TK_NT * KPT];
+  int32_t phys[TK_NT * KPT];
+  int32_t n_e;
+};
+
+template <int MT, int G, int KPT>
+__global__ __launch_bounds__(QD_NT, 4) void quest_decode_fused_kernel(QsKP a, AttnKP p) {
+  __shared__ QuestDecodeLds<MT, G, KPT> L;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t row = blockIdx.x;  // (b, kvh)
+  const int64_t kvh = row % a.Hkv, b = row / a.Hkv;
+  int32_t n_v, own;
+  quest_select_union<MT, G, KPT, QD_NT>(a, b, kvh, 0, L.u.sel.keys, L.u.sel.qd, L.bm, n_v, own);
+  // the last key this query attends: its position, within the cache length
+  const int64_t pos = a.positions ? (int64_t)a.positions[b] : a.pos_offset;
+  const int64_t lim = min(kv_length(p.kv, b) - 1, pos);
+  if (w == 0) {  // the union in ascending order: LDS, out_idx, out_count
+    constexpr int WPL = (TK_NT * KPT / 32 + 63) / 64;  // bitmap words per lane
+    const int64_t words = (n_v + 31) / 32;
+    uint32_t bits[WPL];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int j = 0; j < WPL; ++j) {
+      const int64_t x = lane * WPL + j;
+      bits[j] = x < words ? L.bm[x] : 0u;
+      cnt += __popc(bits[j]);
+    }
+    uint32_t incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t v = (uint32_t)__shfl_up((int)incl, off, 64);
+      if (lane >= off) incl += v;
+    }
+    const uint32_t total = (uint32_t)__shfl((int)incl, 63, 64);
+    uint32_t at = incl - cnt;
+    int32_t *gout = a.out_idx + row * a.width;
+    const int64_t ps = a.page_size;
+    const int32_t *ptab = p.kv.page_table + b * p.kv.pt_stride;
+#pragma unroll
+    for (int j = 0; j < WPL; ++j) {
+      uint32_t bb = bits[j];
+      while (bb) {
+        const int bit = __ffs(bb) - 1;
+        const int32_t page = (int32_t)((lane * WPL + j) * 32 + bit);
+        if (at < (uint32_t)a.width) {
+          gout[at] = page;
+          const int64_t tok0 = (int64_t)page * ps;
+          const bool ok = tok0 <= lim;
+          L.tok0[at] = ok ? (int32_t)tok0 : -1;
+          L.phys[at] = ok ? (int32_t)(((int64_t)ptab[page] * a.Hkv + kvh) * ps) : 0;
+        }
+        ++at;
+        bb &= bb - 1;
+      }
+    }
+    for (int64_t jj = (int64_t)total + lane; jj < a.width; jj += 64) gout[jj] = -1;
+    if (lane == 0) {
+      const int32_t ne = (int32_t)min((int64_t)total, a.width);
+      L.n_e = ne;
+      if (a.out_count) a.out_count[row] = ne;
+    }
+  }
+  __syncthreads();
+  RowCtx rc{};
+  rc.b = b;
+  rc.t = 0;
+  rc.kvh = kvh;
+  rc.h0 = kvh * G;
+  rc.e0 = 0;
+  rc.ne = L.n_e;
+  rc.lim = lim;
+  mfma_attend<LA_BF16, G, true, true, QD_NW>(p, rc, L.tok0, L.phys, L.u.att);
+  finish_row<G, 128, QD_NW>(p, rc, row, 0, L.u.att.acc, L.u.att.m, L.u.att.l);
 }
 
 // Merge the split partials of one (row, head): one workgroup, D threads.
@@ -1007,4 +1126,101 @@ extern "C" int la_sparse_attention_noalloc(const la_sparse_attn_args *a, const l
     if (rc != LA_OK) return rc;
   }
   return sparse_attention_run(a, kv, pl, ws, (hipStream_t)stream);
+}
+
+namespace la {
+template <int MT, int G>
+static int launch_quest_decode(const QsKP &qk, const AttnKP &p, int64_t rows, hipStream_t st) {
+  quest_decode_fused_kernel<MT, G, 4><<<dim3((unsigned)rows), QD_NT, 0, st>>>(qk, p);
+  LA_LAUNCHED();
+  return LA_OK;
+}
+}  // namespace la
+
+extern "C" int la_quest_decode_fused(const la_quest_decode_args *a, void *stream) {
+  LA_REQUIRE(a, "la_quest_decode_fused: null arguments");
+  const la_quest_select_args *s = &a->select;
+  const la_kv *kv = &a->kv;
+  LA_REQUIRE(s->q && s->page_min && s->page_max && s->out_idx && a->out && kv->k && kv->v &&
+                 kv->page_table,
+             "la_quest_decode_fused: null pointer");
+  LA_REQUIRE(s->B > 0 && s->Hq > 0 && s->Hkv > 0 && s->n_pages > 0 && s->k > 0 && kv->T >= 1,
+             "la_quest_decode_fused: bad shape");
+  LA_REQUIRE(s->Hq % s->Hkv == 0, "n_heads must be a multiple of n_kv_heads");
+  LA_REQUIRE(s->page_size > 0 && kv->page_size == s->page_size && kv->pt_stride >= 1,
+             "la_quest_decode_fused: page sizes of the selection and the pool differ");
+  LA_REQUIRE(a->out_dtype == LA_F32 || a->out_dtype == LA_BF16 || a->out_dtype == LA_F16,
+             "la_quest_decode_fused: out dtype");
+  LA_REQUIRE(s->meta_dtype == LA_F32 || s->meta_dtype == LA_BF16, "la_quest_decode_fused: meta dtype");
+  const int64_t G = s->Hq / s->Hkv;
+  const int64_t esz = s->meta_dtype == LA_BF16 ? 2 : 4;
+  const bool layout = s->m_sp == 1 && s->m_sd % 4 == 0 && s->m_sd >= s->n_pages &&
+                      s->m_sb % 4 == 0 && s->m_sh % 4 == 0 &&
+                      (uintptr_t)s->page_min % (4 * esz) == 0 &&
+                      (uintptr_t)s->page_max % (4 * esz) == 0;
+  const bool shape = s->Tq == 1 && s->D == 128 && s->q_dtype == LA_BF16 && kv->dtype == LA_BF16 &&
+                     (G == 2 || G == 4) && s->n_pages <= TK_NT * 4 &&
+                     s->page_size % 16 == 0 && (uintptr_t)kv->k % 16 == 0 &&
+                     (uintptr_t)kv->v % 16 == 0;
+  if (!layout || !shape)
+    return fail(LA_ERR_UNSUPPORTED, "la_quest_decode_fused: shape or layout not fused");
+  LA_REQUIRE(s->n_pages * s->page_size < ((int64_t)1 << 31), "la_quest_decode_fused: cache span");
+  QsKP qk{};
+  qk.q = s->q;
+  qk.mn = s->page_min;
+  qk.mx = s->page_max;
+  qk.out_idx = s->out_idx;
+  qk.out_count = s->out_count;
+  qk.Hq = s->Hq;
+  qk.Hkv = s->Hkv;
+  qk.Tq = 1;
+  qk.D = s->D;
+  qk.q_sb = s->q_sb;
+  qk.q_sh = s->q_sh;
+  qk.q_st = s->q_st;
+  qk.n_pages = s->n_pages;
+  qk.m_sb = s->m_sb;
+  qk.m_sh = s->m_sh;
+  qk.m_sd = s->m_sd;
+  qk.page_size = s->page_size;
+  qk.pos_offset = s->pos_offset;
+  qk.positions = s->positions;
+  qk.k = std::max<int64_t>(1, std::min(s->k, s->n_pages));
+  qk.width = G * qk.k;
+  qk.q_dt = s->q_dtype;
+  AttnKP p{};
+  p.q = s->q;
+  p.out = a->out;
+  p.ids = s->out_idx;
+  p.counts = s->out_count;
+  p.kv = *kv;
+  p.B = s->B;
+  p.Hq = s->Hq;
+  p.Hkv = s->Hkv;
+  p.Tq = 1;
+  p.ids_heads = s->Hkv;
+  p.ids_rows = 1;
+  p.N = qk.width;
+  p.unit = s->page_size;
+  p.offset = s->pos_offset;
+  p.splits = 1;
+  p.eps = qk.width;
+  p.q_sb = s->q_sb;
+  p.q_sh = s->q_sh;
+  p.q_st = s->q_st;
+  p.o_sb = a->o_sb;
+  p.o_sh = a->o_sh;
+  p.o_st = a->o_st;
+  p.qscale = a->scale * 1.4426950408889634f;
+  p.q_dt = LA_BF16;
+  p.out_dt = a->out_dtype;
+  p.causal = 1;
+  p.staged = 1;
+  p.unit_shift = is_pow2(s->page_size) ? ilog2(s->page_size) : -1;
+  const int64_t rows = s->B * s->Hkv;
+  hipStream_t st = (hipStream_t)stream;
+  const bool bf = s->meta_dtype == LA_BF16;
+  if (G == 2)
+    return bf ? launch_quest_decode<LA_BF16, 2>(qk, p, rows, st) : launch_quest_decode<LA_F32, 2>(qk, p, rows, st);
+  return bf ? launch_quest_decode<LA_BF16, 4>(qk, p, rows, st) : launch_quest_decode<LA_F32, 4>(qk, p, rows, st);
 }

@@ -5,21 +5,26 @@
 the GPU.  ``quest_decode_step`` is the batched decode hot path: Quest page
 selection over a paged KV pool followed by split-K attention over the selected
 pages (the decode step of QuestAttention, variants/selection.py:139-248, driven
-by AttentionVariant.forward, core.py:231-279).
+by AttentionVariant.forward, core.py:231-279).  ``quest_decode_fused`` runs
+the same step as one kernel: each (b, KV head) workgroup selects its pages and
+attends them without the list leaving the chip.
 """
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Dict, Optional, Tuple
 
 import torch
 
-from linattn_amd.kernels.block_sparse import sparse_attention
+from linattn_amd import _native as N
+from linattn_amd.kernels.block_sparse import _kv_struct, sparse_attention
 from linattn_amd.kernels.fused_indexer import indexer_topk
 from linattn_amd.kernels.quest_pages import quest_select_hip
 
-__all__ = ["paged_decode", "quest_decode_step", "indexer_decode_step", "quantize_fp8_per_token"]
+__all__ = ["paged_decode", "quest_decode_step", "quest_decode_fused", "indexer_decode_step",
+           "quantize_fp8_per_token"]
 
 
 def quantize_fp8_per_token(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -116,4 +121,63 @@ def quest_decode_step(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tenso
     out = sparse_attention(q, k_pool, v_pool, ids, unit=page_size, counts=counts, causal=True,
                            offset=pos, page_table=page_table, page_size=page_size, kv_len=kv_len,
                            scale=scale, out_dtype=out_dtype, num_splits=num_splits)
+    return out, ids, counts
+
+
+def quest_decode_fused(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                       page_table: torch.Tensor, page_min: torch.Tensor, page_max: torch.Tensor, *,
+                       page_size: int, topk: int, pos: Optional[int] = None,
+                       positions: Optional[torch.Tensor] = None,
+                       kv_len: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                       out_dtype: Optional[torch.dtype] = None
+                       ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``quest_decode_step`` with the GQA union in one kernel
+    (``la_quest_decode_fused``): per (b, KV head), the page scores, top-k of
+    every query head, union and attention over the selected pages.  Same
+    arguments and results (out, ids, counts); the lists equal
+    ``quest_select_hip``'s bit for bit.  One query per sequence, bf16 q and
+    K/V, head_dim 128, at most 1024 pages, G = Hq/Hkv in {2, 4}; raises
+    NotImplementedError otherwise (``quest_decode_step`` covers every
+    shape)."""
+    dev = N.require_gpu(q, k_pool, v_pool, page_table, page_min, page_max, positions, kv_len,
+                        what="quest_decode_fused")
+    if (pos is None) == (positions is None):
+        raise ValueError("pass exactly one of pos and positions")
+    B, Hq, Tq, D = q.shape
+    Hkv, P = page_min.shape[1], page_min.shape[2]
+    if Tq != 1:
+        raise ValueError("quest_decode_fused: one query per sequence")
+    if page_min.shape != (B, Hkv, P, D) or page_max.shape != page_min.shape or Hq % Hkv or \
+            page_min.stride() != page_max.stride() or page_min.dtype != page_max.dtype:
+        raise ValueError("page_min/max must be (B, Hkv, P, D) twins with Hq a multiple of Hkv")
+    if positions is not None and (positions.dtype != torch.int32 or positions.shape != (B,)
+                                  or not positions.is_contiguous()):
+        raise ValueError("positions must be contiguous int32 (B,)")
+    G = Hq // Hkv
+    k = max(1, min(int(topk), P))
+    ids = torch.empty(B, Hkv, 1, G * k, dtype=torch.int32, device=dev)
+    counts = torch.empty(B, Hkv, 1, dtype=torch.int32, device=dev)
+    out = torch.empty(B, Hq, 1, D, dtype=out_dtype or q.dtype, device=dev)
+    a = N.LaQuestDecodeArgs()
+    s = a.select
+    s.q, s.page_min, s.page_max = q.data_ptr(), page_min.data_ptr(), page_max.data_ptr()
+    s.out_idx, s.out_count = ids.data_ptr(), counts.data_ptr()
+    s.B, s.Hq, s.Hkv, s.Tq, s.D = B, Hq, Hkv, 1, D
+    s.q_sb, s.q_sh, s.q_st = q.stride(0), q.stride(1), q.stride(2)
+    s.n_pages = P
+    s.m_sb, s.m_sh, s.m_sp, s.m_sd = page_min.stride()
+    s.page_size, s.pos_offset, s.k = page_size, (pos if pos is not None else 0), k
+    s.q_dtype, s.meta_dtype = N.dtype_code(q.dtype), N.dtype_code(page_min.dtype)
+    s.positions = N.ptr(positions)
+    T = page_table.shape[1] * page_size
+    a.kv = _kv_struct(k_pool, v_pool, page_table=page_table, page_size=page_size, kv_len=kv_len,
+                      k_scale=None, v_scale=None, T=T, D=D, Hkv=Hkv)
+    a.out = out.data_ptr()
+    a.o_sb, a.o_sh, a.o_st = out.stride(0), out.stride(1), out.stride(2)
+    a.scale = float(scale if scale is not None else 1.0 / math.sqrt(D))
+    a.out_dtype = N.dtype_code(out.dtype)
+    rc = N.load().la_quest_decode_fused(ctypes.byref(a), N.stream_handle(dev))
+    if rc == N.LA_ERR_UNSUPPORTED:
+        raise NotImplementedError((N.load().la_last_error() or b"").decode(errors="replace"))
+    N.check(rc, "quest_decode_fused")
     return out, ids, counts

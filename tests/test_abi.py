@@ -28,6 +28,7 @@ STRUCTS = {
     "la_gate_select_args": N.LaGateSelectArgs,
     "la_block_means_args": N.LaBlockMeansArgs,
     "la_xattn_select_args": N.LaXattnSelectArgs,
+    "la_quest_decode_args": N.LaQuestDecodeArgs,
 }
 
 
