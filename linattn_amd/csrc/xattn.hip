@@ -453,6 +453,182 @@ __global__ __launch_bounds__(TK_NT) void xattn_select_kernel(XaKP p) {
                      sh.wtmp[1]);
 }
 
+// 64-bit lane exchanges within a wave (no LDS, no barrier): DPP moves within
+// rows of 16 lanes, then the 16- and 32-lane swaps, on the two 32-bit halves.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)x, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(x >> 32), CTRL, 0xf, 0xf, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+// (the value of lane l, the value of lane l ^ 16 or l ^ 32), lower lane first
+template <bool P32>
+__device__ __forceinline__ void swap_u64(uint64_t x, uint64_t &a, uint64_t &b) {
+  const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+  const auto l = P32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                     : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto h = P32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                     : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  a = ((uint64_t)h[0] << 32) | l[0];
+  b = ((uint64_t)h[1] << 32) | l[1];
+}
+// Sum (MAX = false) or maximum over the wave, in every lane.
+template <bool MAX>
+__device__ __forceinline__ uint64_t wave_red_u64(uint64_t x) {
+  auto op = [](uint64_t a, uint64_t b) { return MAX ? (a > b ? a : b) : a + b; };
+  x = op(x, dpp_u64<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = op(x, dpp_u64<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = op(x, dpp_u64<0x141>(x));  // row_half_mirror
+  x = op(x, dpp_u64<0x140>(x));  // row_mirror
+  uint64_t a, b;
+  swap_u64<false>(x, a, b);
+  x = op(a, b);
+  swap_u64<true>(x, a, b);
+  return op(a, b);
+}
+
+// The selection of xattn_select_kernel for rows whose slot scores are already
+// in the workspace (stride == block) and that have at most 64 * KPL key
+// blocks: one wave per row, block kb = lane + 64 j in slot j of the lane's
+// registers, every reduction a lane exchange -- the ~40 steps of the
+// threshold search take no barrier.  The arithmetic (row maximum, masses,
+// the threshold and tie rules, top-k by (mass desc, block asc), the own
+// block) is the block kernel's, so the lists are identical.
+template <int KPL>
+__global__ __launch_bounds__(256) void xattn_select_wave_kernel(XaKP p, int64_t n_rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, h, qb)
+  if (row >= n_rows) return;  // wave-uniform; the kernel has no barrier
+  const int64_t qb = row % p.n_qb;
+  const int64_t h = (row / p.n_qb) % p.Hq;
+  const int64_t n_kb = p.n_kb, NS = p.n_slots, blk = p.blk;
+  const int64_t pos0 = qb * blk + p.offset;
+  const int64_t lim = min(pos0 / blk, n_kb - 1);
+  const int64_t n_vis = lim + 1;
+  const double *src = p.slots + row * n_kb * NS;
+  const uint64_t lt = lanemask_lt(lane);
+
+  double mx = __int_as_float(0xff800000);
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const int64_t kb = lane + 64 * j;
+    if (kb < n_vis)
+      for (int64_t s = 0; s < NS; ++s) mx = fmax(mx, src[kb * NS + s]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmax(mx, __shfl_xor(mx, off, 64));
+
+  uint64_t u[KPL];
+  uint64_t zpart = 0, umax = 0;
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const int64_t kb = lane + 64 * j;
+    uint64_t m = 0;
+    if (kb < n_vis)
+      for (int64_t s = 0; s < NS; ++s) m += (uint64_t)__builtin_rint(exp_det(src[kb * NS + s] - mx) * p.two_f);
+    u[j] = m;
+    zpart += m;
+    umax = m > umax ? m : umax;
+  }
+  const uint64_t Z = wave_red_u64<false>(zpart);
+  const uint64_t top = wave_red_u64<true>(umax);
+
+  uint32_t kbits = 0;  // bit j: block lane + 64 j is kept
+  // Slots j >= jn hold only blocks past the visible ones (mass 0, never
+  // kept): the searches skip them.  They add nothing to the sums, and as
+  // ties at 0 they would rank after every visible block.
+  const int jn = (int)min((int64_t)KPL, (n_vis + 63) / 64);
+  auto listed = [&](int j) { return j < jn && lane + 64 * (int64_t)j < n_kb; };
+  bool by_count = p.mode == 1;
+  uint32_t K = (uint32_t)min(p.topk, n_kb);
+  if (p.mode == 0) {
+    const double thr_d = p.alpha[h] * (double)Z;
+    if (thr_d > (double)Z) {  // every block
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) kbits |= listed(j) ? 1u << j : 0u;
+    } else if (!(thr_d > 0.0)) {  // C_m < thr for no m: the top block alone
+      by_count = true;
+      K = 1;
+    } else {
+      const uint64_t thr = (uint64_t)ceil(thr_d);
+      // largest v with sum(mass >= v) >= thr (v = 0 qualifies: the sum is Z)
+      uint64_t v = 0;
+      for (int bit = top ? 63 - __clzll((long long)top) : -1; bit >= 0; --bit) {
+        const uint64_t v2 = v | (1ull << bit);
+        uint64_t part = 0;
+#pragma unroll
+        for (int j = 0; j < KPL; ++j)
+          if (j < jn) part += u[j] >= v2 ? u[j] : 0ull;
+        if (wave_red_u64<false>(part) >= thr) v = v2;
+      }
+      uint64_t gpart = 0;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j)
+        if (j < jn) gpart += u[j] > v ? u[j] : 0ull;
+      const uint64_t s_gt = wave_red_u64<false>(gpart);
+      const uint64_t n_eq_take = v ? (thr - s_gt - 1) / v + 1 : 0;
+      // ties at v taken in block order (slot j, then lane: ascending kb)
+      uint64_t eq_before = 0;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        if (j >= jn) break;
+        const bool eq = listed(j) && u[j] == v;
+        const uint64_t bm = __ballot(eq);
+        const uint64_t rank = eq_before + (uint64_t)__popcll(bm & lt);
+        if (listed(j) && (u[j] > v || (eq && rank < n_eq_take))) kbits |= 1u << j;
+        eq_before += (uint64_t)__popcll(bm);
+      }
+    }
+  }
+  if (by_count) {  // the K largest masses over the listed blocks, ties to the lower block
+    uint64_t T = 0;
+    for (int bit = top ? 63 - __clzll((long long)top) : -1; bit >= 0; --bit) {
+      const uint64_t T2 = T | (1ull << bit);
+      uint32_t c = 0;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j)
+        if (j < jn) c += (uint32_t)__popcll(__ballot(listed(j) && u[j] >= T2));
+      if (c >= K) T = T2;
+    }
+    uint32_t gt = 0;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j)
+      if (j < jn) gt += (uint32_t)__popcll(__ballot(listed(j) && u[j] > T));
+    const uint32_t need = K - gt;
+    uint32_t eq_before = 0;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      if (j >= jn) break;
+      const bool eq = listed(j) && u[j] == T;
+      const uint64_t bm = __ballot(eq);
+      const uint32_t rank = eq_before + (uint32_t)__popcll(bm & lt);
+      if (listed(j) && (u[j] > T || (eq && rank < need))) kbits |= 1u << j;
+      eq_before += (uint32_t)__popcll(bm);
+    }
+  }
+  // only visible blocks are kept, and the own block (selection.py:591)
+  const int64_t own = (pos0 % blk == 0 && pos0 / blk < n_kb) ? pos0 / blk : -1;
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const int64_t kb = lane + 64 * j;
+    if (kb > lim) kbits &= ~(1u << j);
+    if (kb == own) kbits |= 1u << j;
+  }
+  // ascending list, -1 padded, count
+  int32_t *out = p.out_idx + row * p.width;
+  uint32_t total = 0;
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const bool k = (kbits >> j) & 1u;
+    const uint64_t bm = __ballot(k);
+    const uint32_t pos = total + (uint32_t)__popcll(bm & lt);
+    if (k && pos < (uint32_t)p.width) out[pos] = (int32_t)(lane + 64 * j);
+    total += (uint32_t)__popcll(bm);
+  }
+  for (int64_t jj = (int64_t)total + lane; jj < p.width; jj += 64) out[jj] = -1;
+  if (lane == 0) p.out_count[row] = (int32_t)min((int64_t)total, p.width);
+}
+
 }  // namespace la
 
 using namespace la;
@@ -544,6 +720,17 @@ extern "C" int la_xattn_select(const la_xattn_select_args *a, void *stream) {
     else
       xattn_slots_mfma_kernel<false><<<grid, XM_NT, 0, st>>>(p);
     LA_LAUNCHED();
+  }
+  if (p.slots && n_kb <= 1024) {  // one wave per row over the scored slots
+    const unsigned grid = (unsigned)ceil_div(nwg, 4);
+    if (n_kb <= 64)
+      xattn_select_wave_kernel<1><<<grid, 256, 0, st>>>(p, nwg);
+    else if (n_kb <= 256)
+      xattn_select_wave_kernel<4><<<grid, 256, 0, st>>>(p, nwg);
+    else
+      xattn_select_wave_kernel<16><<<grid, 256, 0, st>>>(p, nwg);
+    LA_LAUNCHED();
+    return LA_OK;
   }
   const int kpt = (int)ceil_div(n_kb, TK_NT);
   auto launch = [&](auto kern) -> int {

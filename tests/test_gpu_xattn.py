@@ -66,6 +66,27 @@ def test_xattn_select_topk_and_offset(dev, t, tq, block, topk):
     check_lists(ids, counts, ref_ids, ref_counts)
 
 
+@pytest.mark.parametrize("t,tq,block,threshold,topk", [
+    (1000, 1000, 8, [0.0, 1.5], None),   # 125 key blocks: 4 per lane; the top block alone / every block
+    (1000, 1000, 8, 0.8, 7),             # top-k, 4 per lane
+    (4000, 128, 8, 0.9, 30),             # top-k at an offset, 500 blocks: 16 per lane
+    (8000, 64, 8, [0.9, 0.6], None),     # threshold at an offset, 1000 blocks
+    (500, 500, 4, 0.95, None),           # block = stride = 4
+    (64 * 8, 64 * 8, 8, 0.7, None),      # exactly 64 key blocks: one per lane
+])
+def test_xattn_select_one_wave_rows(dev, t, tq, block, threshold, topk):
+    """The one-wave-per-row selection (slots on the matrix cores, at most
+    1024 key blocks) against the oracle, every branch of the threshold rule
+    and the top-k rule at 1, 4 and 16 blocks per lane."""
+    q, k, _ = inputs(1, 2, 1, tq, t, 64, seed=33, dtype=torch.bfloat16)
+    kw = dict(block=block, stride=block, offset=t - tq, threshold=threshold)
+    if topk is not None:
+        kw["topk"] = topk
+    ids, counts = xattn_select_hip(q.to(dev), k.to(dev), **kw)
+    ref_ids, ref_counts = oracle.xattn_select(q, k, **kw)
+    check_lists(ids, counts, ref_ids, ref_counts)
+
+
 def test_xattn_slots_summation_order(dev):
     """Slot entries are fp64 sums over d in increasing order (the matrix-core
     scorer for stride == block relies on the in-order fp64 accumulation).
