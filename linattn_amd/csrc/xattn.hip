@@ -142,7 +142,9 @@ __device__ __forceinline__ void xm_widen8(const uint4 &v, float (&x)[8]) {
 }
 
 template <bool BF>
-__global__ __launch_bounds__(XM_NT, 2) void xattn_slots_mfma_kernel(XaKP p) {
+// Three workgroups per CU (168 VGPRs; the few spills are outside the
+// product loop): 5 % faster than two at 178 VGPRs without spills.
+__global__ __launch_bounds__(XM_NT, 3) void xattn_slots_mfma_kernel(XaKP p) {
   typedef double f64x4 __attribute__((ext_vector_type(4)));
   __shared__ __align__(16) float sq[XM_T][XM_S];
   __shared__ __align__(16) float sk[XM_T][XM_S];
