@@ -370,6 +370,12 @@ __device__ __forceinline__ u32x4 load16_async(const void *ptr) {
   asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(ptr));
   return v;
 }
+// the same load through the caches (for data many waves re-read)
+__device__ __forceinline__ u32x4 load16_async_cached(const void *ptr) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr));
+  return v;
+}
 
 // Wait until at most N loads are outstanding; the chunks are operands so
 // that no use of them is moved above the wait.
@@ -429,14 +435,19 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
   __syncthreads();
   if (nw == 0) return;  // whole wave; no barrier follows
   // chunk i of lane l in the coalesced load of a wave tile: c = i*64 + l of
-  // the tile's KW x cpr chunks (past the end: the tile's last chunk again)
-  auto fetch = [&](u32x4 (&v)[CH], int k) {  // k-th tile of this wave (clamped)
-    const int64_t key0 = (wt0 + w + 4 * (int64_t)min(k, nw - 1)) * KW;
+  // the tile's KW x cpr chunks (past the end: the tile's last chunk again).
+  // The loads past the wave's last tile (issued so that every step waits for
+  // the same count) read the sequence's first tile through the caches, where
+  // every wave's tail finds it, instead of streaming a tile from HBM again.
+  auto fetch = [&](u32x4 (&v)[CH], int k) {  // k-th tile of this wave
+    const bool tail = k >= nw;  // (wave-uniform)
+    const int64_t key0 = tail ? 0 : (wt0 + w + 4 * (int64_t)k) * KW;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = min(i * 64 + lane, KW * cpr - 1);
       const int64_t s = min(key0 + c / cpr, p.Tk - 1);
-      v[i] = load16_async(kb + s * p.k_st + (c % cpr) * 8);
+      const uint16_t *src = kb + s * p.k_st + (c % cpr) * 8;
+      v[i] = tail ? load16_async_cached(src) : load16_async(src);
     }
   };
   auto stage = [&](const u32x4 (&v)[CH]) {
