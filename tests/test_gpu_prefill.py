@@ -90,6 +90,39 @@ def test_prefill_full_selection_is_dense_causal(dev):
     assert np.abs(out_b.cpu().double().numpy() - ref).max() < 1.6e-2  # bf16 output rounding
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_multiset_lists_with_holes(dev, causal):
+    """Hand-made lists: unsorted, one block listed twice (attended twice, as
+    the reference's gather does, block_sparse.py:62-68), -1 holes between
+    entries, a partial last key block (T = 300), and future blocks (read whole
+    without the causal mask, cut by it with the mask; the diagonal block is
+    always listed so every row sees its own token)."""
+    T, hq, hkv = 300, 4, 2
+    q, k, v = c3_inputs(1, hq, hkv, T, 128, seed=7)
+    nqb, W = 5, 7
+    g = np.random.default_rng(7)
+    ids = np.full((1, hq, nqb, W), -1, dtype=np.int32)
+    for h in range(hq):
+        for qb in range(nqb):
+            picks = list(g.choice(nqb, size=3, replace=False))
+            lst = [qb, picks[0], picks[1], picks[0], -1, picks[2], -1]
+            g.shuffle(lst)
+            ids[0, h, qb] = lst
+    out = block_sparse_prefill(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(ids).to(dev),
+                               causal=causal, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    G = hq // hkv
+    for h in range(hq):
+        for qb in range(nqb):
+            t0, t1 = qb * 64, min(T, (qb + 1) * 64)
+            rows = np.broadcast_to(ids[0, h, qb], (1, 1, t1 - t0, W))
+            ref = oracle.attend_lists(q[:, h:h + 1, t0:t1], k[:, h // G:h // G + 1],
+                                      v[:, h // G:h // G + 1], rows, unit=64, causal=causal,
+                                      offset=t0)
+            got = out[0, h, t0:t1].cpu().double().numpy()
+            assert np.abs(got - ref[0, 0]).max() < 2e-3, (h, qb)
+
+
 def test_prefill_empty_list_gives_zeros(dev):
     q, k, v = c3_inputs(1, 1, 1, 128, 128, seed=4, outliers=False)
     ids = torch.full((1, 1, 2, 3), -1, dtype=torch.int32)
