@@ -48,7 +48,8 @@ enum {
 /* device status bits (la_device_status) */
 enum {
   LA_DEV_TOPK_TIMEOUT = 1,  /* a bounded wait of the multi-workgroup top-k ran out */
-  LA_DEV_PREFILL_RANGE = 2  /* la_block_sparse_prefill met a finite |v| >= 2^22 (outputs inf) */
+  LA_DEV_PREFILL_RANGE = 2  /* la_block_sparse_prefill met a finite |v| >= 2^22 (outputs inf;
+                              the Python wrapper raises ValueError) */
 };
 
 /* ABI version of the loaded library (LA_ABI_VERSION). */
@@ -56,7 +57,9 @@ int la_abi_version(void);
 
 /*
  * Status bits the kernels raised on the current device since the last clear
- * (LA_DEV_*), after the given stream has drained; clear != 0 resets them.
+ * (LA_DEV_*), after the work queued on the given stream; clear != 0 resets
+ * them in the same atomic exchange (a bit raised meanwhile by another stream's
+ * kernel is kept for the next read).
  * Kernels report failures they detect on the device here instead of through a
  * return code (a launch returns before the kernel runs): a row of
  * la_topk_rows / la_indexer_topk whose multi-workgroup selection timed out

@@ -19,7 +19,7 @@ int fail(int code, const char *fmt, ...);
 int num_cus();
 // Status bits of prefill.hip's kernels on the current device (read after the
 // caller synchronised), optionally cleared.
-int prefill_status(uint32_t *bits, bool clear);
+int prefill_status(uint32_t *bits, bool clear, hipStream_t st);
 
 #define LA_REQUIRE(cond, ...)                               \
   do {                                                      \

@@ -11,13 +11,17 @@
 // which exceeds 2e-3 on rows whose mass sits on a few keys), and the row sum is
 // taken from the same rounded weights, so a rounding shared by every weight
 // cancels in the division.  V is therefore converted once to fp16 by
-// prefill_v16_kernel, each 64-token block scaled by a power of two 2^-e
-// (e = 0 unless the block's largest |v| reaches 2^15; e <= 7, so |v| < 2^22),
-// which keeps every bf16 value of magnitude >= 2^(e-17) exact.  The kernel
-// folds 2^e into the weights of that block (exp2(x + e): at most 2^15, still
-// an fp16) and weighs them by 2^-e in the row sum.  Blocks with |v| >= 2^22
-// raise LA_DEV_PREFILL_RANGE in the device status word (their fp16 copy
-// overflows to inf).
+// prefill_v16_kernel, each 64-token block scaled by a power of two 2^-e:
+// e = 0 while the block's largest |v| lies in [1, 2^15); above, e > 0 (at most
+// 7, so |v| < 2^22) brings it below 2^15; below 1, e < 0 (at least -8) scales
+// small blocks up to [1, 2), so their values stay normal fp16 down to 2^-22.
+// Every bf16 value of magnitude >= 2^(e-17) is then exact.  The kernel folds
+// 2^e into the weights of that block (exp2(x + e): at most 2^(8+e) <= 2^15,
+// still an fp16; e < 0 only where the block's values are small, since it
+// moves weights of the block towards the fp16 subnormals) and weighs them by
+// 2^-e in the row sum.  Blocks with |v| >= 2^22 raise LA_DEV_PREFILL_RANGE in
+// the device status word (their fp16 copy overflows to inf), which
+// block_sparse_prefill turns into an error.
 //
 // Per workgroup: 4 waves = 2 query halves (32 queries) x 2 key halves (32 of
 // every 64-key block).  Each listed key block's K and V (64 x 128, bf16) are
@@ -118,8 +122,9 @@ __device__ uint32_t la_pf_status;
 
 // V (bf16 at any strides with a unit stride over D, or fp8 e4m3 codes with
 // per-token fp32 scales) -> fp16, one workgroup per 64-token block of one
-// (b, KV head): e = min(7, max(0, E - 141)) for the block's largest |v| with
-// biased exponent E (so |v| * 2^-e < 2^15 when E <= 148), then
+// (b, KV head): for the block's largest |v| with biased exponent E,
+// e = min(7, E - 141) when E > 141 (so |v| * 2^-e < 2^15 when E <= 148),
+// e = max(-8, E - 127) when E < 127 (|v| < 1), and 0 otherwise; then
 // v16 = fp16(v * 2^-e), rounded to nearest even (fp8: v = code * scale in
 // fp32, the product rounded once).  Rows past T (T_b) are not written.
 template <bool F8>
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(256) void prefill_v16_kernel(const void *v, const f
   __syncthreads();
   mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
   const int E = (int)(mx >> 23);
-  const int e = min(7, max(0, E - 141));
+  const int e = E > 141 ? min(7, E - 141) : E < 127 ? max(-8, E - 127) : 0;
   if (tid == 0) {
     vexp[blk] = e;
     if (E > 148 && mx < 0x7f800000u)  // finite |v| >= 2^22 (inf and NaN pass through)
@@ -648,11 +653,12 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       sn[1][kt2] = s1;
     }
     // P = 2^ev * exp2(s*qscale - m*qscale) in fp16 (round to nearest even; at
-    // most 2^(8+ev) <= 2^15); l sums the rounded weights times 2^-ev (exact).
+    // most 2^(8+ev) <= 2^15); l sums the rounded weights times 2^-ev (exact:
+    // 2^-ev, -8 <= ev <= 7, is a normal fp16).
     // Column c16 is this lane's query; the positive scale commutes with the
     // max, so it is applied in the exponent.
     const float evf = (float)ev;
-    // 2^-ev as an fp16 pair (0 <= ev <= 7: biased exponent 15 - ev)
+    // 2^-ev as an fp16 pair (-8 <= ev <= 7: biased exponent 15 - ev in [8, 23])
     const uint32_t wbits = (uint32_t)(15 - ev) << 10;
     const f16x2 wl2 = __builtin_bit_cast(f16x2, wbits | (wbits << 16));
     f16x8 ph[2];
@@ -834,14 +840,23 @@ using namespace la;
 
 namespace la {
 
-int prefill_status(uint32_t *bits, bool clear) {
-  LA_HIP(hipMemcpyFromSymbol(bits, HIP_SYMBOL(la_pf_status), sizeof(uint32_t), 0,
-                             hipMemcpyDeviceToHost));
-  if (clear) {
-    const uint32_t zero = 0;
-    LA_HIP(hipMemcpyToSymbol(HIP_SYMBOL(la_pf_status), &zero, sizeof(uint32_t), 0,
-                             hipMemcpyHostToDevice));
-  }
+// The status word read (and, with clear, reset) in one atomic exchange on the
+// caller's stream, so a bit raised by a kernel of another stream is never lost
+// between a read and a clear.
+__device__ uint32_t la_pf_status_snap;
+__global__ void pf_status_kernel(int clear) {
+  la_pf_status_snap = clear ? __hip_atomic_exchange(&la_pf_status, 0u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT)
+                            : __hip_atomic_load(&la_pf_status, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int prefill_status(uint32_t *bits, bool clear, hipStream_t st) {
+  pf_status_kernel<<<1, 1, 0, st>>>(clear ? 1 : 0);
+  LA_LAUNCHED();
+  LA_HIP(hipMemcpyFromSymbolAsync(bits, HIP_SYMBOL(la_pf_status_snap), sizeof(uint32_t), 0,
+                                  hipMemcpyDeviceToHost, st));
+  LA_HIP(hipStreamSynchronize(st));
   return LA_OK;
 }
 

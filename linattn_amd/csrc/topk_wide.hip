@@ -429,19 +429,28 @@ int topk_wide_launch(const TopkKParams &p, const WidePlan &W, void *ws, hipStrea
 
 using namespace la;
 
+// The status word read (and, with clear, reset) in one atomic exchange on the
+// caller's stream, after the work queued on it: a bit raised by a kernel of
+// another stream is either in this read or kept for the next one.
+__device__ uint32_t la_dev_status_snap;
+__global__ void dev_status_kernel(int clear) {
+  la_dev_status_snap = clear ? __hip_atomic_exchange(&la_dev_status, 0u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)
+                             : __hip_atomic_load(&la_dev_status, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+}
+
 extern "C" int la_device_status(uint32_t *bits, int32_t clear, void *stream) {
   LA_REQUIRE(bits != nullptr, "la_device_status: null pointer");
-  LA_HIP(hipStreamSynchronize((hipStream_t)stream));
-  LA_HIP(hipMemcpyFromSymbol(bits, HIP_SYMBOL(la_dev_status), sizeof(uint32_t), 0,
-                             hipMemcpyDeviceToHost));
-  if (clear) {
-    const uint32_t zero = 0;
-    LA_HIP(hipMemcpyToSymbol(HIP_SYMBOL(la_dev_status), &zero, sizeof(uint32_t), 0,
-                             hipMemcpyHostToDevice));
-  }
+  hipStream_t st = (hipStream_t)stream;
+  dev_status_kernel<<<1, 1, 0, st>>>(clear ? 1 : 0);
+  LA_LAUNCHED();
+  LA_HIP(hipMemcpyFromSymbolAsync(bits, HIP_SYMBOL(la_dev_status_snap), sizeof(uint32_t), 0,
+                                  hipMemcpyDeviceToHost, st));
+  LA_HIP(hipStreamSynchronize(st));
   // status words of the other source files (each holds its own device symbol)
   uint32_t more = 0;
-  const int rc = prefill_status(&more, clear != 0);
+  const int rc = prefill_status(&more, clear != 0, st);
   if (rc != LA_OK) return rc;
   *bits |= more;
   return LA_OK;

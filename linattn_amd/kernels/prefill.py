@@ -84,7 +84,8 @@ def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids:
                          out_dtype: Optional[torch.dtype] = None,
                          lengths: Optional[torch.Tensor] = None,
                          k_scale: Optional[torch.Tensor] = None,
-                         v_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+                         v_scale: Optional[torch.Tensor] = None,
+                         check_range: bool = True) -> torch.Tensor:
     """Attention of every 64-query block over its listed 64-key blocks.
 
     q (B, Hq, T, 128) bf16; k/v (B, Hkv, T, 128) bf16, or float8_e4m3fn codes
@@ -93,7 +94,13 @@ def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids:
     (B, Hq, n_qb, W) (-1 entries read nothing); counts optional (B, Hq, n_qb).
     Returns (B, Hq, T, 128) in ``out_dtype`` (default q.dtype).  ``lengths``
     (int32 (B,), optional): a ragged batch; rows of sequence b at or past
-    lengths[b] are never read and come out as zeros."""
+    lengths[b] are never read and come out as zeros.
+
+    The weights multiply an fp16 copy of V scaled by a power of two per
+    64-token block, which holds |v| < 2^22; a finite |v| >= 2^22 raises
+    ValueError after the call (``check_range``, default True: one read of the
+    device status word, a host synchronisation; with False the rows reading
+    such a block come out inf and the device status word records it)."""
     dev = N.require_gpu(q, k, v, ids, counts, lengths, k_scale, v_scale,
                         what="block_sparse_prefill")
     B, Hq, T, D = q.shape
@@ -144,6 +151,10 @@ def block_sparse_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids:
     a.workspace, a.ws_bytes = N.ptr(ws), ws_bytes
     N.check(L.la_block_sparse_prefill(ctypes.byref(a), N.stream_handle(dev)),
             "block_sparse_prefill")
+    if check_range and N.device_status(dev, clear=False) & N.LA_DEV_PREFILL_RANGE:
+        N.device_status(dev, clear=True)
+        raise ValueError("block_sparse_prefill: v holds a finite value with |v| >= 2^22 "
+                         "(beyond the fp16 range of the weighted V product)")
     return out
 
 

@@ -144,7 +144,8 @@ def _alphas(threshold, Hq: int, dev: torch.device) -> torch.Tensor:
 
 def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride: int = 8,
                      threshold: Union[float, Sequence[float]] = 0.9, offset: int = 0,
-                     topk: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                     topk: Optional[int] = None,
+                     top_ratio: Optional[float] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """XAttention's block selection (XAttention.antidiagonal_scores / select,
     selection.py:528-595) for every (b, query head, query block).
 
@@ -155,7 +156,12 @@ def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride
     reference's ``threshold_per_head``) keeps the minimal prefix of blocks,
     by mass, whose cumulative mass reaches it (_cumulative_select,
     selection.py:62-69); with ``topk`` the top-k blocks by mass are kept
-    instead (select_mode "topk").  The own block is OR'd in and blocks past
+    instead (select_mode "topk").  With ``top_ratio`` (select_mode
+    "top_ratio", selection.py:583-585) the cumulative mass is compared with
+    the block count max(1, ceil(n_visible * ratio)) >= 1 (:598-606); the
+    masses of a row are positive and sum to 1, so that count is reached only
+    once every visible block is in: every visible block is kept, and no
+    score is computed.  The own block is OR'd in and blocks past
     causality dropped.  Masses are exact integers of fixed-point weights from
     a deterministic exp, so ties and the threshold crossing are a fixed
     function of the inputs (ties to the lowest block).
@@ -179,6 +185,16 @@ def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride
     if topk is not None and topk < 1:
         raise ValueError("topk >= 1 required")
     n_qb, n_kb = -(-Tq // block), -(-T // block)
+    if top_ratio is not None:
+        if not top_ratio > 0:
+            raise ValueError("top_ratio > 0 required")
+        # visible key blocks of query block i: kb * block <= offset + i * block
+        last = torch.clamp((offset + torch.arange(n_qb, device=dev) * block) // block, max=n_kb - 1)
+        kb = torch.arange(n_kb, device=dev)
+        ids = torch.where(kb[None, :] <= last[:, None], kb[None, :], -1).to(torch.int32)
+        ids = ids.expand(B, Hq, n_qb, n_kb).contiguous()
+        counts = (last + 1).to(torch.int32).expand(B, Hq, n_qb).contiguous()
+        return ids, counts
     width = min(topk, n_kb) + 1 if topk is not None else n_kb
     ids = torch.empty(B, Hq, n_qb, width, dtype=torch.int32, device=dev)
     counts = torch.empty(B, Hq, n_qb, dtype=torch.int32, device=dev)

@@ -370,10 +370,12 @@ class HipXAttention(HipAttention):
 
     extras: ``xattn_block`` (default 8), ``antidiagonal_stride`` (default
     ``cfg.stride``), ``select_mode`` ("threshold", default, or "topk" with
-    ``cfg.topk_blocks``), ``threshold_per_head``.  The reference's
-    "top_ratio" mode compares the cumulative probability mass against a block
-    count (selection.py:583-585 with :598-606), which keeps every block; it
-    is not offered.  64-token blocks over a whole bf16 prefill (offset 0,
+    ``cfg.topk_blocks``, or "top_ratio" with ``top_ratio``, default 0.02),
+    ``threshold_per_head``.  The reference's "top_ratio" mode compares the
+    cumulative probability mass (at most 1) against a block count of at
+    least 1 (selection.py:583-585 with :598-606), which is reached only when
+    every visible block is in: it reads every visible block, as here.
+    64-token blocks over a whole bf16 prefill (offset 0,
     head_dim 128) run the MFMA prefill kernel; otherwise every query row reads
     its block's list through ``sparse_attention``."""
 
@@ -385,9 +387,9 @@ class HipXAttention(HipAttention):
         self.block = int(ex.get("xattn_block", 8))
         self.r = int(ex.get("antidiagonal_stride", self.cfg.stride))
         self.select_mode = ex.get("select_mode", "threshold")
-        if self.select_mode not in ("threshold", "topk"):
+        if self.select_mode not in ("threshold", "topk", "top_ratio"):
             raise ValueError(f"hip_xattention: select_mode {self.select_mode!r} not supported "
-                             "(threshold or topk)")
+                             "(threshold, topk or top_ratio)")
 
     def attend(self, q, state, offset: int = 0):
         k, v = state["k"], state["v"]
@@ -395,6 +397,9 @@ class HipXAttention(HipAttention):
         if self.select_mode == "topk":
             ids, counts = xattn_select_hip(q, k, block=blk, stride=self.r, offset=offset,
                                            topk=self.cfg.topk_blocks)
+        elif self.select_mode == "top_ratio":
+            ids, counts = xattn_select_hip(q, k, block=blk, stride=self.r, offset=offset,
+                                           top_ratio=float(self.cfg.extras.get("top_ratio", 0.02)))
         else:
             th = self.cfg.extras.get("threshold_per_head", self.cfg.threshold)
             ids, counts = xattn_select_hip(q, k, block=blk, stride=self.r, threshold=th,

@@ -568,7 +568,7 @@ def gate_select(q, k, *, block: int, topk: int, offset: int = 0) -> np.ndarray:
 
 # ------------------------------------------------------------- XAttention --
 def xattn_select(q, k, *, block: int = 8, stride: int = 8, threshold=0.9, offset: int = 0,
-                 topk: Optional[int] = None):
+                 topk: Optional[int] = None, top_ratio: Optional[float] = None):
     """XAttention's block selection (selection.py:528-595) per (b, query
     head, query block), in the integer-mass form the kernel computes
     (la_oracle.c or_xattn_select): antidiagonal slot scores in fp64, weights
@@ -576,12 +576,31 @@ def xattn_select(q, k, *, block: int = 8, stride: int = 8, threshold=0.9, offset
     cumulative threshold (``threshold`` a float or one value per query head)
     or, with ``topk``, the top-k blocks; own block OR'd, invisible blocks
     dropped.  Returns (ids (B, Hq, n_qb, width) ascending, -1 padded,
-    counts (B, Hq, n_qb)); width = n_kb, or min(topk, n_kb) + 1."""
+    counts (B, Hq, n_qb)); width = n_kb, or min(topk, n_kb) + 1.
+
+    ``top_ratio`` (select_mode "top_ratio", selection.py:583-585): the
+    reference keeps the shortest prefix of blocks, by mass, whose cumulative
+    mass reaches the count c = max(1, ceil(n_visible * ratio)) (the
+    _select_with_per_head rule, :598-606, with c in place of a threshold),
+    or every block when none does.  A row's masses are a softmax over its
+    visible blocks: each is positive and they sum to 1 <= c, so the prefix
+    reaches c only when it holds every visible block, and either way every
+    visible block is kept (width n_kb)."""
     q, k = to_f64(q), to_f64(k)
     B, Hq, Tq, D = q.shape
     Hkv, T = k.shape[1], k.shape[2]
     G = Hq // Hkv
     n_qb, n_kb = -(-Tq // block), -(-T // block)
+    if top_ratio is not None:
+        ids = np.full((B, Hq, n_qb, n_kb), -1, dtype=np.int32)
+        counts = np.zeros((B, Hq, n_qb), dtype=np.int32)
+        for i in range(n_qb):
+            n_vis = min(n_kb, (offset + i * block) // block + 1)
+            c = max(1, math.ceil(n_vis * top_ratio))
+            assert c >= 1  # the cumulative mass (a sum of positive masses, total 1) reaches c last
+            ids[:, :, i, :n_vis] = np.arange(n_vis, dtype=np.int32)
+            counts[:, :, i] = n_vis
+        return ids, counts
     mode = 1 if topk is not None else 0
     width = min(topk, n_kb) + 1 if mode else n_kb
     alphas = np.broadcast_to(np.asarray(threshold, dtype=np.float64), (Hq,))

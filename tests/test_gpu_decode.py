@@ -10,6 +10,8 @@ torch.Generator draws q, k, v in that order from N(0, 1).
 from __future__ import annotations
 
 import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 import numpy as np
@@ -372,8 +374,9 @@ def test_config4_paged_quest_decode_full_size(dev, union):
     permuted page table, 2048-token budget with the last page forced.
     Every list is checked by properties on the GPU (own page present, sorted
     and unique, selected scores dominate unselected ones with the index tie
-    rule), and every one of the 64 sequences against the oracle: page ids bit
-    for bit, outputs within 2e-3."""
+    rule), and every one of the 64 sequences against the oracle: the page
+    bounds of all 8 KV heads and the page ids bit for bit (the oracle selects
+    from its own bounds), outputs within 2e-3."""
     B, Hq, Hkv, T, D, ps, topk = 64, 32, 8, 65536, 128, 64, 32
     P = T // ps
     g = torch.Generator(device=dev).manual_seed(0)
@@ -412,19 +415,30 @@ def test_config4_paged_quest_decode_full_size(dev, union):
         got = torch.zeros(B, Hq, P, dtype=torch.bool, device=dev)
         got.scatter_(-1, ids.squeeze(2).long(), True)
         assert torch.equal(got, want)
-    # the page bounds of two sequences against the oracle (two KV heads each)
-    for b in (0, 37):
-        kb = pool_k[pt[b].long(), :2].permute(1, 0, 2, 3).reshape(1, 2, T, D).cpu()
+    # the page bounds of every sequence and KV head against the oracle's, and
+    # the oracle's selection from the oracle's own bounds (one sequence per
+    # thread: each gathers its 1024 pages and takes their channel min/max)
+    mins_h, maxs_h, q_h = mins.cpu(), maxs.cpu(), q.cpu()
+    pool_h = pool_k.cpu()
+    pt_h = pt.cpu().long()
+
+    def oracle_bounds(b):
+        kb = pool_h[pt_h[b]].permute(1, 0, 2, 3).reshape(1, Hkv, T, D)
         om, ox = oracle.page_bounds(kb, ps)
-        assert np.array_equal(oracle.to_f64(mins[b:b + 1, :2].cpu()), om)
-        assert np.array_equal(oracle.to_f64(maxs[b:b + 1, :2].cpu()), ox)
+        ok = (np.array_equal(oracle.to_f64(mins_h[b:b + 1]), om)
+              and np.array_equal(oracle.to_f64(maxs_h[b:b + 1]), ox))
+        return ok, om, ox
+
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4)) as ex:
+        bounds = list(ex.map(oracle_bounds, range(B)))
+    del pool_h
+    assert all(ok for ok, _, _ in bounds), [b for b, (ok, _, _) in enumerate(bounds) if not ok]
     # every sequence against the oracle: its selected pages gathered into a
     # compact pool, addressed through a remapped page table
     ids_h, out_h = ids.cpu().numpy(), out.cpu().double().numpy()
-    mins_h, maxs_h, q_h = mins.cpu(), maxs.cpu(), q.cpu()
-    pt_h = pt.cpu().long()
     for b in range(B):
-        rid = oracle.quest_select(q_h[b:b + 1], mins_h[b:b + 1], maxs_h[b:b + 1], page_size=ps,
+        _, om, ox = bounds[b]
+        rid = oracle.quest_select(q_h[b:b + 1], om, ox, page_size=ps,
                                   topk=topk, offset=T - 1, gqa_union=union)
         assert np.array_equal(ids_h[b:b + 1], rid), b
         sel = np.unique(rid[rid >= 0])

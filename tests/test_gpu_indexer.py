@@ -4,6 +4,9 @@ the oracle's fp64 scores rounded to fp32."""
 
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 import pytest
 import torch
@@ -128,8 +131,9 @@ def test_indexer_summation_order_is_sequential(dev):
 
 def test_config2_indexer_full_size(dev):
     """C2: B=1, T=8192, 4 heads of dim 64, bf16 q/k, w ~ U(0,1), causal top-2048,
-    int32 indices.  Every row is checked for structure; 48 rows (both ends and
-    the middle) against the oracle bit for bit."""
+    int32 indices.  Every one of the 8192 rows against the oracle bit for bit
+    (indices and fp32 values), in chunks of 256 query rows on a thread pool
+    (the oracle's C scorer releases the GIL)."""
     T, HI, d, kk = 8192, 4, 64, 2048
     q, k, w = inputs(1, T, T, HI, d, seed=0, dtype=torch.bfloat16)
     val, idx = indexer_topk(q.to(dev), k.to(dev), w.to(dev), kk, causal=True)
@@ -138,14 +142,17 @@ def test_config2_indexer_full_size(dev):
     n_valid = torch.clamp(t + 1, max=kk)
     got = (idx[0] >= 0).sum(-1)
     assert torch.equal(got, n_valid)
-    assert (idx[0].max(-1).values <= t).all()
-    srt = idx[0].clone().masked_fill(idx[0] < 0, 1 << 30).sort(-1).values
-    assert ((srt[:, 1:] > srt[:, :-1]) | (srt[:, 1:] == 1 << 30)).all()  # unique
-    vv = val[0]
-    assert ((vv[:, 1:] <= vv[:, :-1]) | torch.isinf(vv[:, 1:])).all()  # sorted by score
-    rows = list(range(0, 16)) + list(range(2040, 2056)) + list(range(T - 16, T))
-    for t0 in rows:
-        rv, ri = oracle.indexer_topk(q[:, t0:t0 + 1], k, w[:, t0:t0 + 1], kk, causal=True,
-                                     offset=t0)
-        assert np.array_equal(idx[0, t0].cpu().numpy(), ri[0, 0]), t0
-        assert np.array_equal(val[0, t0].cpu().numpy(), rv[0, 0].astype(np.float32)), t0
+    idx_h, val_h = idx[0].cpu().numpy(), val[0].cpu().numpy()
+    chunk = 256
+
+    def job(t0):
+        rv, ri = oracle.indexer_topk(q[:, t0:t0 + chunk], k, w[:, t0:t0 + chunk], kk,
+                                     causal=True, offset=t0)
+        ok_i = np.array_equal(idx_h[t0:t0 + chunk], ri[0])
+        ok_v = np.array_equal(val_h[t0:t0 + chunk], rv[0].astype(np.float32))
+        return t0, ok_i, ok_v
+
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4)) as ex:
+        res = list(ex.map(job, range(0, T, chunk)))
+    bad = [(t0, oi, ov) for t0, oi, ov in res if not (oi and ov)]
+    assert not bad, bad

@@ -4,6 +4,8 @@ block-sparse causal prefill (within 2e-3 of the fp64 oracle, fp32 output)."""
 from __future__ import annotations
 
 import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -123,6 +125,41 @@ def test_prefill_multiset_lists_with_holes(dev, causal):
             assert np.abs(got - ref[0, 0]).max() < 2e-3, (h, qb)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_long_lists(dev, causal):
+    """Lists of 64, 65 and 100 entries: the kernel keeps lists of up to 64
+    entries in VGPR lanes and reads longer ones through the scalar cache, so
+    both paths and the 64/65 boundary run.  Causal: every block up to the
+    diagonal (query blocks 63, 64 and 99); non-causal: seeded multisets of
+    any blocks, -1 padded.  Within 2e-3 of the fp64 oracle."""
+    T, hq, hkv, W = 6400, 2, 1, 100
+    q, k, v = c3_inputs(1, hq, hkv, T, 128, seed=9)
+    nqb = T // 64
+    ids = np.full((1, hq, nqb, W), -1, dtype=np.int32)
+    g = np.random.default_rng(9)
+    check = {63: 64, 64: 65, 99: 100}
+    for h in range(hq):
+        for qb in range(nqb):
+            if causal:
+                n = qb + 1
+                ids[0, h, qb, :n] = np.arange(n)
+            else:
+                n = check.get(qb, int(g.integers(1, W + 1)))
+                ids[0, h, qb, :n] = g.integers(0, nqb, size=n)
+    out = block_sparse_prefill(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(ids).to(dev),
+                               causal=causal, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    for h in range(hq):
+        for qb, n in check.items():
+            assert (ids[0, h, qb] >= 0).sum() == n
+            t0 = qb * 64
+            rows = np.broadcast_to(ids[0, h, qb], (1, 1, 64, W))
+            ref = oracle.attend_lists(q[:, h:h + 1, t0:t0 + 64], k, v, rows, unit=64,
+                                      causal=causal, offset=t0)
+            got = out[0, h, t0:t0 + 64].cpu().double().numpy()
+            assert np.abs(got - ref[0, 0]).max() < 2e-3, (h, qb)
+
+
 def test_prefill_empty_list_gives_zeros(dev):
     q, k, v = c3_inputs(1, 1, 1, 128, 128, seed=4, outliers=False)
     ids = torch.full((1, 1, 2, 3), -1, dtype=torch.int32)
@@ -133,8 +170,9 @@ def test_prefill_empty_list_gives_zeros(dev):
 
 def test_config3_full_size(dev):
     """C3: B=2, T=32768, 32/8 heads, D=128, 64x64 blocks, sink + 4-block window
-    + top-16.  Lists of two heads are checked bit for bit against the oracle;
-    output rows of five query blocks per head against the fp64 oracle."""
+    + top-16.  The lists of all 64 (b, head) pairs are checked bit for bit
+    against the oracle (one pair per thread); output rows of five query blocks
+    of two heads against the fp64 oracle."""
     B, Hq, Hkv, T, D = 2, 32, 8, 32768, 128
     q, k, v = c3_inputs(B, Hq, Hkv, T, D, seed=0, device=dev)
     out, ids, counts = sparse_prefill(q, k, v, topk=16, sink_blocks=1, window_blocks=4,
@@ -146,12 +184,22 @@ def test_config3_full_size(dev):
     assert (ids.max(-1).values <= qb_idx).all()  # causal
     assert ((ids == qb_idx.view(1, 1, -1, 1)).any(-1)).all()  # diagonal block present
     assert (ids[..., 0] == 0).all()  # sink
+    ids_h, q_h, k_h = ids.cpu().numpy(), q.cpu(), k.cpu()
+
+    def lists_equal(bh):
+        b, h = divmod(bh, Hq)
+        kvh = h // (Hq // Hkv)
+        ref = oracle.block_select(q_h[b:b + 1, h:h + 1], k_h[b:b + 1, kvh:kvh + 1], block=64,
+                                  topk=16, sink_blocks=1, window_blocks=4)
+        return bh, np.array_equal(ids_h[b:b + 1, h:h + 1], ref)
+
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4)) as ex:
+        res = list(ex.map(lists_equal, range(B * Hq)))
+    assert all(ok for _, ok in res), [bh for bh, ok in res if not ok]
     for b, h in ((0, 0), (1, 13)):
         kvh = h // (Hq // Hkv)
         qc, kc, vc = q[b:b + 1, h:h + 1].cpu(), k[b:b + 1, kvh:kvh + 1].cpu(), \
             v[b:b + 1, kvh:kvh + 1].cpu()
-        ref = oracle.block_select(qc, kc, block=64, topk=16, sink_blocks=1, window_blocks=4)
-        assert np.array_equal(ids[b:b + 1, h:h + 1].cpu().numpy(), ref)
         ids_c, counts_c = ids[b:b + 1, h:h + 1].cpu(), counts[b:b + 1, h:h + 1].cpu()
         rows = oracle_rows(qc, kc, vc, ids_c, counts_c, 0, 0, (0, 1, 17, 300, nqb - 1))
         for qb, r in rows.items():
@@ -213,7 +261,8 @@ def test_prefill_large_v_blocks(dev):
     """V blocks whose values reach 2^15..2^22 are converted to fp16 with a
     power-of-two block exponent (folded back into the weights): outputs stay
     within 2e-3 relative to the value scale.  A finite |v| >= 2^22 raises
-    LA_DEV_PREFILL_RANGE (its fp16 copy overflows)."""
+    ValueError (its fp16 copy would overflow); with check_range=False the
+    rows come out inf and LA_DEV_PREFILL_RANGE is raised on the device."""
     q, k, v = c3_inputs(1, 4, 2, 512, 128, seed=6, outliers=False)
     v = v.float()
     v[0, 0, 128:192] *= 2.0 ** 18   # block 2 of KV head 0: e = 5 or 6
@@ -231,13 +280,34 @@ def test_prefill_large_v_blocks(dev):
     scale = np.abs(v.double().numpy()).max(axis=(2, 3))[:, np.repeat(np.arange(2), 2)]
     err = np.abs(out.cpu().double().numpy() - ref).max(axis=(2, 3))
     assert (err < 2e-3 * np.maximum(scale, 1.0)).all(), (err, scale)
-    # a finite value beyond the fp16 range of its scaled block is reported
+    # a finite value beyond the fp16 range of its scaled block is an error
     v2 = v.clone()
     v2[0, 0, 5, 3] = 2.0 ** 23
+    with pytest.raises(ValueError):
+        block_sparse_prefill(q.to(dev), k.to(dev), v2.to(dev), ids.to(dev),
+                             out_dtype=torch.float32)
+    assert N.device_status(dev) == 0  # the error consumed the status bit
     out2 = block_sparse_prefill(q.to(dev), k.to(dev), v2.to(dev), ids.to(dev),
-                                out_dtype=torch.float32)
+                                out_dtype=torch.float32, check_range=False)
     assert N.device_status(dev) & N.LA_DEV_PREFILL_RANGE
     assert not torch.isfinite(out2[0, :2]).all()
+
+
+def test_prefill_small_v_blocks_keep_relative_precision(dev):
+    """V blocks of small magnitude (|v| ~ 2^-18, below the fp16 normal range)
+    are scaled up by their block exponent (by up to 2^8): outputs keep 2e-3
+    relative precision, not only absolute."""
+    q, k, v = c3_inputs(1, 2, 1, 256, 128, seed=8, outliers=False)
+    v = (v.float() * 2.0 ** -20).bfloat16()
+    nqb = 4
+    ids = torch.full((1, 2, nqb, nqb), -1, dtype=torch.int32)
+    for i in range(nqb):
+        ids[:, :, i, :i + 1] = torch.arange(i + 1, dtype=torch.int32)
+    out = block_sparse_prefill(q.to(dev), k.to(dev), v.to(dev), ids.to(dev),
+                               out_dtype=torch.float32)
+    ref = oracle.dense_attention(q, k, v)
+    scale = float(np.abs(v.double().numpy()).max())
+    assert np.abs(out.cpu().double().numpy() - ref).max() < 2e-3 * scale
 
 
 def test_ragged_batch_equals_one_call_per_sequence(dev):

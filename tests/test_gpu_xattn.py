@@ -158,6 +158,27 @@ def test_hip_xattention_prefill_kernel_path(dev):
     assert np.abs(out.cpu().double().numpy() - ref).max() < 2e-3 + 2 ** -9 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("ratio", [0.02, 0.5])
+def test_hip_xattention_top_ratio(dev, ratio):
+    """select_mode "top_ratio" (selection.py:583-585): lists equal the
+    oracle's (every visible block) for a prefill and an offset chunk, and the
+    variant's output equals the oracle's chunked forward and dense causal
+    attention."""
+    q, k, v = inputs(1, 4, 2, 160, 160, 64, seed=36)
+    for s0 in (0, 101):
+        ids, counts = xattn_select_hip(q[:, :, s0:].to(dev), k.to(dev), block=8, stride=8,
+                                       offset=s0, top_ratio=ratio)
+        ref_ids, ref_counts = oracle.xattn_select(q[:, :, s0:], k, block=8, stride=8, offset=s0,
+                                                  top_ratio=ratio)
+        check_lists(ids, counts, ref_ids, ref_counts)
+    c = cfg(extras={"select_mode": "top_ratio", "top_ratio": ratio})
+    out, _ = build("hip_xattention", c).forward(q.to(dev), k.to(dev), v.to(dev), chunk=48)
+    ref = xattn_oracle(q, k, v, c, 48, top_ratio=ratio)
+    assert np.abs(out.cpu().double().numpy() - ref).max() < 1e-5
+    dense = oracle.dense_attention(q, k, v)
+    assert np.abs(out.cpu().double().numpy() - dense).max() < 1e-5
+
+
 def test_hip_xattention_full_budget_recovers_dense(dev):
     """test_budgets.py:64-81 for XAttention (select_mode topk over every
     block, and a threshold above 1), float64 in and out."""

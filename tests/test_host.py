@@ -19,10 +19,11 @@ def test_registry_names_and_errors():
     assert set(KERNEL_VARIANTS) == {"hip_quest", "hip_dsa", "hip_moba", "hip_xattention",
                                     "hip_sliding_window", "hip_streaming_sink"}
     assert describe_kernel("hip_xattention")["reference"] == "xattention"
-    # top_ratio compares cumulative mass with a block count (selection.py:583-585):
-    # not offered
+    # the three selection rules of selection.py:578-590; anything else is refused
+    for mode in ("threshold", "topk", "top_ratio"):
+        assert build("hip_xattention", extras={"select_mode": mode}).select_mode == mode
     with pytest.raises(ValueError):
-        build("hip_xattention", extras={"select_mode": "top_ratio"})
+        build("hip_xattention", extras={"select_mode": "top_p"})
     assert describe_kernel("hip_moba")["reference"] == "moba"
     assert describe_kernel("hip_quest")["reference"] == "quest"
     assert build("hip_quest").name == "hip_quest"

@@ -606,7 +606,7 @@ def test_exp_det_matches_libm():
     assert oracle.exp_det(-700.0) == 0.0 and oracle.exp_det(-1e9) == 0.0
 
 
-def _xattn_float_reference(q, k, *, block, stride, threshold, offset, topk=None):
+def _xattn_float_reference(q, k, *, block, stride, threshold, offset, topk=None, top_ratio=None):
     """XAttention.select (selection.py:528-595) restated with numpy floats:
     antidiagonal sums by einsum over the whole (query block, key block) gram
     tensor, fp64 softmax over the visible (block, slot) pairs, a stable sort
@@ -638,6 +638,10 @@ def _xattn_float_reference(q, k, *, block, stride, threshold, offset, topk=None)
         order = sorted(range(n_kb), key=lambda j: (-mass[j], j))
         if topk is not None:
             n_keep = min(topk, n_kb)
+        elif top_ratio is not None:  # _select_with_per_head with a block count (:583-585)
+            c = max(1.0, math.ceil(vis.sum() * top_ratio))
+            reached = np.cumsum(mass[order]) >= c
+            n_keep = int(reached.argmax()) + 1 if reached.any() else n_kb
         else:
             cs = np.cumsum(mass[order])
             n_keep = min(int((cs < threshold).sum()) + 1, n_kb)
@@ -648,10 +652,13 @@ def _xattn_float_reference(q, k, *, block, stride, threshold, offset, topk=None)
     return out
 
 
-@pytest.mark.parametrize("block,stride,threshold,offset,topk,T", [
-    (8, 8, 0.9, 0, None, 203), (8, 4, 0.6, 0, None, 128), (16, 8, 0.95, 5, None, 150),
-    (4, 2, 0.5, 0, None, 61), (8, 8, None, 0, 3, 203), (8, 8, 1.5, 0, None, 100)])
-def test_xattn_select_matches_float_restatement(block, stride, threshold, offset, topk, T):
+@pytest.mark.parametrize("block,stride,threshold,offset,topk,T,top_ratio", [
+    (8, 8, 0.9, 0, None, 203, None), (8, 4, 0.6, 0, None, 128, None),
+    (16, 8, 0.95, 5, None, 150, None), (4, 2, 0.5, 0, None, 61, None),
+    (8, 8, None, 0, 3, 203, None), (8, 8, 1.5, 0, None, 100, None),
+    (8, 8, None, 0, None, 203, 0.02), (4, 2, None, 7, None, 150, 0.3)])
+def test_xattn_select_matches_float_restatement(block, stride, threshold, offset, topk, T,
+                                                top_ratio):
     r = rng(21)
     B, Hq, Hkv, D = 1, 2, 1, 32
     Tq = T - offset
@@ -660,10 +667,11 @@ def test_xattn_select_matches_float_restatement(block, stride, threshold, offset
     k[0, 0, r.permutation(T)[:T // 10]] *= 4.0  # peaked rows
     ids, counts = oracle.xattn_select(q, k, block=block, stride=stride,
                                       threshold=threshold if threshold else 0.9, offset=offset,
-                                      topk=topk)
+                                      topk=topk, top_ratio=top_ratio)
     for h in range(Hq):
         ref = _xattn_float_reference(q[0, h], k[0, 0], block=block, stride=stride,
-                                     threshold=threshold, offset=offset, topk=topk)
+                                     threshold=threshold, offset=offset, topk=topk,
+                                     top_ratio=top_ratio)
         for qb, lst in enumerate(ref):
             got = [int(x) for x in ids[0, h, qb] if x >= 0]
             assert got == lst, (h, qb, got, lst)
@@ -693,7 +701,7 @@ def test_xattn_full_budget_recovers_dense():
     q = r.standard_normal((1, 2, 70, 16)).astype(np.float32)
     k = r.standard_normal((1, 1, 70, 16)).astype(np.float32)
     v = r.standard_normal((1, 1, 70, 16)).astype(np.float32)
-    for kw in (dict(threshold=1.5), dict(topk=100)):
+    for kw in (dict(threshold=1.5), dict(topk=100), dict(top_ratio=0.02)):
         ids, counts = oracle.xattn_select(q, k, block=8, stride=8, **kw)
         rows = np.repeat(ids, 8, axis=2)[:, :, :70]
         out = oracle.attend_lists(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
