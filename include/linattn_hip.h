@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 11
+#define LA_ABI_VERSION 12
 
 /* element types */
 enum {
@@ -81,7 +81,11 @@ const char *la_last_error(void);
  *    t % page_size.  The reference has no page table; this layout is new.
  * fp8 caches carry one fp32 scale per token and KV head (kv/quant.py:90-93
  * with group_size == head_dim): contiguous scales are (B, Hkv, T) with
- * strides s_sb/s_sh/s_st; paged scales are [phys_page][Hkv][page_size].
+ * strides s_sb/s_sh/s_st; paged scales are [phys_page][Hkv][page_size] with
+ * pool row r's scale at k_scale[r * s_st] / v_scale[r * s_st] (s_st = 0 reads
+ * as 1; s_st = 2 with v_scale = k_scale + 1 interleaves each token's K and V
+ * scales, so a token read from a random position costs one 64-byte sector of
+ * scales instead of two).
  * kv_len (optional, int32 [B]) limits the valid tokens of each sequence.
  */
 typedef struct {
@@ -283,7 +287,7 @@ typedef struct {
   void *k_pool;
   void *v_pool;
   float *k_scale; /* fp8 pool: (n_phys, Hkv, pool_page) per-token scales */
-  float *v_scale;
+  float *v_scale; /* (pool row r's at r * s_stride) */
   const int32_t *page_table;
   const int32_t *positions;
   void *page_min;
@@ -294,6 +298,8 @@ typedef struct {
   int64_t meta_page, n_pages, m_sb, m_sh, m_sp, m_sd;
   int32_t in_dtype;   /* LA_F32 or LA_BF16 */
   int32_t pool_dtype; /* in_dtype, or LA_FP8_E4M3 */
+  int64_t s_stride;   /* fp8 pool: scale elements between pool rows (0 reads as 1;
+                         2: K and V scales interleaved, v_scale = k_scale + 1) */
 } la_kv_append_args;
 
 int la_paged_kv_append(const la_kv_append_args *a, void *stream);

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -105,7 +105,7 @@ class LaKvAppendArgs(ctypes.Structure):
                 ("D", _i64), ("n_sb", _i64), ("n_sh", _i64), ("n_st", _i64), ("n_phys", _i64),
                 ("pool_page", _i64), ("pt_sb", _i64), ("pt_pages", _i64), ("meta_page", _i64),
                 ("n_pages", _i64), ("m_sb", _i64), ("m_sh", _i64), ("m_sp", _i64), ("m_sd", _i64),
-                ("in_dtype", _i32), ("pool_dtype", _i32)]
+                ("in_dtype", _i32), ("pool_dtype", _i32), ("s_stride", _i64)]
 
 
 class LaIndexerArgs(ctypes.Structure):

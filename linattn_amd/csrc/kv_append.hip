@@ -25,6 +25,7 @@ struct KaKP {
   int64_t n_phys, pool_page, pt_sb, pt_pages;
   int64_t meta_page, n_pages, m_sb, m_sh, m_sp, m_sd;
   int32_t in_dt, pool_dt;
+  int64_t s_stride;  // fp8: scale elements between pool rows
 };
 
 // fp32 absmax of the row over the workgroup (every thread gets it)
@@ -67,7 +68,7 @@ __device__ __forceinline__ void ka_store_row(const KaKP &p, void *pool, float *s
         ((uint8_t *)pool)[row + d] = (uint8_t)(w & 0xff);
       }
     }
-    if (tid == 0) scales[srow] = scale;
+    if (tid == 0) scales[srow * p.s_stride] = scale;
     return;
   }
   if (!ok) return;
@@ -176,6 +177,7 @@ extern "C" int la_paged_kv_append(const la_kv_append_args *a, void *stream) {
   p.v_pool = a->v_pool;
   p.k_scale = a->k_scale;
   p.v_scale = a->v_scale;
+  p.s_stride = a->s_stride > 0 ? a->s_stride : 1;
   p.page_table = a->page_table;
   p.positions = a->positions;
   p.mn = meta ? a->page_min : nullptr;

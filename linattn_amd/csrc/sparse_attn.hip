@@ -181,7 +181,7 @@ __device__ __forceinline__ bool token_rows(const AttnKP &p, const RowCtx &rc, co
       prow = (phys * p.Hkv + rc.kvh) * ps + tok % ps;
     }
     ko = vo = prow * D;
-    so = prow;
+    so = prow * p.kv.s_st;  // paged scales: pool row r at r * s_st
   } else {
     ko = rc.k_bh + (int64_t)tok * p.kv.k_st;
     vo = rc.v_bh + (int64_t)tok * p.kv.v_st;
@@ -550,9 +550,10 @@ __device__ __forceinline__ void mfma_attend(const AttnKP &p, const RowCtx &rc,
   struct Round {
     int32_t tok;    // first token of the round (-1: nothing to attend)
     int64_t kb, vb; // element offsets of its K and V rows
+    int64_t sb;     // fp8: index of its first token's scale (tokens s_st apart)
   };
   auto round_of = [&](int32_t base) {
-    Round rd{-1, 0, 0};
+    Round rd{-1, 0, 0, 0};
     const int32_t fw = base + wu * RT;
     if (fw >= F) return rd;
     int32_t e, j;
@@ -569,13 +570,15 @@ __device__ __forceinline__ void mfma_attend(const AttnKP &p, const RowCtx &rc,
     if constexpr (PAGED) {
       const uint32_t prow = (uint32_t)__builtin_amdgcn_readfirstlane(s_phys[e]) + (uint32_t)j;
       rd.kb = rd.vb = (int64_t)prow * D;
+      rd.sb = (int64_t)prow * p.kv.s_st;
     } else {
       rd.kb = rc.k_bh + (int64_t)rd.tok * p.kv.k_st;
       rd.vb = rc.v_bh + (int64_t)rd.tok * p.kv.v_st;
+      rd.sb = rc.s_bh + (int64_t)rd.tok * p.kv.s_st;
     }
     return rd;
   };
-  Round rd_next{-1, 0, 0};
+  Round rd_next{-1, 0, 0, 0};
   // U16 loads are issued for every lane: the 16 rows of a round lie in one
   // pool page, so every row address is valid; a round with nothing to attend
   // reads the first rows of the pool instead.  Tokens that are not attended
@@ -593,11 +596,11 @@ __device__ __forceinline__ void mfma_attend(const AttnKP &p, const RowCtx &rc,
       const char *rp = rd_next.tok >= 0 ? kbase + rd_next.kb * ESZ : kbase;  // wave-uniform
 #pragma unroll
       for (int s = 0; s < (F8 ? 2 : 4); ++s) kr[s] = nt_ld((const uint4 *)(rp + koff + 16 * (F8 ? 1 : 4) * s));
-      if constexpr (F8) f8s.k = p.kv.k_scale[(rd_next.tok >= 0 ? rd_next.kb / D : 0) + c];
+      if constexpr (F8) f8s.k = p.kv.k_scale[rd_next.tok >= 0 ? rd_next.sb + c * p.kv.s_st : 0];
     } else {
       int64_t ko = 0, vo = 0, so = 0;
       kok = token_rows<D, PAGED>(p, rc, s_tok0, s_phys, base + w * RT + c, F, lim32, ko, vo, so);
-      if constexpr (PAGED) prow_k = kok ? (uint32_t)so : 0xffffffffu;
+      if constexpr (PAGED) prow_k = kok ? (uint32_t)(ko / D) : 0xffffffffu;  // ko = pool row * D
       if constexpr (F8) {
 #pragma unroll
         for (int s = 0; s < 2; ++s)
@@ -617,7 +620,8 @@ __device__ __forceinline__ void mfma_attend(const AttnKP &p, const RowCtx &rc,
       const VVec x = nt_ld((const VVec *)(rp + voff + 4 * u * D * ESZ));
       if constexpr (F8) vr[u] = ok ? x : uint2{0, 0}; else vr[u] = ok ? x : uint4{0, 0, 0, 0};
       if constexpr (F8) {
-        const float sv = p.kv.v_scale[(rd_next.tok >= 0 ? rd_next.vb / D : 0) + 4 * u + slot];
+        const float sv =
+            p.kv.v_scale[rd_next.tok >= 0 ? rd_next.sb + (4 * u + slot) * p.kv.s_st : 0];
         f8s.v[u] = ok ? sv : 0.f;
       }
     } else {
@@ -629,7 +633,7 @@ __device__ __forceinline__ void mfma_attend(const AttnKP &p, const RowCtx &rc,
         const uint32_t pr = (uint32_t)__shfl((int)prow_k, 4 * u + slot, 64);
         ok = pr != 0xffffffffu;
         vo = (int64_t)pr * D;
-        so = pr;
+        so = (int64_t)pr * p.kv.s_st;
       } else {
         ok = token_rows<D, PAGED>(p, rc, s_tok0, s_phys, base + w * RT + 4 * u + slot, F, lim32, ko, vo, so);
       }
@@ -1027,6 +1031,7 @@ static int sparse_attention_run(const la_sparse_attn_args *a, const la_kv *kv, c
   p.ids = a->ids;
   p.counts = a->counts;
   p.kv = *kv;
+  if (kv->page_table && p.kv.s_st <= 0) p.kv.s_st = 1;  // paged scales: contiguous by default
   p.B = a->B;
   p.Hq = a->Hq;
   p.Hkv = a->Hkv;

@@ -77,19 +77,18 @@ __device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
   return r;
 }
 
-// Long plain rows split over several workgroups per row (topk_wide.hip):
-// C chunks per row, R rows per cooperative launch, workspace bytes (state of
-// one launch, then the candidate rows of a sorted selection).  C = 0 when the
-// device cannot hold one row's chunks at once.
-struct WidePlan {
-  int64_t C = 0, R = 0, state_bytes = 0, bytes = 0;
-  bool plain = false;  // ordinary launch instead of a cooperative one
+// Long plain rows split over several workgroups per row (topk_radix.hip): C
+// chunks per row; workspace bytes (per-row state, digit histograms, chunk
+// records, then the candidate rows of a sorted selection).  C = 0 when a row
+// holds 2^31 keys or more.
+struct RadixPlan {
+  int64_t C = 0, bytes = 0;
 };
-WidePlan wide_plan(const TopkKParams &p);
-int topk_wide_launch(const TopkKParams &p, const WidePlan &W, void *ws, hipStream_t st);
+RadixPlan radix_plan(const TopkKParams &p);
+int topk_radix_launch(const TopkKParams &p, const RadixPlan &R, void *ws, hipStream_t st);
 
-// Workspace bytes topk_launch needs (rows longer than the LDS can hold are
-// selected in segments: candidates of each level are kept in the workspace).
+// Workspace bytes topk_launch_ws needs (rows longer than the LDS can hold go
+// to the multi-workgroup radix select).
 int64_t topk_workspace_bytes(const TopkKParams &p);
 
 // As topk_launch, with a workspace for long rows.

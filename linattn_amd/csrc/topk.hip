@@ -918,48 +918,11 @@ static int max_dynamic_lds() {
   return cached;
 }
 
-// Gather the segment winners into candidate rows: slot (row, seg*k + j) gets
-// the score and the original index of winner j of segment seg, or padding
-// (lowest key, index -1).
-// Segments are laid out in order and winners in increasing position, so slot
-// order is original-index order and position ties keep the lowest-index rule.
-__global__ __launch_bounds__(256) void topk_gather_kernel(
-    const double *scores, int64_t row_stride, const int32_t *prev_idx, const int32_t *win,
-    const int32_t *win_count, int64_t nseg, int64_t seg_len, int64_t k, double *cand_sc,
-    int32_t *cand_id) {
-  const int64_t g = blockIdx.x;  // (row, seg)
-  const int64_t row = g / nseg, seg = g % nseg;
-  const int64_t cnt = win_count[g];
-  const int64_t n_c = nseg * k;
-  for (int64_t j = threadIdx.x; j < k; j += blockDim.x) {
-    const int32_t pos = j < cnt ? win[g * k + j] : -1;
-    // padding: the all-ones pattern maps to key 0, below every real score
-    double s = __longlong_as_double((long long)0xffffffffffffffffull);
-    int32_t id = -1;
-    if (pos >= 0) {
-      const int64_t src = seg * seg_len + pos;
-      s = scores[row * row_stride + src];
-      id = prev_idx ? prev_idx[row * row_stride + src] : (int32_t)src;
-    }
-    cand_sc[row * n_c + seg * k + j] = s;
-    cand_id[row * n_c + seg * k + j] = id;
-  }
-}
-
-struct LongPlan {
-  int64_t levels = 0;    // segmented levels before the final select
-  int64_t seg_len = 0;
-  int64_t n[4] = {0, 0, 0, 0};  // row length at each level (n[levels] is final)
-  int64_t bytes = 0;
-};
-
 static int64_t lds_limit() { return (int64_t)max_dynamic_lds() - (int64_t)sizeof(TkShared) - 256; }
 
-// Long rows (keys + sort buffer beyond LDS) of a plain top-k are reduced in
-// segments that fit the LDS; each level keeps k per segment, in index order,
-// so the candidate rows of the final level are in ascending unit order.
-// Sorted (order 0) or index-order (order 1) rows of one head with no extras,
-// too long for one workgroup's LDS.
+// Plain rows (sorted or index-order rows of one head with no extras) too long
+// for one workgroup's LDS go to the multi-workgroup radix select
+// (topk_radix.hip).
 static bool long_plain(const TopkKParams &p) {
   const bool plain = p.G == 1 && p.sink == 0 && p.window == 0 && (p.order == 0 || p.order == 1) &&
                      !p.force_own && !p.cand_idx && p.seg_len == 0;
@@ -968,105 +931,25 @@ static bool long_plain(const TopkKParams &p) {
   return plain && p.n * 8 + p2 * 12 + 64 > lds_limit();
 }
 
-static LongPlan long_plan(const TopkKParams &p) {
-  LongPlan L;
-  int64_t p2 = 1;
-  while (p2 < p.k) p2 <<= 1;
-  const int64_t limit = lds_limit();
-  if (!long_plain(p)) return L;
-  int64_t seg = 1;
-  while ((seg * 2) * 8 + (seg * 2) / 8 + 64 <= limit) seg *= 2;
-  if (p.k * 2 > seg) return L;  // segments would not shrink the rows
-  int64_t n = p.n;
-  L.seg_len = seg;
-  L.n[0] = n;
-  while (n * 8 + p2 * 12 + 64 > limit && L.levels < 3) {
-    const int64_t nseg = (n + seg - 1) / seg;
-    const int64_t n_next = nseg * p.k;
-    // winners (positions + counts) and candidate rows (fp64 score + int32 index)
-    L.bytes += align16(p.NG * nseg * p.k * 4) + align16(p.NG * nseg * 4) +
-               align16(p.NG * n_next * 8) + align16(p.NG * n_next * 4);
-    n = n_next;
-    L.n[++L.levels] = n;
-  }
-  if (n * 8 + p2 * 12 + 64 > limit) L.levels = -1;  // would not converge
-  return L;
-}
-
 int64_t topk_workspace_bytes(const TopkKParams &p) {
   if (long_plain(p)) {
-    const WidePlan W = wide_plan(p);
-    if (W.C > 0) return W.bytes;
+    const RadixPlan R = radix_plan(p);
+    if (R.C > 0) return R.bytes;
   }
-  const LongPlan L = long_plan(p);
-  return L.levels > 0 ? L.bytes : 0;
+  return 0;
 }
 
 int topk_launch_ws(TopkKParams p, void *ws, int64_t ws_bytes, hipStream_t st) {
   if (p.NG <= 0) return LA_OK;
   if (long_plain(p)) {
-    const WidePlan W = wide_plan(p);
-    if (W.C > 0) {
-      if (!ws || ws_bytes < W.bytes)
-        return fail(LA_ERR_WORKSPACE, "topk: long rows need %lld workspace bytes",
-                    (long long)W.bytes);
-      return topk_wide_launch(p, W, ws, st);
-    }
+    const RadixPlan R = radix_plan(p);
+    if (R.C <= 0) return fail(LA_ERR_UNSUPPORTED, "topk: rows of 2^31 or more keys");
+    if (!ws || ws_bytes < R.bytes)
+      return fail(LA_ERR_WORKSPACE, "topk: long rows need %lld workspace bytes",
+                  (long long)R.bytes);
+    return topk_radix_launch(p, R, ws, st);
   }
-  const LongPlan L = long_plan(p);
-  if (L.levels <= 0) return topk_launch(p, st);
-  if (!ws || ws_bytes < L.bytes)
-    return fail(LA_ERR_WORKSPACE, "topk: long rows need %lld workspace bytes",
-                (long long)L.bytes);
-  char *w = (char *)ws;
-  const double *src_sc = p.scores;
-  int64_t src_stride = p.row_stride;
-  const int32_t *src_id = nullptr;
-  for (int64_t lev = 0; lev < L.levels; ++lev) {
-    const int64_t n = L.n[lev];
-    const int64_t nseg = (n + L.seg_len - 1) / L.seg_len;
-    const int64_t n_next = L.n[lev + 1];
-    int32_t *win = (int32_t *)w;
-    w += align16(p.NG * nseg * p.k * 4);
-    int32_t *cnt = (int32_t *)w;
-    w += align16(p.NG * nseg * 4);
-    double *csc = (double *)w;
-    w += align16(p.NG * n_next * 8);
-    int32_t *cid = (int32_t *)w;
-    w += align16(p.NG * n_next * 4);
-    TopkKParams s = p;
-    s.scores = src_sc;
-    s.row_stride = src_stride;
-    s.n = n;
-    s.width = p.k;
-    s.order = 1;
-    s.out_idx = win;
-    s.out_val = nullptr;
-    s.out_count = cnt;
-    s.seg_len = L.seg_len;
-    s.nseg = nseg;
-    s.NG = p.NG * nseg;
-    if (lev > 0) {  // candidate rows: every slot is valid (padding is -inf)
-      s.pos_unit = 0;
-      s.n_valid_tab = nullptr;
-    }
-    int rc = topk_launch(s, st);
-    if (rc != LA_OK) return rc;
-    topk_gather_kernel<<<dim3((unsigned)(p.NG * nseg)), 256, 0, st>>>(
-        src_sc, src_stride, src_id, win, cnt, nseg, L.seg_len, p.k, csc, cid);
-    LA_LAUNCHED();
-    src_sc = csc;
-    src_stride = n_next;
-    src_id = cid;
-  }
-  TopkKParams f = p;
-  f.scores = src_sc;
-  f.row_stride = src_stride;
-  f.n = L.n[L.levels];
-  f.pos_unit = 0;
-  f.n_valid_tab = nullptr;
-  f.cand_idx = src_id;
-  return topk_launch(f, st);
+  return topk_launch(p, st);
 }
 
 template <bool BITMAP, int KPT>

@@ -10,18 +10,47 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
 from linattn_amd import _native as N
 
-__all__ = ["sparse_attention", "block_sparse_attention", "block_sparse_attention_hip"]
+__all__ = ["sparse_attention", "block_sparse_attention", "block_sparse_attention_hip",
+           "fp8_scale_pairs"]
 
 
 def _strides3(t: torch.Tensor):
     s = t.stride()
     return s[0], s[1], s[2]
+
+
+def _paged_scale_stride(scale: torch.Tensor, pool: torch.Tensor) -> int:
+    """Element stride between the scales of consecutive pool rows of a paged
+    fp8 pool (n_phys, Hkv, page_size, D): scales are (n_phys, Hkv, page_size)
+    with strides (Hkv*page_size*s, page_size*s, s) -- s = 1 for a contiguous
+    tensor, s = 2 for the K or V half of an interleaved (..., 2) pair tensor
+    (``fp8_scale_pairs``)."""
+    n_phys, Hkv, ps = pool.shape[0], pool.shape[1], pool.shape[2]
+    if scale.dim() == 4 and scale.shape[3] == 1:
+        scale = scale.squeeze(3)
+    if scale.shape != (n_phys, Hkv, ps):
+        raise ValueError("paged fp8 scales must be (n_pages, Hkv, page_size)")
+    s = scale.stride(2)
+    if s < 1 or scale.stride() != (Hkv * ps * s, ps * s, s):
+        raise ValueError("paged fp8 scales: rows at one constant stride (contiguous, or one "
+                         "half of an interleaved (n_pages, Hkv, page_size, 2) tensor)")
+    return s
+
+
+def fp8_scale_pairs(n_pages: int, Hkv: int, page_size: int, device) -> Tuple[torch.Tensor,
+                                                                          torch.Tensor]:
+    """Per-token K and V scales of a paged fp8 pool stored interleaved
+    ((n_pages, Hkv, page_size, 2) fp32): returns the K and V views.  A token
+    then reads both of its scales from one 8-byte pair (one memory sector)
+    instead of two scattered 4-byte values."""
+    pairs = torch.empty(n_pages, Hkv, page_size, 2, dtype=torch.float32, device=device)
+    return pairs[..., 0], pairs[..., 1]
 
 
 def _kv_struct(k: torch.Tensor, v: torch.Tensor, *, page_table: Optional[torch.Tensor],
@@ -62,8 +91,8 @@ def _kv_struct(k: torch.Tensor, v: torch.Tensor, *, page_table: Optional[torch.T
         kv.k_scale, kv.v_scale = k_scale.data_ptr(), v_scale.data_ptr()
         if page_table is None:
             kv.s_sb, kv.s_sh, kv.s_st = _strides3(k_scale)
-        elif not k_scale.is_contiguous():
-            raise ValueError("paged fp8 scales must be contiguous (n_pages, Hkv, page_size[, 1])")
+        else:
+            kv.s_st = _paged_scale_stride(k_scale, k)
     if kv_len is not None:
         if kv_len.dtype != torch.int32 or not kv_len.is_contiguous():
             raise ValueError("kv_len must be contiguous int32 (B,)")

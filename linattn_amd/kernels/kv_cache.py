@@ -18,6 +18,7 @@ from typing import Optional
 import torch
 
 from linattn_amd import _native as N
+from linattn_amd.kernels.block_sparse import _paged_scale_stride
 
 __all__ = ["paged_kv_append"]
 
@@ -37,7 +38,8 @@ def paged_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tens
     ``page_size`` tokens that the new tokens touch are updated in place; for an
     append at the end of each sequence the result equals ``page_update_hip``
     over the grown cache bit for bit.  An fp8 (``torch.float8_e4m3fn``) pool
-    takes ``k_scale`` / ``v_scale`` (n_phys, Hkv, pool_page) fp32 and stores
+    takes ``k_scale`` / ``v_scale`` (n_phys, Hkv, pool_page) fp32 (contiguous,
+    or the interleaved halves of ``fp8_scale_pairs``) and stores
     codes = e4m3(x / scale), scale = max(|x|, 1e-8) / 448 per token (no page
     bounds for fp8 pools).  Runs on the current stream; inputs are not
     modified."""
@@ -70,11 +72,12 @@ def paged_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tens
     a.k_new, a.v_new = k_new.data_ptr(), v_new.data_ptr()
     a.k_pool, a.v_pool = k_pool.data_ptr(), v_pool.data_ptr()
     if fp8:
-        sshape = (n_phys, Hkv, pool_page)
         for s in (k_scale, v_scale):
-            if s is None or s.dtype != torch.float32 or s.shape != sshape or not s.is_contiguous():
-                raise ValueError("fp8 pools need contiguous fp32 k_scale / v_scale "
-                                 "(n_phys, Hkv, pool_page)")
+            if s is None or s.dtype != torch.float32:
+                raise ValueError("fp8 pools need fp32 k_scale / v_scale (n_phys, Hkv, pool_page)")
+        if k_scale.stride() != v_scale.stride():
+            raise ValueError("k_scale / v_scale must share strides")
+        a.s_stride = _paged_scale_stride(k_scale, k_pool)
         a.k_scale, a.v_scale = k_scale.data_ptr(), v_scale.data_ptr()
     a.page_table, a.positions = page_table.data_ptr(), positions.data_ptr()
     if (page_min is None) != (page_max is None):

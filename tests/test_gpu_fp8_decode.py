@@ -9,12 +9,15 @@ import pytest
 import torch
 
 import oracle
+from linattn_amd.kernels.block_sparse import fp8_scale_pairs
 from linattn_amd.kernels.paged_decode import indexer_decode_step, quantize_fp8_per_token
 
 pytestmark = pytest.mark.gpu
 
 
-def c5_inputs(B, Hq, Hkv, T, D, ps, HI, d, seed, dev):
+def c5_inputs(B, Hq, Hkv, T, D, ps, HI, d, seed, dev, pairs=False):
+    """Seeded C5 inputs; with ``pairs`` the per-token K and V scales are the
+    interleaved halves of one (pages, Hkv, page, 2) tensor (fp8_scale_pairs)."""
     g = torch.Generator(device=dev).manual_seed(seed)
     P = T // ps
     q = torch.randn(B, Hq, 1, D, generator=g, device=dev).bfloat16()
@@ -23,6 +26,11 @@ def c5_inputs(B, Hq, Hkv, T, D, ps, HI, d, seed, dev):
     kc, ks = quantize_fp8_per_token(kf)
     vc, vs = quantize_fp8_per_token(vf)
     del kf, vf
+    if pairs:
+        ks2, vs2 = fp8_scale_pairs(B * P, Hkv, ps, dev)
+        ks2.copy_(ks)
+        vs2.copy_(vs)
+        ks, vs = ks2, vs2
     pt = torch.randperm(B * P, generator=g, device=dev).view(B, P).to(torch.int32)
     q_idx = torch.randn(B, 1, HI, d, generator=g, device=dev).bfloat16()
     k_idx = torch.randn(B, T, HI, d, generator=g, device=dev).bfloat16()
@@ -65,9 +73,10 @@ def check_rows(out, idx, q, kc, vc, ks, vs, pt, q_idx, k_idx, w, b, topk, pos, p
     assert err < 1e-2, err
 
 
-def test_fp8_indexer_decode_small(dev):
+@pytest.mark.parametrize("pairs", [False, True])
+def test_fp8_indexer_decode_small(dev, pairs):
     B, Hq, Hkv, T, D, ps, HI, d, topk = 2, 8, 2, 8192, 128, 64, 4, 64, 512
-    x = c5_inputs(B, Hq, Hkv, T, D, ps, HI, d, seed=3, dev=dev)
+    x = c5_inputs(B, Hq, Hkv, T, D, ps, HI, d, seed=3, dev=dev, pairs=pairs)
     q, kc, vc, ks, vs, pt, q_idx, k_idx, w = x
     out, idx = indexer_decode_step(q, kc, vc, pt, q_idx, k_idx, w, topk=topk, pos=T - 1,
                                    page_size=ps, k_scale=ks, v_scale=vs, out_dtype=torch.float32)
@@ -91,9 +100,10 @@ def test_config5_fp8_decode_full_size(dev):
     """C5: batch 16, context 131072, 64-token pages, 32/8 heads, D=128, fp8 KV,
     indexer (4 x 64, bf16) top-4096.  All lists checked for structure, and
     every one of the 16 sequences against the oracle: token ids bit for bit,
-    outputs within 1e-2 of the fp8-dequantised attention."""
+    outputs within 1e-2 of the fp8-dequantised attention.  The scales are
+    stored interleaved (K, V) per token, as the benchmark stores them."""
     B, Hq, Hkv, T, D, ps, HI, d, topk = 16, 32, 8, 131072, 128, 64, 4, 64, 4096
-    x = c5_inputs(B, Hq, Hkv, T, D, ps, HI, d, seed=0, dev=dev)
+    x = c5_inputs(B, Hq, Hkv, T, D, ps, HI, d, seed=0, dev=dev, pairs=True)
     q, kc, vc, ks, vs, pt, q_idx, k_idx, w = x
     out, idx = indexer_decode_step(q, kc, vc, pt, q_idx, k_idx, w, topk=topk, pos=T - 1,
                                    page_size=ps, k_scale=ks, v_scale=vs, out_dtype=torch.float32)

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 import oracle
+from linattn_amd.kernels.block_sparse import fp8_scale_pairs
 from linattn_amd.kernels.kv_cache import paged_kv_append
 from linattn_amd.kernels.paged_decode import quest_decode_step
 from linattn_amd.kernels.quest_pages import page_update_hip, quest_select_hip
@@ -72,15 +73,23 @@ def test_append_matches_recompute(dev, dtype, Tn, meta_page):
     assert np.array_equal(maxs[0:1, :, :npg].cpu().double().numpy(), ox)
 
 
-def test_append_fp8_codec(dev):
+@pytest.mark.parametrize("pairs", [False, True])
+def test_append_fp8_codec(dev, pairs):
+    """fp8 pool append: codes and per-token scales equal the codec's, with the
+    scales contiguous or interleaved (K, V) per token (fp8_scale_pairs)."""
     B, Hkv, D, pool_page, max_len, Tn = 2, 2, 128, 16, 128, 20
     g = torch.Generator(device="cpu").manual_seed(7)
     n_phys = B * (max_len // pool_page)
     pt = torch.randperm(n_phys, generator=g).view(B, -1).to(torch.int32).to(dev)
     k_pool = torch.zeros(n_phys, Hkv, pool_page, D, dtype=torch.float8_e4m3fn, device=dev)
     v_pool = torch.zeros_like(k_pool)
-    k_scale = torch.zeros(n_phys, Hkv, pool_page, device=dev)
-    v_scale = torch.zeros_like(k_scale)
+    if pairs:
+        k_scale, v_scale = fp8_scale_pairs(n_phys, Hkv, pool_page, dev)
+        k_scale.zero_()
+        v_scale.zero_()
+    else:
+        k_scale = torch.zeros(n_phys, Hkv, pool_page, device=dev)
+        v_scale = torch.zeros_like(k_scale)
     positions = torch.tensor([3, 50], dtype=torch.int32, device=dev)
     k_new = (torch.randn(B, Hkv, Tn, D, generator=g) * 3).bfloat16()
     v_new = torch.randn(B, Hkv, Tn, D, generator=g).bfloat16()

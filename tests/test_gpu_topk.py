@@ -1,6 +1,6 @@
 """The row top-k kernel alone against the oracle's ranking (value desc, index
 asc), on rows built to stress it: heavy exact ties, short valid prefixes, and
-rows longer than one workgroup's LDS (selected in segments)."""
+rows longer than one workgroup's LDS (the multi-workgroup radix select)."""
 
 from __future__ import annotations
 
@@ -37,30 +37,12 @@ def test_topk_ties_and_prefixes(dev, n, k):
     assert np.array_equal(vals[0, 0].cpu().numpy(), rv.astype(np.float32))
 
 
-@pytest.mark.parametrize("order", [0, 1])
-def test_topk_long_rows_segmented_fallback(dev, monkeypatch, order):
-    """Long rows with the multi-workgroup kernel switched off (LA_TOPK_WIDE=0):
-    the segmented levels, the form used where a device cannot launch
-    cooperatively, give the same selection."""
-    n, k = 70000, 3000
-    g = torch.Generator().manual_seed(3)
-    sc = torch.randint(-3, 4, (1, 1, 2, n), generator=g).double()
-    sc[0, 0, 1] = torch.randn(n, generator=g, dtype=torch.float64)
-    ref_i, _ = oracle.topk_rows(sc[0, 0].numpy(), k)
-    monkeypatch.setenv("LA_TOPK_WIDE", "0")
-    ids, counts, _ = _topk(sc.to(dev), k=k, width=k, group=1, order=order, pos_offset=0,
-                           pos_unit=0, force_own=False, with_values=False)
-    got = ids[0, 0].cpu().numpy()
-    want = ref_i if order == 0 else np.sort(ref_i, axis=-1)
-    assert np.array_equal(got, want)
-
-
 @pytest.mark.parametrize("order", [1, 0])
 def test_topk_wide_many_batches_short_prefixes(dev, order):
-    """The multi-workgroup kernel over more rows than one cooperative launch
-    holds (300 rows of 65536 keys go in several batches), with valid prefixes
-    shorter than k, equal to k and in between; ascending-index (order 1) and
-    sorted (order 0) output.  The device status stays clean."""
+    """The multi-workgroup radix select over many rows (300 rows of 65536
+    keys in one call), with valid prefixes shorter than k, equal to k and in
+    between; ascending-index (order 1) and sorted (order 0) output.  The
+    device status stays clean."""
     n, k, Tq = 65536, 3000, 300
     g = torch.Generator().manual_seed(11)
     sc = torch.randint(-50, 50, (1, 1, Tq, n), generator=g).double()
@@ -80,34 +62,30 @@ def test_topk_wide_many_batches_short_prefixes(dev, order):
 
 
 @pytest.mark.parametrize("order", [1, 0])
-def test_topk_wide_timeout_is_reported(dev, monkeypatch, order):
-    """A bounded wait that runs out must not pass for a result.  With
-    LA_TOPK_WIDE_FAULT=1 no wait of the multi-workgroup kernel can be
-    satisfied, and with LA_TOPK_WIDE_SPIN=64 each gives up after 64 polls, so
-    every workgroup exits normally: every row comes back with count -1 and -1
-    ids, and the device status carries LA_DEV_TOPK_TIMEOUT.  The next call
-    without the fault is correct again."""
-    n, k, Tq = 65536, 1000, 4
-    g = torch.Generator().manual_seed(12)
-    sc = torch.randn(1, 1, Tq, n, generator=g, dtype=torch.float64).to(dev)
+def test_topk_radix_long_rows_every_depth(dev, order):
+    """Long rows of the multi-workgroup radix select (200000 keys, 49 chunks):
+    a row of equal keys (every digit pass runs, then index ties), a row of
+    keys equal above their lowest bits, a row whose valid prefix is shorter
+    than k (everything taken), an empty row, and an ordinary row.  The
+    device status stays clean, and a second call on the same scores gives the
+    same result (the per-call state starts from scratch)."""
+    n, k = 200000, 5000
+    g = torch.Generator().manual_seed(13)
+    sc = torch.randn(1, 1, 5, n, generator=g, dtype=torch.float64)
+    sc[0, 0, 0] = 0.75
+    sc[0, 0, 1] = 1.5 + torch.randint(0, 4, (n,), generator=g).double() * 2.0 ** -51
+    nv = torch.tensor([n, n, k - 7, 0, n - 3], dtype=torch.int32)
     N.device_status(dev)
-    monkeypatch.setenv("LA_TOPK_WIDE_FAULT", "1")
-    monkeypatch.setenv("LA_TOPK_WIDE_SPIN", "64")
-    ids, counts, vals = _topk(sc, k=k, width=k, group=1, order=order, pos_offset=0, pos_unit=0,
-                              force_own=False, with_values=order == 0)
-    assert N.device_status(dev) & N.LA_DEV_TOPK_TIMEOUT
-    assert (counts == -1).all() and (ids == -1).all()
-    if order == 0:
-        assert torch.isneginf(vals).all()
-    monkeypatch.delenv("LA_TOPK_WIDE_FAULT")
-    monkeypatch.delenv("LA_TOPK_WIDE_SPIN")
-    ids, counts, _ = _topk(sc, k=k, width=k, group=1, order=order, pos_offset=0, pos_unit=0,
-                           force_own=False)
-    assert N.device_status(dev) == 0
-    ri, _ = oracle.topk_rows(sc[0, 0].cpu().numpy(), k)
-    want = ri if order == 0 else np.sort(ri, axis=-1)
-    assert np.array_equal(ids[0, 0].cpu().numpy(), want)
-    assert (counts == k).all()
+    for _ in range(2):
+        ids, counts, _ = _topk(sc.to(dev), k=k, width=k, group=1, order=order, pos_offset=0,
+                               pos_unit=0, force_own=False, n_valid=nv.to(dev))
+        assert N.device_status(dev) == 0
+        ri, _ = oracle.topk_rows(sc[0, 0].numpy(), k, n_valid=nv.numpy())
+        want = ri if order == 0 else np.sort(np.where(ri < 0, n, ri), axis=-1)
+        if order == 1:
+            want = np.where(want == n, -1, want)
+        assert np.array_equal(ids[0, 0].cpu().numpy(), want)
+        assert np.array_equal(counts[0, 0].cpu().numpy(), np.minimum(nv.numpy(), k))
 
 
 def test_topk_short_rows_pad(dev):
