@@ -62,6 +62,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
@@ -113,7 +114,8 @@ struct PfKP {
   float thr_gap;  // 8 / qscale: raw-score headroom above the reference maximum
   int32_t causal, out_dt;
   const int32_t *lens;  // ragged batch: rows of sequence b (clamped to [0, T]); null: T
-  const float *kscale;  // fp8 K: per-token scales, (B, Hkv, nkb * 64), zero past T
+  const float *ks;      // fp8 K: per-token scales (B, Hkv, T) at strides s_sb, s_sh, s_st
+  int64_t s_sb, s_sh, s_st;
 };
 
 // Status bits this file's kernels raise on the current device (read through
@@ -205,63 +207,26 @@ __global__ __launch_bounds__(256) void prefill_v16_kernel(const void *v, const f
   }
 }
 
-// fp8 e4m3 K codes -> fp16 codes (exact: every e4m3 value is an fp16 value)
-// and the per-token scales into a padded row-major copy (zero past T), one
-// workgroup per 64-token block of one (b, KV head).  Output contiguous
-// (B, Hkv, T, 128) codes and (B, Hkv, nkb * 64) scales; rows past T (T_b) of
-// the codes are not written.
-__global__ __launch_bounds__(256) void prefill_kdeq_kernel(const uint8_t *k, const float *ks,
-                                                           int64_t s_sb, int64_t s_sh, int64_t s_st,
-                                                           int64_t k_sb, int64_t k_sh, int64_t k_st,
-                                                           int64_t Hkv, int64_t T, int64_t nkb,
-                                                           uint16_t *kout, float *kscale,
-                                                           const int32_t *lens) {
-  const int64_t blk = blockIdx.x;
-  const int64_t kb = blk % nkb, bh = blk / nkb;
-  const int64_t b = bh / Hkv, kvh = bh % Hkv;
-  const int tid = threadIdx.x;
-  const int64_t Tfull = T;
-  if (lens) T = min(max((int64_t)lens[b], (int64_t)0), T);
-  if (tid < PF_BS) {
-    const int64_t row = kb * PF_BS + tid;
-    kscale[bh * nkb * PF_BS + row] = row < T ? ks[b * s_sb + kvh * s_sh + row * s_st] : 0.f;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = kb * PF_BS + (tid >> 4) + 16 * i;
-    if (row >= T) continue;
-    const int col = 8 * (tid & 15);
-    const uint2 c = *(const uint2 *)(k + b * k_sb + kvh * k_sh + row * k_st + col);
-    const float2 a[4] = {fp8x2_to_f32<false>(c.x), fp8x2_to_f32<true>(c.x),
-                         fp8x2_to_f32<false>(c.y), fp8x2_to_f32<true>(c.y)};
-    uint32_t o[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a[j].x, a[j].y}), f16x2));
-    *(uint4 *)(kout + (bh * Tfull + row) * PF_D + col) = uint4{o[0], o[1], o[2], o[3]};
-  }
-}
-
-// KF16 (fp8 K/V): K staged as its fp16 codes (exact) and q converted to fp16
-// per query row (scaled by 2^-eq, the power of two that puts the row's
-// largest |q| just below 2^15), scores by fp16 MFMA; each raw score is then
-// multiplied by its key's scale.  Scores are kept in "lane units" (the true
-// score times 2^-eq of the lane's query); qs = qscale * 2^eq turns lane units
-// into the exponent.  Without KF16, qs = qscale.
-template <bool KF16>
+// KF8 (fp8 K/V): K is staged as its e4m3 codes (64 rows of 128 bytes, half
+// the bytes of a bf16 block) and scored on the fp8 matrix cores
+// (v_mfma_scale_f32_16x16x128_f8f6f4, unit block scales): q is split per
+// query row into a two-term fp8 expansion q = sq (hi + lo), sq a power of two,
+// hi = e4m3(q / sq), lo = e4m3(q / sq - hi), so a
+// score is two fp8 products into one accumulator, then multiplied by its
+// key's scale.  With sq a power of two (below) the two terms hold the bf16 q
+// exactly, so the products are those of the dequantised keys and q.  Scores
+// are kept in "lane units" (the true score / sq of the lane's query);
+// qs = qscale * sq turns lane units into the exponent.  Without KF8,
+// qs = qscale.  V (codes times scale) goes through the fp16 copy as for bf16.
+template <bool KF8>
 __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
-  auto qk_mfma = [](const bf16x8 &a, const bf16x8 &b, f32x4 c) {
-    if constexpr (KF16)
-      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-    else
-      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  };
-  // K slots 0..1, V slots 2..3 (64 KiB: two workgroups per CU); after the
-  // loop, the key-half merge area
-  __shared__ __align__(16) uint16_t smem[4 * PF_BLK];
-  // KF16: the per-key scales of the K block in each K slot (copied with it)
-  __shared__ __align__(16) float sscale[KF16 ? 2 * PF_BS : 4];
+  // K slots 0..1 (16 KiB each, KF8: 8 KiB), V slots 0..1 after them (16 KiB
+  // each): 64 / 48 KiB, two workgroups per CU; after the loop, the key-half
+  // merge area
+  constexpr int KSL = KF8 ? PF_BLK / 2 : PF_BLK;  // uint16 elements of a K slot
+  __shared__ __align__(16) uint16_t smem[2 * KSL + 2 * PF_BLK];
+  // KF8: the per-key scales of the K block in each K slot (copied with it)
+  __shared__ __align__(16) float sscale[KF8 ? 2 * PF_BS : 4];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
@@ -329,7 +294,9 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // an unsigned compare
   const uint32_t nwhole = (uint32_t)(T32 / PF_BS);
   auto whole_block = [&](int kb) { return (uint32_t)kb < nwhole; };
-  // LDS slots of PF_BLK elements: K in 0..1, V in 2..3
+  // LDS slots: K x at element kslot(x), V x at vslot(x), x in {0, 1}
+  auto kslot = [](int x) { return (uint32_t)(x * KSL); };
+  auto vslot = [](int x) { return (uint32_t)(2 * KSL + x * PF_BLK); };
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t *)smem);
   const int wu = __builtin_amdgcn_readfirstlane(w);
   // LDS-DMA of a block: instruction t of wave w fills rows 16 t + 4 w + lane/16;
@@ -345,8 +312,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     vvo[t] = (uint32_t)((((int64_t)(16 * t + drow)) * p.v_st + 8 * vdch) * 2);
   }
   auto dma_part = [&](const uint16_t *bh, int64_t st, uint32_t blk, const uint32_t (&vo)[4], int dch,
-                      int kb, int slot) {
-    const uint32_t m0 = lds0 + 2 * (slot * PF_BLK + 4 * wu * PF_D);
+                      int kb, uint32_t soff) {
+    const uint32_t m0 = lds0 + 2 * (soff + 4 * wu * PF_D);
     if (whole_block(kb)) {
       const uint16_t *base = bh + (uint32_t)kb * blk;  // fits 32 bits (checked at launch)
 #pragma unroll
@@ -362,17 +329,50 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       }
     }
   };
-  auto dma_k = [&](int kb, int slot) { dma_part(kbh, p.k_st, p.k_blk, kvo, kdch, kb, slot); };
-  auto dma_v = [&](int kb, int slot) { dma_part(vbh, p.v_st, p.v_blk, vvo, vdch, kb, slot); };
-  // rows of a landed partial block that lie past T (or all rows of a -1
-  // entry) are cleared, so masked keys hold zeros rather than copies
-  auto clear_rows = [&](int kb, int slot) {
-    uint16_t *d = smem + slot * PF_BLK;
-    for (int ch = tid; ch < PF_BS * 16; ch += PF_NT) {
-      const int r = ch >> 4;
-      if (kb < 0 || kb * PF_BS + r >= T32) *(uint4 *)(d + r * PF_D + 8 * (ch & 15)) = uint4{0, 0, 0, 0};
+  // KF8 K blocks: rows of 128 bytes (8 chunks); instruction t of wave w
+  // fills rows 32 t + 8 w + lane/8, a lane writes chunk position lane%8 of its
+  // row and fetches global chunk (lane%8) ^ (row & 7).  Byte offsets.
+  const int drow8 = 8 * w + (lane >> 3);
+  const int kdch8 = (lane & 7) ^ (drow8 & 7);
+  uint32_t k8o[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) k8o[t] = (uint32_t)(((int64_t)(32 * t + drow8)) * p.k_st + 16 * kdch8);
+  const char *kbh8 = (const char *)p.k + b * p.k_sb + kvh * p.k_sh;  // KF8: byte strides
+  auto dma_k = [&](int kb, int x) {
+    if constexpr (KF8) {
+      const uint32_t m0 = lds0 + 2 * kslot(x) + 8 * PF_D * wu;
+      if (whole_block(kb)) {
+        const char *base = kbh8 + (uint32_t)kb * p.k_blk;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(k8o[t]), "s"(base),
+                       "{m0}"(m0 + 32 * PF_D * t) : "memory");
+      } else {  // a partial last block or a -1 entry: rows clamped into [0, T)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int64_t key = min((int64_t)max(kb, 0) * PF_BS + 32 * t + drow8, Tb - 1);
+          asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(kbh8 + key * p.k_st + 16 * kdch8),
+                       "{m0}"(m0 + 32 * PF_D * t) : "memory");
+        }
+      }
+    } else {
+      dma_part(kbh, p.k_st, p.k_blk, kvo, kdch, kb, kslot(x));
     }
   };
+  auto dma_v = [&](int kb, int x) { dma_part(vbh, p.v_st, p.v_blk, vvo, vdch, kb, vslot(x)); };
+  // rows of a landed partial block that lie past T (or all rows of a -1
+  // entry) are cleared, so masked keys hold zeros rather than copies
+  auto clear_part = [&](int kb, uint32_t soff, int row_elems) {
+    uint16_t *d = smem + soff;
+    const int cpr = row_elems / 8;  // 16-byte chunks per row
+    for (int ch = tid; ch < PF_BS * cpr; ch += PF_NT) {
+      const int r = ch / cpr;
+      if (kb < 0 || kb * PF_BS + r >= T32)
+        *(uint4 *)(d + r * row_elems + 8 * (ch % cpr)) = uint4{0, 0, 0, 0};
+    }
+  };
+  auto clear_k = [&](int kb, int x) { clear_part(kb, kslot(x), KF8 ? PF_D / 2 : PF_D); };
+  auto clear_v = [&](int kb, int x) { clear_part(kb, vslot(x), PF_D); };
 
   // LDS element offsets of this lane's operand reads:
   // K: row 32 kh + c16 (+16 kt2), global chunk 4 s + g
@@ -380,6 +380,22 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   const int ksw = pf_swz_k(c16);
 #pragma unroll
   for (int s = 0; s < 4; ++s) koffs[s] = (32 * kh + c16) * PF_D + 8 * ((4 * s + g) ^ ksw);
+  // KF8 K: row 32 kh + c16 (+16 kt2), the lane's 32 codes (dims 32 g .. +31)
+  // are chunks 2 g and 2 g + 1 (byte offsets in the slot)
+  int k8offs[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) k8offs[h] = (32 * kh + c16) * PF_D + 16 * ((2 * g + h) ^ (c16 & 7));
+  auto load_k8 = [&](uint32_t soff, int kt2) {
+    const char *sk8 = (const char *)(smem + soff) + 16 * kt2 * PF_D;
+    const uint4 a0 = *(const uint4 *)(sk8 + k8offs[0]), a1 = *(const uint4 *)(sk8 + k8offs[1]);
+    return i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z,
+                 (int)a1.w};
+  };
+  // fp8 e4m3 K codes x fp8 e4m3 q terms (unit scales: e8m0 127)
+  auto mfma8 = [](const i32x8 &a, const i32x8 &b, f32x4 c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+  };
+  i32x8 qh8[2], ql8[2];  // KF8: this lane's q terms (query q_row[qg], dims 32 g .. +31)
   // V (transpose reads): row 32 kh + 4 g + c16/4 (+16), global column
   // 16 dt + 4 (c16 % 4) = chunk 2 dt + (c16/2)%2, element 4 (c16 % 2) in it
   const int vr = 4 * g + (c16 >> 2), vsw = pf_swz(vr);
@@ -388,17 +404,23 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   for (int dt = 0; dt < 8; ++dt)
     voffs[dt] = (32 * kh + vr) * PF_D + 8 * ((2 * dt + ((c16 >> 1) & 1)) ^ vsw) + 4 * (c16 & 1);
 
-  // S^T = K Q^T over this wave's 32 keys of the K block in LDS slot `slot`
-  auto scores = [&](int slot, f32x4 (&st)[2][2]) {
-    const uint16_t *sk = smem + slot * PF_BLK;
+  // S^T = K Q^T over this wave's 32 keys of the K block in LDS slot x
+  auto scores = [&](int x, f32x4 (&st)[2][2]) {
+    const uint16_t *sk = smem + kslot(x);
 #pragma unroll
     for (int kt2 = 0; kt2 < 2; ++kt2) {
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KF8) {
+        const i32x8 a = load_k8(kslot(x), kt2);
+        s0 = mfma8(a, ql8[0], mfma8(a, qh8[0], s0));
+        s1 = mfma8(a, ql8[1], mfma8(a, qh8[1], s1));
+      } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 a = *(const bf16x8 *)&sk[koffs[s] + 16 * kt2 * PF_D];
-        s0 = qk_mfma(a, qreg[0][s], s0);
-        s1 = qk_mfma(a, qreg[1][s], s1);
+        for (int s = 0; s < 4; ++s) {
+          const bf16x8 a = *(const bf16x8 *)&sk[koffs[s] + 16 * kt2 * PF_D];
+          s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[0][s], s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[1][s], s1, 0, 0, 0);
+        }
       }
       st[0][kt2] = s0;
       st[1][kt2] = s1;
@@ -409,23 +431,24 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   // per group; thr = m + thr_gap, the raw score above which m must be raised;
   // nmu = -m * qscale (0 while m = -inf), the exponent offset of the weights
   const float NEG_INF = __int_as_float(0xff800000);
-  float qs[2] = {p.qscale, p.qscale}, tg[2] = {p.thr_gap, p.thr_gap};  // KF16: per lane and group
+  float qs[2] = {p.qscale, p.qscale}, tg[2] = {p.thr_gap, p.thr_gap};  // KF8: per lane and group
   auto QS = [&](int qg) {
-    if constexpr (KF16) return qs[qg]; else return p.qscale;
+    if constexpr (KF8) return qs[qg]; else return p.qscale;
   };
   auto TG = [&](int qg) {
-    if constexpr (KF16) return tg[qg]; else return p.thr_gap;
+    if constexpr (KF8) return tg[qg]; else return p.thr_gap;
   };
-  // KF16: the 64 scales of K block kb go to LDS with its codes (wave 0: one
-  // 4-byte LDS-DMA load per lane, counted and waited for like the block
-  // copies; an empty or out-of-range entry copies block 0's, never used)
-  auto dma_ks = [&](int kb, int slot) {
-    if constexpr (KF16) {
+  // KF8: the 64 scales of K block kb go to LDS with its codes (wave 0: one
+  // 4-byte LDS-DMA load per lane from the caller's scale tensor, counted and
+  // waited for like the block copies; keys past T read the last key's scale,
+  // and an empty entry block 0's, never used)
+  auto dma_ks = [&](int kb, int x) {
+    if constexpr (KF8) {
       if (wu == 0) {
-        const uint32_t kbc = (uint32_t)kb < (uint32_t)nkb32 ? (uint32_t)kb : 0u;
-        const float *sp = p.kscale + ((b * p.Hkv + kvh) * p.nkb + kbc) * PF_BS + lane;
+        const int64_t key = min((int64_t)max(kb, 0) * PF_BS + lane, Tb - 1);
+        const float *sp = p.ks + b * p.s_sb + kvh * p.s_sh + key * p.s_st;
         const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-            (uint32_t)(uintptr_t)(lds_void_t *)(sscale + slot * PF_BS));
+            (uint32_t)(uintptr_t)(lds_void_t *)(sscale + x * PF_BS));
         asm volatile("global_load_lds_dword %0, off" ::"v"(sp), "{m0}"(m0) : "memory");
       }
     }
@@ -513,26 +536,29 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   };
   // Software pipeline over the list.  Step j computes the scores of block
   // j+1 while the weights of block j are formed, then block j's PV product
-  // while the maxima of block j+1 are taken.  K block x lives in slot x % 2
-  // and V block x in slot 2 + x % 2; both are fetched one step ahead (K of
+  // while the maxima of block j+1 are taken.  K block x lives in K slot x % 2
+  // and V block x in V slot x % 2; both are fetched one step ahead (K of
   // block j+2 and V of block j+1 during step j).  bf16 K/V: lists of up to
   // 64 entries sit in VGPR lanes (entry i in lane i, with the exponent of its
   // V block) and are read per step by v_readlane; longer lists, and every
   // list of the fp8 form (which has no registers to spare), come through the
   // scalar cache (see sload_i32).
   if (n <= 1) kb1 = 0;
-  const bool lanes = !KF16 && n <= 64;
+  const bool lanes = !KF8 && n <= 64;
   int lv = 0, evv = 0;
   if (lanes) lv = list[min(lane, n - 1)];
   dma_k(kbj, 0);
-  dma_v(kbj, 2);
+  dma_v(kbj, 0);
   if (n > 1) dma_k(kb1, 1);
-  // q, read once: streamed past the caches that keep the K/V blocks
+  // q, read once: streamed past the caches that keep the K/V blocks.  bf16:
+  // dims 32 s + 8 g .. +7 (the bf16 MFMA operand); KF8: dims 32 g + 8 s .. +7
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg) {
     const uint16_t *qp = p.q + b * p.q_sb + h * p.q_sh + min(q_row[qg], Tb - 1) * p.q_st;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qreg[qg][s] = __builtin_nontemporal_load((const bf16x8 *)(qp + 32 * s + 8 * g));
+    for (int s = 0; s < 4; ++s)
+      qreg[qg][s] = __builtin_nontemporal_load(
+          (const bf16x8 *)(qp + (KF8 ? 32 * g + 8 * s : 32 * s + 8 * g)));
   }
   dma_ks(kbj, 0);
   if (n > 1) dma_ks(kb1, 1);
@@ -543,33 +569,53 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     for (int s = 0; s < 4; ++s) settle(qreg[qg][s]);  // q landed with the first blocks
   settle(lv);
   if (lanes) evv = vexp[(uint32_t)lv < (uint32_t)nkb32 ? (uint32_t)lv : 0u];
-  if constexpr (KF16) {
-    // q row -> fp16 * 2^-eq (the row's 128 values are spread over the 4
-    // lanes c16 + 16 g: their largest |q| is taken across those lanes)
+  if constexpr (KF8) {
+    // q row -> 2^e (hi + lo) in e4m3 codes, 2^e putting the row's largest |q|
+    // in [128, 256) (its 128 values are spread over the 4 lanes c16 + 16 g).
+    // With a power-of-two scale q / 2^e keeps its bf16 significand, and two
+    // e4m3 terms hold any 8-bit significand exactly (hi its top 4 bits,
+    // rounded; lo = q / 2^e - hi a multiple of 2^-7 of hi's binade of at most
+    // 4 significant bits) while lo stays in the e4m3 range: every element
+    // of magnitude >= 2^-9 of the row's largest is represented exactly, the
+    // rest within 2^-17 of it.
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      uint32_t mb = 0;
+      float x[32];
+      float am = 0.f;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const u32x4 w = __builtin_bit_cast(u32x4, qreg[qg][s]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mb = max(mb, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
-      }
-      const float mf = pf_pair32_max(pf_pair16_max(__uint_as_float(mb << 16)));
-      const int eq = min(127, max(-100, (int)(__float_as_uint(mf) >> 23) - 141));
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4 w = __builtin_bit_cast(u32x4, qreg[qg][s]);
-        u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float lo = __builtin_amdgcn_ldexpf(bf16lo(w[e]), -eq);
-          const float hi = __builtin_amdgcn_ldexpf(bf16hi(w[e]), -eq);
-          o[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+          x[8 * s + 2 * e] = bf16lo(w[e]);
+          x[8 * s + 2 * e + 1] = bf16hi(w[e]);
         }
-        qreg[qg][s] = __builtin_bit_cast(bf16x8, o);
       }
-      qs[qg] = __builtin_amdgcn_ldexpf(p.qscale, eq);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) am = pf_max(am, fabsf(x[i]));
+      am = pf_pair32_max(pf_pair16_max(am));
+      const int e = am > 0.f ? (int)((__float_as_uint(am) >> 23) & 0xff) - 127 - 7 : 0;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = __builtin_amdgcn_ldexpf(x[i], -e);
+      // codes by round to nearest; x keeps the residual for the second term
+      auto term = [&]() {
+        i32x8 t;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          int wv = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * j], x[4 * j + 1], 0, false);
+          wv = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * j + 2], x[4 * j + 3], wv, true);
+          t[j] = wv;
+          const float2 a = fp8x2_to_f32<false>((uint32_t)wv), c = fp8x2_to_f32<true>((uint32_t)wv);
+          x[4 * j] -= a.x;
+          x[4 * j + 1] -= a.y;
+          x[4 * j + 2] -= c.x;
+          x[4 * j + 3] -= c.y;
+        }
+        return t;
+      };
+      qh8[qg] = term();
+      ql8[qg] = term();
+      qs[qg] = __builtin_amdgcn_ldexpf(p.qscale, e);
       tg[qg] = 8.f / qs[qg];
     }
   }
@@ -577,16 +623,16 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
   {
     const bool c0 = !whole_block(kbj), c1 = n > 1 && !whole_block(kb1);
     if (c0) {
-      clear_rows(kbj, 0);
-      clear_rows(kbj, 2);
+      clear_k(kbj, 0);
+      clear_v(kbj, 0);
     }
-    if (c1) clear_rows(kb1, 1);
+    if (c1) clear_k(kb1, 1);
     if (c0 || c1) lds_barrier();
   }
   // scores of blocks with even / odd list position
   f32x4 sA[2][2], sB[2][2];
   scores(0, sA);
-  if constexpr (KF16) scale_scores(sA, 0);
+  if constexpr (KF8) scale_scores(sA, 0);
   if (needs_mask(kbj)) apply_mask(kbj, sA);
   {
     float mx[2], alpha[2];
@@ -621,15 +667,21 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
       dma_k(kb2, par);
       dma_ks(kb2, par);
     }
-    if (FULL || j + 1 < n) dma_v(kb1, 2 + (par ^ 1));  // held block j-1 (multiplied)
-    const uint16_t *sk = smem + (par ^ 1) * PF_BLK;
-    const uint16_t *sv = smem + (2 + par) * PF_BLK;
+    if (FULL || j + 1 < n) dma_v(kb1, par ^ 1);  // held block j-1 (multiplied)
+    const uint16_t *sk = smem + kslot(par ^ 1);
+    const uint16_t *sv = smem + vslot(par);
     bf16x8 ka[2][4];
+    i32x8 ka8[2];
     f16x8 va[8];
+    if constexpr (KF8) {
 #pragma unroll
-    for (int kt2 = 0; kt2 < 2; ++kt2)
+      for (int kt2 = 0; kt2 < 2; ++kt2) ka8[kt2] = load_k8(kslot(par ^ 1), kt2);
+    } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ka[kt2][s] = *(const bf16x8 *)&sk[koffs[s] + 16 * kt2 * PF_D];
+      for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ka[kt2][s] = *(const bf16x8 *)&sk[koffs[s] + 16 * kt2 * PF_D];
+    }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       // V^T rows through the LDS transpose read: lane (g, j) of a 16-lane group
@@ -644,10 +696,17 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
     for (int kt2 = 0; kt2 < 2; ++kt2) {
       f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KF8) {
+        s0 = mfma8(ka8[kt2], qh8[0], s0);
+        s1 = mfma8(ka8[kt2], qh8[1], s1);
+        s0 = mfma8(ka8[kt2], ql8[0], s0);
+        s1 = mfma8(ka8[kt2], ql8[1], s1);
+      } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        s0 = qk_mfma(ka[kt2][s], qreg[0][s], s0);
-        s1 = qk_mfma(ka[kt2][s], qreg[1][s], s1);
+        for (int s = 0; s < 4; ++s) {
+          s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kt2][s], qreg[0][s], s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kt2][s], qreg[1][s], s1, 0, 0, 0);
+        }
       }
       sn[0][kt2] = s0;
       sn[1][kt2] = s1;
@@ -687,20 +746,30 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg)
         acc[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], ph[qg], acc[qg][dt], 0, 0, 0);
-    // KF16: the key scales of block j+1, applied with its maxima (its scores
+    // KF8: the key scales of block j+1, applied with its maxima (its scores
     // are ready by then; applied right after the score products, the
     // multiplies would wait for the matrix core)
-    if constexpr (KF16) scale_scores(sn, par ^ 1);
+    if constexpr (KF8) scale_scores(sn, par ^ 1);
     float mx[2];
     lane_max(sn, mx);
-    // order within the block: the 24 LDS reads, then the 16 score MFMAs each
-    // followed by weight VALU work, then the 16 PV MFMAs each followed by
-    // VALU work of the next block's maxima
-    __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);
+    // order within the block: the LDS reads (24, KF8: 20), then the score
+    // MFMAs (16, KF8: 8 of twice the work) each followed by weight VALU work,
+    // then the 16 PV MFMAs each followed by VALU work of the next block's
+    // maxima
+    if constexpr (KF8) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 20, 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      }
+    } else {
+      __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -722,8 +791,8 @@ __global__ __launch_bounds__(PF_NT, 2) void prefill_kernel(PfKP p) {
     const bool ck = (FULL || j + 2 < n) && !whole_block(kb2);
     const bool cv = (FULL || j + 1 < n) && !whole_block(kb1);
     if (ck || cv) {
-      if (ck) clear_rows(kb2, par);
-      if (cv) clear_rows(kb1, 2 + (par ^ 1));
+      if (ck) clear_k(kb2, par);
+      if (cv) clear_v(kb1, par ^ 1);
       lds_barrier();
     }
     kbj = kb1;
@@ -862,17 +931,13 @@ int prefill_status(uint32_t *bits, bool clear, hipStream_t st) {
 
 static int64_t pf_align(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Workspace: the fp16 copy of V (B, Hkv, T, 128), then the block exponents.
 static bool prefill_fp8(const la_prefill_args *a) { return a->kv_dtype == LA_FP8_E4M3; }
 
-// Workspace: the fp16 copy of V (B, Hkv, T, 128) and its block exponents;
-// for fp8 K/V also the fp16 K codes (B, Hkv, T, 128) and the padded K scales
-// (B, Hkv, nkb * 64).
+// Workspace: the fp16 copy of V (B, Hkv, T, 128) and its block exponents
+// (fp8 K is staged from the caller's codes and scales directly).
 static int64_t prefill_ws_bytes(const la_prefill_args *a) {
   const int64_t nkb = ceil_div(a->T, PF_BS);
-  const int64_t kv = pf_align(a->B * a->Hkv * a->T * PF_D * 2);
-  const int64_t ex = pf_align(a->B * a->Hkv * nkb * 4);
-  return kv + ex + (prefill_fp8(a) ? kv + pf_align(a->B * a->Hkv * nkb * PF_BS * 4) : 0);
+  return pf_align(a->B * a->Hkv * a->T * PF_D * 2) + pf_align(a->B * a->Hkv * nkb * 4);
 }
 
 static int prefill_validate(const la_prefill_args *a) {
@@ -887,11 +952,13 @@ static int prefill_validate(const la_prefill_args *a) {
   LA_REQUIRE(a->scale > 0.f, "la_block_sparse_prefill: scale must be positive");
   if (prefill_fp8(a)) {
     LA_REQUIRE(a->k_scale && a->v_scale, "la_block_sparse_prefill: fp8 K/V need k_scale and v_scale");
-    // 8-byte code loads; element strides are bytes for fp8
-    const bool al8 = (uintptr_t)a->k % 8 == 0 && (uintptr_t)a->v % 8 == 0 && a->k_sb % 8 == 0 &&
-                     a->k_sh % 8 == 0 && a->k_st % 8 == 0 && a->v_sb % 8 == 0 && a->v_sh % 8 == 0 &&
-                     a->v_st % 8 == 0;
-    LA_REQUIRE(al8, "la_block_sparse_prefill: fp8 rows must be contiguous and 8-byte aligned");
+    // K rows go to LDS in 16-byte pieces, V codes are read 8 bytes at a time;
+    // element strides are bytes for fp8
+    const bool al8 = (uintptr_t)a->k % 16 == 0 && (uintptr_t)a->v % 8 == 0 && a->k_sb % 16 == 0 &&
+                     a->k_sh % 16 == 0 && a->k_st % 16 == 0 && a->v_sb % 8 == 0 &&
+                     a->v_sh % 8 == 0 && a->v_st % 8 == 0;
+    LA_REQUIRE(al8, "la_block_sparse_prefill: fp8 rows must be contiguous, K 16-byte and V 8-byte "
+                    "aligned");
   } else {
     const bool alk = (uintptr_t)a->k % 16 == 0 && (uintptr_t)a->v % 16 == 0 && a->k_sb % 8 == 0 &&
                      a->k_sh % 8 == 0 && a->k_st % 8 == 0 && a->v_sb % 8 == 0 && a->v_sh % 8 == 0 &&
@@ -937,20 +1004,9 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
     prefill_v16_kernel<false><<<dim3((unsigned)nvb), 256, 0, st>>>(
         a->v, nullptr, 0, 0, 0, a->v_sb, a->v_sh, a->v_st, a->Hkv, a->T, nkb, v16, vexp, a->lengths);
   LA_LAUNCHED();
-  // fp8 K: dequantized once into fp16 with block exponents, staged like bf16 K
-  char *ws_k = (char *)a->workspace + pf_align(a->B * a->Hkv * a->T * PF_D * 2) +
-               pf_align(a->B * a->Hkv * nkb * 4);
-  uint16_t *kdq = f8 ? (uint16_t *)ws_k : nullptr;
-  float *kscale = f8 ? (float *)(ws_k + pf_align(a->B * a->Hkv * a->T * PF_D * 2)) : nullptr;
-  if (f8) {
-    prefill_kdeq_kernel<<<dim3((unsigned)nvb), 256, 0, st>>>(
-        (const uint8_t *)a->k, a->k_scale, a->s_sb, a->s_sh, a->s_st, a->k_sb, a->k_sh, a->k_st,
-        a->Hkv, a->T, nkb, kdq, kscale, a->lengths);
-    LA_LAUNCHED();
-  }
   PfKP p{};
   p.q = (const uint16_t *)a->q;
-  p.k = f8 ? kdq : (const uint16_t *)a->k;
+  p.k = (const uint16_t *)a->k;  // fp8: the codes, addressed in bytes
   p.v = v16;
   p.vexp = vexp;
   p.out = a->out;
@@ -961,11 +1017,7 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   p.Hkv = a->Hkv;
   p.T = a->T;
   p.q_sb = a->q_sb; p.q_sh = a->q_sh; p.q_st = a->q_st;
-  if (f8) {
-    p.k_st = PF_D; p.k_sh = a->T * PF_D; p.k_sb = a->Hkv * a->T * PF_D;
-  } else {
-    p.k_sb = a->k_sb; p.k_sh = a->k_sh; p.k_st = a->k_st;
-  }
+  p.k_sb = a->k_sb; p.k_sh = a->k_sh; p.k_st = a->k_st;
   p.v_st = PF_D; p.v_sh = a->T * PF_D; p.v_sb = a->Hkv * a->T * PF_D;
   LA_REQUIRE(nkb * PF_BS * std::max<int64_t>(p.k_st, PF_D) < ((int64_t)1 << 31),
              "la_block_sparse_prefill: K rows of one head span >= 2^31 elements");
@@ -984,7 +1036,10 @@ extern "C" int la_block_sparse_prefill(const la_prefill_args *a, void *stream) {
   p.causal = a->causal;
   p.out_dt = a->out_dtype;
   p.lens = a->lengths;
-  p.kscale = kscale;
+  if (f8) {
+    p.ks = a->k_scale;
+    p.s_sb = a->s_sb; p.s_sh = a->s_sh; p.s_st = a->s_st;
+  }
   const int64_t nwg = a->B * a->Hq * p.nqb;
   LA_REQUIRE(nwg < ((int64_t)1 << 31), "la_block_sparse_prefill: too many query blocks");
   if (f8)

@@ -351,9 +351,11 @@ def test_ragged_batch_equals_one_call_per_sequence(dev):
 def test_prefill_fp8_kv_matches_dequantised_oracle(dev, T, hq, hkv):
     """fp8 e4m3 K/V with per-token scales (kv/quant.py:76-109): the prefill
     equals fp64 attention over the dequantised cache (codes times scales, the
-    oracle's fp8 reader) within 2e-3, inside the 1e-2 fp8 gate: the K codes
-    are scored exactly (fp16 MFMA against q converted per row to fp16) and
-    each score times its key's scale; V is dequantised into fp16."""
+    oracle's fp8 reader) within 2e-3, inside the 1e-2 fp8 gate of the north
+    star.  The K codes are scored on the fp8 matrix cores against q as a
+    two-term fp8 expansion per query row with a power-of-two scale (which
+    holds a bf16 q exactly), each score times its key's scale; V is
+    dequantised into fp16."""
     from linattn_amd.kernels.paged_decode import quantize_fp8_per_token
     q, k, v = c3_inputs(1, hq, hkv, T, 128, seed=21)
     kc, ks = quantize_fp8_per_token(k.float())
