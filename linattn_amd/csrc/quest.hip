@@ -276,20 +276,26 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
 // is selected from there (register radix select) into a union bitmap, which
 // is written in ascending page order.  Equals quest_scores_kernel followed by
 // the union top-k, without the score rows leaving the chip.
+// qs_nt threads: up to 2048 pages, eight waves score two pages each (four
+// waves per SIMD with two workgroups per CU hide the metadata reads and the
+// fp64 work behind each other); longer rows keep four waves, whose selecting
+// wave holds 64 keys per lane.  One wave per head selects.
+template <int KPT> constexpr int qs_nt() { return KPT <= 8 ? 512 : TK_NT; }
 template <int MT, int G, int KPT>
-__global__ __launch_bounds__(TK_NT) void quest_select_kernel(QsKP a) {
+__global__ __launch_bounds__(qs_nt<KPT>()) void quest_select_kernel(QsKP a) {
+  constexpr int QS_NT = qs_nt<KPT>();
   extern __shared__ __align__(16) uint64_t keys[];  // [G][NP]
   __shared__ double qd[G * 256];
-  __shared__ uint32_t wtmp[TK_NW];
+  __shared__ uint32_t wtmp[QS_NT / 64];
   __shared__ uint32_t bm[TK_NT * KPT / 32];
   const int64_t row = blockIdx.x;  // (b, kvh, t)
   const int64_t t = row % a.Tq;
   const int64_t kvh = (row / a.Tq) % a.Hkv;
   const int64_t b = row / (a.Tq * a.Hkv);
   int32_t n_v, own;
-  quest_select_union<MT, G, KPT>(a, b, kvh, t, keys, qd, bm, n_v, own);
-  tk_emit_bitmap_row(bm, n_v, own, 0, 0, a.width, a.out_idx + row * a.width,
-                     a.out_count ? a.out_count + row : nullptr, wtmp);
+  quest_select_union<MT, G, KPT, QS_NT, QS_NT>(a, b, kvh, t, keys, qd, bm, n_v, own);
+  tk_emit_bitmap_row<QS_NT>(bm, n_v, own, 0, 0, a.width, a.out_idx + row * a.width,
+                            a.out_count ? a.out_count + row : nullptr, wtmp);
 }
 
 template <int MT, int G>
@@ -417,7 +423,7 @@ static int launch_select(const QsKP &k, int64_t rows, hipStream_t st) {
       attr_set = true;
     }
   }
-  quest_select_kernel<MT, G, KPT><<<dim3((unsigned)rows), TK_NT, bytes, st>>>(k);
+  quest_select_kernel<MT, G, KPT><<<dim3((unsigned)rows), qs_nt<KPT>(), bytes, st>>>(k);
   LA_LAUNCHED();
   return LA_OK;
 }

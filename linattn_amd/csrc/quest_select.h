@@ -29,19 +29,34 @@ __device__ __forceinline__ float4 ntl(const float4 *p) {
   const v4f x = __builtin_nontemporal_load((const v4f *)p);
   return float4{x[0], x[1], x[2], x[3]};
 }
+__device__ __forceinline__ uint32_t ntl(const uint32_t *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ float2 ntl(const float2 *p) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f x = __builtin_nontemporal_load((const v2f *)p);
+  return float2{x[0], x[1]};
+}
+
+// Metadata vector of PPT consecutive pages (page-minor layout).
+template <int MT, int PPT> struct QsVec;
+template <> struct QsVec<LA_BF16, 4> { using T = uint2; };
+template <> struct QsVec<LA_BF16, 2> { using T = uint32_t; };
+template <> struct QsVec<LA_F32, 4> { using T = float4; };
+template <> struct QsVec<LA_F32, 2> { using T = float2; };
 
 // The union selection of one (b, KV head, query t) row: fp64 upper-bound
-// scores of every page for the G query heads (the first 256 threads of the
-// NT-thread workgroup, four pages x G heads each), the own page forced, each head's
-// top-k OR'd into the bitmap bm by one wave per head.  keys [G][256 KPT]
-// and qd [G][256] are scratch.  Every thread of the workgroup takes part in
-// the barriers; n_v (visible pages) and own (the own page) are returned.
-template <int MT, int G, int KPT, int NT = TK_NT>
+// scores of every page for the G query heads (the first SNT threads of the
+// NT-thread workgroup, 1024 / SNT pages x G heads each), the own page forced,
+// each head's top-k OR'd into the bitmap bm by one wave per head.  keys
+// [G][256 KPT] and qd [G][256] are scratch.  Every thread of the workgroup
+// takes part in the barriers; n_v (visible pages) and own (the own page) are
+// returned.
+template <int MT, int G, int KPT, int NT = TK_NT, int SNT = TK_NT>
 __device__ __forceinline__ void quest_select_union(const QsKP &a, int64_t b, int64_t kvh, int64_t t,
                                                    uint64_t *keys, double *qd, uint32_t *bm,
                                                    int32_t &n_v_out, int32_t &own_out) {
   constexpr int NP = TK_NT * KPT;  // pages held (>= n_pages)
-  constexpr int PPT = 4, QD = 8;
+  constexpr int PPT = 4 * TK_NT / SNT, QD = 8;
+  static_assert(SNT <= NT && (PPT == 2 || PPT == 4), "scoring threads");
   const int tid = threadIdx.x;
   const int64_t D = a.D;
   for (int64_t i = tid; i < G * D; i += NT) {
@@ -57,15 +72,15 @@ __device__ __forceinline__ void quest_select_union(const QsKP &a, int64_t b, int
   n_v_out = n_v;
   own_out = own;
   __syncthreads();
-  if (NT == TK_NT || tid < TK_NT) {  // (wave-uniform)
+  if (NT == SNT || tid < SNT) {  // (wave-uniform)
 
-  using V = typename std::conditional<MT == LA_BF16, uint2, float4>::type;
+  using V = typename QsVec<MT, PPT>::T;
   constexpr int ESZ = MT == LA_BF16 ? 2 : 4;
   const int64_t mbase = b * a.m_sb + kvh * a.m_sh;
   const int Dn = (int)D;
   const int sd = (int)(a.m_sd / PPT);  // vectors per d step
-  for (int c = 0; c < KPT / 4; ++c) {
-    const int p0 = c * TK_NT * PPT + tid * PPT;
+  for (int c = 0; c < NP / (SNT * PPT); ++c) {
+    const int p0 = c * SNT * PPT + tid * PPT;
     double acc[G][PPT];
 #pragma unroll
     for (int g = 0; g < G; ++g)
@@ -85,10 +100,14 @@ __device__ __forceinline__ void quest_select_union(const QsKP &a, int64_t b, int
         }
       };
       auto widen = [](const V &v, double (&x)[PPT]) {
-        if constexpr (MT == LA_BF16) {
+        if constexpr (MT == LA_BF16 && PPT == 4) {
           x[0] = bf16lo(v.x); x[1] = bf16hi(v.x); x[2] = bf16lo(v.y); x[3] = bf16hi(v.y);
-        } else {
+        } else if constexpr (MT == LA_BF16) {
+          x[0] = bf16lo(v); x[1] = bf16hi(v);
+        } else if constexpr (PPT == 4) {
           x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+        } else {
+          x[0] = v.x; x[1] = v.y;
         }
       };
       auto consume = [&](int d0, int buf) {

@@ -15,7 +15,9 @@ __device__ __forceinline__ uint64_t lanemask_lt(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-// Inclusive scan of one value per thread across the workgroup.
+// Inclusive scan of one value per thread across a workgroup of NT threads
+// (wtmp holds NT / 64 words).
+template <int NT = TK_NT>
 __device__ __forceinline__ uint32_t tk_block_incl_scan(uint32_t v, uint32_t *wtmp, uint32_t &total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
@@ -27,7 +29,7 @@ __device__ __forceinline__ uint32_t tk_block_incl_scan(uint32_t v, uint32_t *wtm
   __syncthreads();
   uint32_t base = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < TK_NW; ++i) {
+  for (int i = 0; i < NT / 64; ++i) {
     const uint32_t x = wtmp[i];
     base += (i < w) ? x : 0u;
     tot += x;
@@ -479,6 +481,7 @@ __device__ __forceinline__ void tk_wave_select_bits(const uint64_t (&u_in)[KPL],
 // out[0, width), -1 padded; *count (if given) gets the number kept.  With
 // cand (a candidate row of a segmented top-k), slot i stands for unit
 // cand[i]: slots whose candidate is -1 are dropped and cand[i] is written.
+template <int NT = TK_NT>
 __device__ __forceinline__ void tk_emit_bitmap_row(uint32_t *bm, int64_t n_v, int64_t own,
                                                    int64_t sink, int64_t window, int64_t width,
                                                    int32_t *out, int32_t *count, uint32_t *wtmp,
@@ -486,17 +489,17 @@ __device__ __forceinline__ void tk_emit_bitmap_row(uint32_t *bm, int64_t n_v, in
   const int tid = threadIdx.x;
   if (n_v > 0) {
     const int64_t s_end = min(sink, n_v);
-    for (int64_t i = tid; i < s_end; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+    for (int64_t i = tid; i < s_end; i += NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
     if (window > 0 && own >= 0) {
       const int64_t w0 = max((int64_t)0, own - window + 1);
       const int64_t w1 = min(own, n_v - 1);
-      for (int64_t i = w0 + tid; i <= w1; i += TK_NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
+      for (int64_t i = w0 + tid; i <= w1; i += NT) atomicOr(&bm[i >> 5], 1u << (i & 31));
     }
   }
   __syncthreads();
   // each thread owns a run of bitmap words
   const int64_t words = (n_v + 31) / 32;
-  const int64_t wpt = (words + TK_NT - 1) / TK_NT;
+  const int64_t wpt = (words + NT - 1) / NT;
   const int64_t w_beg = min(words, (int64_t)tid * wpt), w_end = min(words, w_beg + wpt);
   uint32_t cnt = 0;
   for (int64_t x = w_beg; x < w_end; ++x) {
@@ -512,7 +515,7 @@ __device__ __forceinline__ void tk_emit_bitmap_row(uint32_t *bm, int64_t n_v, in
     cnt += __popc(bm[x]);
   }
   uint32_t total;
-  const uint32_t incl = tk_block_incl_scan(cnt, wtmp, total);
+  const uint32_t incl = tk_block_incl_scan<NT>(cnt, wtmp, total);
   uint32_t pos = incl - cnt;
   for (int64_t x = w_beg; x < w_end; ++x) {
     uint32_t bits = bm[x];
@@ -523,7 +526,7 @@ __device__ __forceinline__ void tk_emit_bitmap_row(uint32_t *bm, int64_t n_v, in
       bits &= bits - 1;
     }
   }
-  for (int64_t jj = (int64_t)total + tid; jj < width; jj += TK_NT) out[jj] = -1;
+  for (int64_t jj = (int64_t)total + tid; jj < width; jj += NT) out[jj] = -1;
   if (count && tid == 0) *count = (int32_t)min((int64_t)total, width);
 }
 
