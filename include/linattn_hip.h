@@ -47,7 +47,9 @@ enum {
 
 /* device status bits (la_device_status) */
 enum {
-  LA_DEV_TOPK_TIMEOUT = 1,  /* a bounded wait of the multi-workgroup top-k ran out */
+  LA_DEV_TOPK_TIMEOUT = 1,  /* the multi-workgroup top-k's last workgroup of a stage waited
+                               past its bound for atomics already issued (a hardware fault
+                               guard: that wait depends on no other workgroup running) */
   LA_DEV_PREFILL_RANGE = 2  /* la_block_sparse_prefill met a finite |v| >= 2^22 (outputs inf;
                               the Python wrapper raises ValueError) */
 };
@@ -61,9 +63,10 @@ int la_abi_version(void);
  * them in the same atomic exchange (a bit raised meanwhile by another stream's
  * kernel is kept for the next read).
  * Kernels report failures they detect on the device here instead of through a
- * return code (a launch returns before the kernel runs): a row of
- * la_topk_rows / la_indexer_topk whose multi-workgroup selection timed out
- * comes back with count -1 and -1 ids, and LA_DEV_TOPK_TIMEOUT is raised.
+ * return code (a launch returns before the kernel runs): a long row of
+ * la_topk_rows / la_indexer_topk whose multi-workgroup selection hit that
+ * guard comes back with -1 ids (and count -1 in index order), and
+ * LA_DEV_TOPK_TIMEOUT is raised.
  * No counterpart in the reference (its kernels report nothing).  Synchronous.
  */
 int la_device_status(uint32_t *bits, int32_t clear, void *stream);

@@ -38,6 +38,10 @@ struct IdxKP {
   int64_t offset;
   int64_t unit;  // tokens per key (pooled groups); key s starts at token s*unit
   int32_t dt, causal;
+  // one query per chunk only (may be null): the radix top-k's first-digit
+  // histogram of each batch row, [b * hist_stride + bin], fed with the valid keys
+  uint32_t *hist0;
+  int64_t hist_stride;
 };
 
 constexpr int IT_Q = 64, IT_K = 128, IT_D = 64;  // tile, d slice
@@ -390,8 +394,9 @@ __device__ __forceinline__ void wait_chunks(u32x4 (&v)[CH]) {
   }
 }
 
-static size_t decode16_lds(int64_t tn, int64_t HI, int64_t d) {
-  return (size_t)(4 * 64 * (2 * d + 16) + ((tn * HI * d + 3) & ~3) * 4 + tn * HI * 8);
+static size_t decode16_lds(int64_t tn, int64_t HI, int64_t d, bool hist0) {
+  return (size_t)(4 * 64 * (2 * d + 16) + ((tn * HI * d + 3) & ~3) * 4 + tn * HI * 8) +
+         (hist0 ? RX_BINS * 4 : 0);
 }
 
 // waves per SIMD the registers are sized for (two tiles of 16-byte chunks in
@@ -419,6 +424,16 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
   unsigned char *rows = smem + w * 64 * hs;              // this wave's KW rows of HI segments
   float *sqf = (float *)(smem + 4 * 64 * hs);            // q [tn][hd] (fp32: exact for 2-byte inputs)
   double *sw = (double *)(sqf + ((tn * hd + 3) & ~3));   // head weights [tn][HI]
+  uint32_t *lh = (uint32_t *)(sw + tn * HI);             // first-digit histogram (hist0)
+  const bool hist = TN1 && p.hist0 != nullptr;
+  // the keys the top-k sees: a causal decode query at pos sees keys s <= pos / unit
+  int64_t n_v = p.Tk;
+  if (p.causal) {
+    const int64_t pos = p.offset + p.t0;
+    n_v = pos >= 0 ? min(p.Tk, pos / p.unit + 1) : 0;
+  }
+  if (hist)
+    for (int i = tid; i < RX_BINS; i += 256) lh[i] = 0u;
   const uint16_t *kb = (const uint16_t *)p.k + b * p.k_sb;
   // wave tiles of this workgroup: [wt0, wt0 + 4 * tiles * HI / ... ) interleaved over waves
   const int64_t n_wt = (p.Tk + KW - 1) / KW;
@@ -433,7 +448,17 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
   for (int i = tid; i < tn * HI; i += 256)
     sw[i] = (double)p.w[b * p.w_sb + (p.t0 + i / HI) * p.w_st + (i % HI) * p.w_sh];
   __syncthreads();
-  if (nw == 0) return;  // whole wave; no barrier follows
+  if (nw == 0) {  // no tiles for this wave: only the histogram's flush remains
+    if (hist) {
+      __syncthreads();
+      for (int i = tid; i < RX_BINS; i += 256) {
+        const uint32_t x = lh[i];
+        if (x) __hip_atomic_fetch_add(&p.hist0[b * p.hist_stride + i], x, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    return;
+  }
   // chunk i of lane l in the coalesced load of a wave tile: c = i*64 + l of
   // the tile's KW x cpr chunks (past the end: the tile's last chunk again).
   // The loads past the wave's last tile (issued so that every step waits for
@@ -503,6 +528,7 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
         acc = add_product(acc, sw[tl * HI + hh], rl);
       }
       if (h == 0 && s < p.Tk) p.scores[(b * p.tn + tl) * p.Tk + s] = acc;
+      if (hist && h == 0 && s < n_v) atomicAdd(&lh[(uint32_t)(ord_key(acc) >> (64 - RX_RB))], 1u);
     }
   };
   u32x4 va[CH];
@@ -531,6 +557,14 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
     }
   }
   wait_vmcnt<0>();  // drain the last (repeated) loads before the wave ends
+  if (hist) {
+    __syncthreads();
+    for (int i = tid; i < RX_BINS; i += 256) {
+      const uint32_t x = lh[i];
+      if (x) __hip_atomic_fetch_add(&p.hist0[b * p.hist_stride + i], x, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 template <int HI, bool TN1, bool BF>
@@ -550,7 +584,7 @@ static int launch_decode16(const IdxKP &p, size_t lds, dim3 grid, int tiles, hip
 
 template <int HI>
 static int dispatch_decode16(const IdxKP &p, hipStream_t st) {
-  const size_t lds = decode16_lds(p.tn, HI, p.d);
+  const size_t lds = decode16_lds(p.tn, HI, p.d, p.hist0 != nullptr);
   // a few workgroups per CU (by LDS, at most 4), each walking consecutive
   // 64-key steps of one batch row
   const int64_t per_cu = std::max<int64_t>(
@@ -664,8 +698,18 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     p.dt = a->in_dtype;
     p.causal = a->causal;
     p.unit = std::max<int64_t>(1, a->causal_unit);
+    const TopkKParams tp = topk_params(a, p.scores, t0, p.tn);
+    void *tws = (char *)a->workspace + sc_bytes;
+    // a decode step whose rows go to the multi-workgroup radix select: the
+    // scores kernel histograms the first digit on the way
+    const RadixPlan R = decode16 && p.tn == 1 ? topk_long_plan(tp) : RadixPlan{};
+    if (R.C > 0) {
+      rc = topk_radix_setup(tp, R, tws, true, st);
+      if (rc != LA_OK) return rc;
+      p.hist0 = radix_hist0(tp, tws);
+      p.hist_stride = radix_hist_stride();
+    }
     if (decode16) {
-      int rc;
       switch (a->HI) {
         case 1: rc = dispatch_decode16<1>(p, st); break;
         case 2: rc = dispatch_decode16<2>(p, st); break;
@@ -688,8 +732,8 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
         indexer_tile_kernel<<<grid, IT_NT, 0, st>>>(p);
     }
     LA_LAUNCHED();
-    rc = topk_launch_ws(topk_params(a, p.scores, t0, p.tn), (char *)a->workspace + sc_bytes,
-                        a->ws_bytes - sc_bytes, st);
+    rc = R.C > 0 ? topk_radix_finish(tp, R, tws, true, st)
+                 : topk_launch_ws(tp, tws, a->ws_bytes - sc_bytes, st);
     if (rc != LA_OK) return rc;
   }
   return LA_OK;

@@ -84,8 +84,22 @@ __device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
 struct RadixPlan {
   int64_t C = 0, bytes = 0;
 };
+constexpr int RX_RB = 11;  // radix digit bits
+constexpr int RX_BINS = 1 << RX_RB;
 RadixPlan radix_plan(const TopkKParams &p);
 int topk_radix_launch(const TopkKParams &p, const RadixPlan &R, void *ws, hipStream_t st);
+// The same in two parts, for a scores kernel that histograms the first digit
+// (the top RX_RB bits of ord_key of every valid key of row gi, added into
+// radix_hist0(p, ws)[gi * radix_hist_stride() + bin]) between them.
+int topk_radix_setup(const TopkKParams &p, const RadixPlan &R, void *ws, bool hist0_external,
+                     hipStream_t st);
+int topk_radix_finish(const TopkKParams &p, const RadixPlan &R, void *ws, bool hist0_external,
+                      hipStream_t st);
+uint32_t *radix_hist0(const TopkKParams &p, void *ws);
+int64_t radix_hist_stride();
+// The radix plan when topk_launch_ws sends these rows to the radix select
+// (else C = 0).
+RadixPlan topk_long_plan(const TopkKParams &p);
 
 // Workspace bytes topk_launch_ws needs (rows longer than the LDS can hold go
 // to the multi-workgroup radix select).

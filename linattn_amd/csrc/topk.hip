@@ -931,6 +931,10 @@ static bool long_plain(const TopkKParams &p) {
   return plain && p.n * 8 + p2 * 12 + 64 > lds_limit();
 }
 
+RadixPlan topk_long_plan(const TopkKParams &p) {
+  return long_plain(p) ? radix_plan(p) : RadixPlan{};
+}
+
 int64_t topk_workspace_bytes(const TopkKParams &p) {
   if (long_plain(p)) {
     const RadixPlan R = radix_plan(p);

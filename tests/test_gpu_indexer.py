@@ -97,6 +97,28 @@ def test_indexer_decode_form(dev, tq, hi, d, dtype):
     check(q, k, w, 512, dev, causal=True, offset=5000 - tq)
 
 
+@pytest.mark.parametrize("offset,kk,sorted_", [
+    (50000, 4096, True),     # causal row, threshold above the ReLU zeros
+    (50000, 4096, False),
+    (50000, 48000, False),   # threshold among the tied zeros: lowest indices first
+    (4200, 4096, True),      # the same, sorted (4201 visible keys, about 260 zeros)
+    (None, 4096, True),      # every key visible
+    (None, 69990, False),
+])
+def test_indexer_decode_long_row(dev, offset, kk, sorted_):
+    """One query against 70000 keys: the multi-workgroup radix select, with
+    the first digit histogrammed by the scores kernel."""
+    q, k, w = inputs(2, 1, 70000, 4, 64, seed=31, dtype=torch.bfloat16)
+    causal = offset is not None
+    if sorted_:
+        check(q, k, w, kk, dev, causal=causal, offset=offset or 0)
+        return
+    val, idx = indexer_topk(q.to(dev), k.to(dev), w.to(dev), kk, causal=causal,
+                            offset=offset or 0, sorted=False)
+    _, ri = oracle.indexer_topk(q, k, w, kk, causal=causal, offset=offset or 0)
+    assert np.array_equal(idx.cpu().numpy(), index_order(ri))
+
+
 def test_indexer_summation_order_is_sequential(dev):
     """The tiled score kernel adds q.k products over d in increasing order
     (the matrix-core form relies on gfx950's in-order fp64 accumulation).
