@@ -537,7 +537,12 @@ int la_block_means(const la_block_means_args *a, void *stream);
  * -i mod block: block dense gram products per head, in-order fp64
  * accumulation over d, the same bits) and the selection reads the slots from
  * the workspace; otherwise the selection kernel scores every slot itself.
- * la_xattn_select_workspace() returns 0 when no workspace is used.
+ * The slots of a chunk of query blocks are scored and then selected, chunk
+ * after chunk: la_xattn_select_workspace() sizes the chunk so that its slots
+ * take at most 256 MiB (at least one chunk of 64 query blocks), and a smaller
+ * workspace (B*Hq*64*n_kb*n_slots*8 bytes or more) gives smaller chunks with
+ * the same lists.  la_xattn_select_workspace() returns 0 when no workspace
+ * is used.
  */
 typedef struct {
   const void *q;

@@ -69,12 +69,15 @@ struct XaKP {
   const void *q, *k;
   int32_t *out_idx, *out_count;
   const double *alpha;  // per query head (threshold mode)
-  double *slots;        // optional: [b][h][qb][kb][slot] scored by xattn_slots_mfma_kernel
+  double *slots;        // optional: [b][h][qb - qc0][kb][slot] scored by xattn_slots_mfma_kernel
   int64_t B, Hq, Hkv, Tq, T, D;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st;
   int64_t blk, r, n_slots, offset, n_qb, n_kb, topk, width;
   double inv_sqrt_d, two_f;
   int32_t in_dt, mode;  // mode 0: threshold, 1: top-k
+  // the launch covers query blocks [qc0, qc0 + n_qc) (rows (b, h, qb) of
+  // that range, numbered b, h, qb - qc0 within the launch)
+  int64_t qc0, n_qc;
 };
 
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t *red) {
@@ -150,12 +153,13 @@ __global__ __launch_bounds__(XM_NT, 3) void xattn_slots_mfma_kernel(XaKP p) {
   __shared__ __align__(16) float sk[XM_T][XM_S];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r16 = lane & 15, kq = lane >> 4;
-  const int64_t kb0 = (int64_t)blockIdx.x * XM_T, qb0 = (int64_t)blockIdx.y * XM_T;
+  const int64_t kb0 = (int64_t)blockIdx.x * XM_T, qb0 = p.qc0 + (int64_t)blockIdx.y * XM_T;
+  const int64_t qend = p.qc0 + p.n_qc;  // first query block past the launch's range
   const int64_t bh = blockIdx.z, b = bh / p.Hq, h = bh % p.Hq, kvh = h / (p.Hq / p.Hkv);
   const int64_t blk = p.blk;
   const int D = (int)p.D;
-  if (qb0 >= p.n_qb) return;
-  const int64_t qlast = min(qb0 + XM_T, p.n_qb) - 1;
+  if (qb0 >= qend) return;
+  const int64_t qlast = min(qb0 + XM_T, qend) - 1;
   if (kb0 * blk > qlast * blk + p.offset) return;  // every key block past causality
   const uint16_t *qbase = (const uint16_t *)p.q + b * p.q_sb + h * p.q_sh;
   const uint16_t *kbase = (const uint16_t *)p.k + b * p.k_sb + kvh * p.k_sh;
@@ -169,7 +173,7 @@ __global__ __launch_bounds__(XM_NT, 3) void xattn_slots_mfma_kernel(XaKP p) {
       const int c = tid + u * XM_NT, r = c >> 3, dc = c & 7;
       const int dd = min(d0 + dc * 8, D - 8);
       const int64_t t = (qb0 + r) * blk + i, s = (kb0 + r) * blk + j;
-      lq[u] = (qb0 + r < p.n_qb && t < p.Tq) ? *(const uint4 *)(qbase + t * p.q_st + dd)
+      lq[u] = (qb0 + r < qend && t < p.Tq) ? *(const uint4 *)(qbase + t * p.q_st + dd)
                                               : uint4{0u, 0u, 0u, 0u};
       lk[u] = (kb0 + r < p.n_kb && s < p.T) ? *(const uint4 *)(kbase + s * p.k_st + dd)
                                              : uint4{0u, 0u, 0u, 0u};
@@ -197,8 +201,8 @@ __global__ __launch_bounds__(XM_NT, 3) void xattn_slots_mfma_kernel(XaKP p) {
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
       const int64_t qb = qb0 + 32 * qw + 16 * jb + r16;
-      if (qb >= p.n_qb) continue;
-      double *rowp = p.slots + ((bh * p.n_qb + qb) * p.n_kb) * p.n_slots + slot;
+      if (qb >= qend) continue;
+      double *rowp = p.slots + ((bh * p.n_qc + qb - p.qc0) * p.n_kb) * p.n_slots + slot;
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
@@ -272,10 +276,11 @@ __global__ __launch_bounds__(TK_NT) void xattn_select_kernel(XaKP p) {
   __shared__ double redd[TK_NW];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t row = blockIdx.x;  // (b, h, qb)
-  const int64_t qb = row % p.n_qb;
-  const int64_t h = (row / p.n_qb) % p.Hq;
-  const int64_t b = row / (p.n_qb * p.Hq);
+  const int64_t lrow = blockIdx.x;  // (b, h, qb - qc0)
+  const int64_t qb = p.qc0 + lrow % p.n_qc;
+  const int64_t h = (lrow / p.n_qc) % p.Hq;
+  const int64_t b = lrow / (p.n_qc * p.Hq);
+  const int64_t row = (b * p.Hq + h) * p.n_qb + qb;  // the output row
   const int64_t kvh = h / (p.Hq / p.Hkv);
   const int64_t blk = p.blk, D = p.D, NS = p.n_slots, n_kb = p.n_kb;
 
@@ -290,7 +295,7 @@ __global__ __launch_bounds__(TK_NT) void xattn_select_kernel(XaKP p) {
   const int64_t kbase = b * p.k_sb + kvh * p.k_sh;
 
   if (p.slots) {  // scored on the matrix cores: the row's visible slots
-    const double *src = p.slots + row * n_kb * NS;
+    const double *src = p.slots + lrow * n_kb * NS;
     for (int64_t x = tid; x < n_vis * NS; x += TK_NT) ss[x] = src[x];
   } else {
     for (int64_t x = tid; x < blk * D; x += TK_NT) {
@@ -499,15 +504,16 @@ __device__ __forceinline__ uint64_t wave_red_u64(uint64_t x) {
 template <int KPL>
 __global__ __launch_bounds__(256) void xattn_select_wave_kernel(XaKP p, int64_t n_rows) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, h, qb)
-  if (row >= n_rows) return;  // wave-uniform; the kernel has no barrier
-  const int64_t qb = row % p.n_qb;
-  const int64_t h = (row / p.n_qb) % p.Hq;
+  const int64_t lrow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, h, qb - qc0)
+  if (lrow >= n_rows) return;  // wave-uniform; the kernel has no barrier
+  const int64_t qb = p.qc0 + lrow % p.n_qc;
+  const int64_t h = (lrow / p.n_qc) % p.Hq;
+  const int64_t row = (lrow / (p.n_qc * p.Hq) * p.Hq + h) * p.n_qb + qb;  // the output row
   const int64_t n_kb = p.n_kb, NS = p.n_slots, blk = p.blk;
   const int64_t pos0 = qb * blk + p.offset;
   const int64_t lim = min(pos0 / blk, n_kb - 1);
   const int64_t n_vis = lim + 1;
-  const double *src = p.slots + row * n_kb * NS;
+  const double *src = p.slots + lrow * n_kb * NS;
   const uint64_t lt = lanemask_lt(lane);
 
   double mx = __int_as_float(0xff800000);
@@ -657,16 +663,55 @@ static bool xattn_mfma_shape(const la_xattn_select_args *a) {
          a->k_st % 8 == 0;
 }
 
-static int64_t xattn_slot_bytes(const la_xattn_select_args *a) {
+// Query blocks scored per launch: all of them while their slot scores fit
+// `avail` bytes, else a multiple of XM_T that does (0: not even XM_T do).
+// The workspace asked for is bounded by XA_SLOT_BUDGET (not quadratic in T);
+// a smaller workspace from the caller gives smaller chunks.
+constexpr int64_t XA_SLOT_BUDGET = (int64_t)256 << 20;
+static int64_t xattn_chunk_qb(const la_xattn_select_args *a, int64_t avail) {
   const int64_t n_kb = ceil_div(a->T, a->block), n_qb = ceil_div(a->Tq, a->block);
   const int64_t ns = (2 * a->block - 2) / a->stride + 1;
-  return a->B * a->Hq * n_qb * n_kb * ns * 8;
+  const int64_t per_qb = std::max<int64_t>(a->B * a->Hq * n_kb * ns * 8, 1);
+  const int64_t c = avail / per_qb;
+  if (c >= n_qb) return n_qb;
+  return c / XM_T * XM_T;
+}
+
+static int64_t xattn_slot_bytes(const la_xattn_select_args *a, int64_t cq) {
+  const int64_t n_kb = ceil_div(a->T, a->block);
+  const int64_t ns = (2 * a->block - 2) / a->stride + 1;
+  return a->B * a->Hq * cq * n_kb * ns * 8;
+}
+
+// The block-per-row selection over rows [0, nrows) of the launch's chunk.
+static int xattn_launch_select(const XaKP &p, int64_t n_kb, size_t lds, int64_t nrows,
+                               hipStream_t st) {
+  const int kpt = (int)ceil_div(n_kb, TK_NT);
+  auto launch = [&](auto kern) -> int {
+    if (lds > 64 * 1024)
+      LA_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    kern<<<dim3((unsigned)nrows), TK_NT, lds, st>>>(p);
+    return (int)LA_OK;
+  };
+  int rc;
+  if (kpt <= 1)
+    rc = launch(&xattn_select_kernel<1>);
+  else if (kpt <= 4)
+    rc = launch(&xattn_select_kernel<4>);
+  else
+    rc = launch(&xattn_select_kernel<16>);
+  if (rc != LA_OK) return rc;
+  LA_LAUNCHED();
+  return LA_OK;
 }
 
 extern "C" size_t la_xattn_select_workspace(const la_xattn_select_args *a) {
   if (!a || a->B <= 0 || a->Hq <= 0 || a->Tq <= 0 || a->T <= 0 || a->block < 1 || a->stride < 1)
     return 0;
-  return xattn_mfma_shape(a) ? (size_t)xattn_slot_bytes(a) : 0;
+  if (!xattn_mfma_shape(a)) return 0;
+  const int64_t cq = std::max<int64_t>(xattn_chunk_qb(a, XA_SLOT_BUDGET),
+                                       std::min<int64_t>(XM_T, ceil_div(a->Tq, a->block)));
+  return (size_t)xattn_slot_bytes(a, cq);
 }
 
 extern "C" int la_xattn_select(const la_xattn_select_args *a, void *stream) {
@@ -712,43 +757,39 @@ extern "C" int la_xattn_select(const la_xattn_select_args *a, void *stream) {
   const int64_t nwg = a->B * a->Hq * n_qb;
   LA_REQUIRE(nwg < ((int64_t)1 << 31), "la_xattn_select: too many rows");
   hipStream_t st = (hipStream_t)stream;
-  if (a->workspace && xattn_mfma_shape(a) && a->ws_bytes >= xattn_slot_bytes(a)) {
+  const int64_t cq = a->workspace && xattn_mfma_shape(a) ? xattn_chunk_qb(a, a->ws_bytes) : 0;
+  if (cq > 0) {
     p.slots = (double *)a->workspace;
     LA_REQUIRE(a->B * a->Hq < 65536, "la_xattn_select: B * Hq >= 65536");
-    const dim3 grid((unsigned)ceil_div(n_kb, XM_T), (unsigned)ceil_div(n_qb, XM_T),
-                    (unsigned)(a->B * a->Hq));
-    if (a->in_dtype == LA_BF16)
-      xattn_slots_mfma_kernel<true><<<grid, XM_NT, 0, st>>>(p);
-    else
-      xattn_slots_mfma_kernel<false><<<grid, XM_NT, 0, st>>>(p);
-    LA_LAUNCHED();
-  }
-  if (p.slots && n_kb <= 1024) {  // one wave per row over the scored slots
-    const unsigned grid = (unsigned)ceil_div(nwg, 4);
-    if (n_kb <= 64)
-      xattn_select_wave_kernel<1><<<grid, 256, 0, st>>>(p, nwg);
-    else if (n_kb <= 256)
-      xattn_select_wave_kernel<4><<<grid, 256, 0, st>>>(p, nwg);
-    else
-      xattn_select_wave_kernel<16><<<grid, 256, 0, st>>>(p, nwg);
-    LA_LAUNCHED();
+    // chunks of query blocks: score the chunk's slots, then select its rows
+    for (int64_t q0 = 0; q0 < n_qb; q0 += cq) {
+      p.qc0 = q0;
+      p.n_qc = std::min(cq, n_qb - q0);
+      const dim3 grid((unsigned)ceil_div(n_kb, XM_T), (unsigned)ceil_div(p.n_qc, XM_T),
+                      (unsigned)(a->B * a->Hq));
+      if (a->in_dtype == LA_BF16)
+        xattn_slots_mfma_kernel<true><<<grid, XM_NT, 0, st>>>(p);
+      else
+        xattn_slots_mfma_kernel<false><<<grid, XM_NT, 0, st>>>(p);
+      LA_LAUNCHED();
+      const int64_t nrows = a->B * a->Hq * p.n_qc;
+      if (n_kb <= 1024) {  // one wave per row over the scored slots
+        const unsigned g4 = (unsigned)ceil_div(nrows, 4);
+        if (n_kb <= 64)
+          xattn_select_wave_kernel<1><<<g4, 256, 0, st>>>(p, nrows);
+        else if (n_kb <= 256)
+          xattn_select_wave_kernel<4><<<g4, 256, 0, st>>>(p, nrows);
+        else
+          xattn_select_wave_kernel<16><<<g4, 256, 0, st>>>(p, nrows);
+        LA_LAUNCHED();
+      } else {
+        const int rc = xattn_launch_select(p, n_kb, lds, nrows, st);
+        if (rc != LA_OK) return rc;
+      }
+    }
     return LA_OK;
   }
-  const int kpt = (int)ceil_div(n_kb, TK_NT);
-  auto launch = [&](auto kern) -> int {
-    if (lds > 64 * 1024)
-      LA_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    kern<<<dim3((unsigned)nwg), TK_NT, lds, st>>>(p);
-    return (int)LA_OK;
-  };
-  int rc;
-  if (kpt <= 1)
-    rc = launch(&xattn_select_kernel<1>);
-  else if (kpt <= 4)
-    rc = launch(&xattn_select_kernel<4>);
-  else
-    rc = launch(&xattn_select_kernel<16>);
-  if (rc != LA_OK) return rc;
-  LA_LAUNCHED();
-  return LA_OK;
+  p.qc0 = 0;
+  p.n_qc = n_qb;
+  return xattn_launch_select(p, n_kb, lds, nwg, st);
 }

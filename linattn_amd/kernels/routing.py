@@ -144,8 +144,9 @@ def _alphas(threshold, Hq: int, dev: torch.device) -> torch.Tensor:
 
 def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride: int = 8,
                      threshold: Union[float, Sequence[float]] = 0.9, offset: int = 0,
-                     topk: Optional[int] = None,
-                     top_ratio: Optional[float] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                     topk: Optional[int] = None, top_ratio: Optional[float] = None,
+                     max_workspace_bytes: Optional[int] = None
+                     ) -> Tuple[torch.Tensor, torch.Tensor]:
     """XAttention's block selection (XAttention.antidiagonal_scores / select,
     selection.py:528-595) for every (b, query head, query block).
 
@@ -165,6 +166,11 @@ def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride
     causality dropped.  Masses are exact integers of fixed-point weights from
     a deterministic exp, so ties and the threshold crossing are a fixed
     function of the inputs (ties to the lowest block).
+
+    The slot scores of a chunk of query blocks are kept in a workspace of at
+    most 256 MiB (the chunk shrinks as T grows); ``max_workspace_bytes``
+    bounds it further (smaller chunks, same lists; below one chunk of 64 query
+    blocks the rows are scored without a workspace).
 
     q (B, Hq, Tq, D) at positions offset + t; k (B, Hkv, T, D).  Returns ids
     (B, Hq, n_qb, W) ascending, -1 padded (W = n_kb, or min(topk, n_kb) + 1)
@@ -214,6 +220,8 @@ def xattn_select_hip(q: torch.Tensor, k: torch.Tensor, *, block: int = 8, stride
     a.in_dtype = N.dtype_code(q.dtype)
     L = N.load()
     ws_bytes = L.la_xattn_select_workspace(ctypes.byref(a))
+    if max_workspace_bytes is not None:
+        ws_bytes = min(ws_bytes, max(0, int(max_workspace_bytes)))
     ws = N.workspace(ws_bytes, dev) if ws_bytes else None
     a.workspace, a.ws_bytes = N.ptr(ws), ws_bytes
     N.check(L.la_xattn_select(ctypes.byref(a), N.stream_handle(dev)), "xattn_select_hip")

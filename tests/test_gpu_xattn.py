@@ -87,6 +87,33 @@ def test_xattn_select_one_wave_rows(dev, t, tq, block, threshold, topk):
     check_lists(ids, counts, ref_ids, ref_counts)
 
 
+@pytest.mark.parametrize("t,tq,block,topk", [
+    (8192 - 100, 8192 - 100, 8, None),  # 1012 query blocks: 16 chunks of 64, the last partial
+    (1000 * 8, 300 * 8, 8, 20),         # top-k, queries at an offset: 5 chunks
+    (1200 * 8, 130 * 8, 8, None),       # 1200 key blocks: the block-per-row selection per chunk
+])
+def test_xattn_select_chunked_workspace(dev, t, tq, block, topk):
+    """A workspace bounded to one chunk of 64 query blocks: the slots are
+    scored and selected chunk by chunk, with the lists of the one-pass call
+    (and of the oracle on a sample of rows)."""
+    q, k, _ = inputs(1, 2, 1, tq, t, 64, seed=35, dtype=torch.bfloat16)
+    kw = dict(block=block, stride=block, offset=t - tq, threshold=[0.9, 0.7])
+    if topk is not None:
+        kw["topk"] = topk
+    n_kb = -(-t // block)
+    one_chunk = 2 * 64 * n_kb * 2 * 8  # B * Hq * 64 query blocks * n_kb * 2 slots * 8 B
+    ids, counts = xattn_select_hip(q.to(dev), k.to(dev), max_workspace_bytes=one_chunk, **kw)
+    ids1, counts1 = xattn_select_hip(q.to(dev), k.to(dev), **kw)
+    assert torch.equal(ids, ids1) and torch.equal(counts, counts1)
+    r0 = max(0, (tq // block // 64 - 1) * 64 - 5)
+    rows = slice(r0, r0 + 10)  # straddles a chunk boundary
+    ref_ids, ref_counts = oracle.xattn_select(q[:, :, rows.start * block:rows.stop * block], k,
+                                              block=block, stride=block,
+                                              offset=t - tq + rows.start * block,
+                                              threshold=kw["threshold"], topk=topk)
+    check_lists(ids[:, :, rows], counts[:, :, rows], ref_ids, ref_counts)
+
+
 def test_xattn_slots_summation_order(dev):
     """Slot entries are fp64 sums over d in increasing order (the matrix-core
     scorer for stride == block relies on the in-order fp64 accumulation).
