@@ -21,9 +21,15 @@
 // copies, by launch parity), written by the row's chunk-0 workgroup.  Rows
 // that finish early do nothing in the remaining launches.
 //
+// The sequence is short: RX_FAST_PASSES chunk-parallel passes (33 bits
+// fixed, which settles the threshold of scores spread over their leading
+// bits), the count, and a last launch that writes.  A row still undecided by
+// then (keys tied over most of their bits) is finished in that last launch
+// by one workgroup, which loops over the row's chunks.
+//
 // The first pass's histogram (the top RX_RB bits) may come from the kernel
-// that writes the scores (the decode indexer: rx_hist0_add), which saves a
-// launch and a read of the scores.
+// that writes the scores (the decode indexer, indexer_decode16_kernel),
+// which saves a launch and a read of the scores.
 //
 // The selection equals tk_select's over the whole row: the K largest keys,
 // threshold ties taken lowest index first.
@@ -39,6 +45,10 @@ constexpr int64_t RX_CHUNK = (int64_t)TK_NT * RX_KPT;  // keys per workgroup
 constexpr int RX_BPT = RX_BINS / TK_NT;                // bins per thread when picking
 constexpr int RX_PASSES = (64 + RX_RB - 1) / RX_RB;
 enum { RX_PASS = 0, RX_COUNT = 1, RX_WRITE = 2, RX_DONE = 3 };
+// digit passes run chunk-parallel: three settle the threshold of scores
+// spread over their leading bits (33 bits fixed); rows that need more finish
+// in one workgroup in the last launch
+constexpr int RX_FAST_PASSES = 3;
 
 // Status bits raised by kernels of this library on the current device, read
 // and cleared by la_device_status.
@@ -89,7 +99,15 @@ __global__ __launch_bounds__(TK_NT) void rx_setup_kernel(RxKP a, int hist0_exter
   }
 }
 
-__global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch) {
+// Launch `launch` of a row's stage sequence.  Launches before the last one
+// run the phases chunk-parallel (above).  The last launch writes the rows
+// that have reached the write phase the same way; a row that has not (its
+// threshold still undecided after the chunk-parallel passes: keys tied over
+// many of their leading bits) is finished by its chunk-0 workgroup alone,
+// which runs the remaining passes, then counts and writes chunk after chunk
+// in index order (one read of the row per pass, one for the count and the
+// write together), while the row's other workgroups exit.
+__global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int last) {
   __shared__ uint32_t hist[RX_BINS];
   __shared__ uint32_t eqc[RX_KPT][TK_NW];  // per slot and wave: threshold keys
   __shared__ uint32_t tkc[RX_KPT][TK_NW];  // per slot and wave: keys taken
@@ -109,29 +127,53 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch) {
     return;
   }
   uint64_t prefix = sin->prefix, mask = sin->mask;
-  uint32_t need = sin->need, pass = sin->pass;
+  uint32_t need = sin->need, pass = sin->pass, pend = sin->pend;
   int top = sin->top;
-  auto publish = [&](uint32_t next_phase, uint32_t pend) {
+  auto publish = [&](uint32_t next_phase, uint32_t next_pend) {
     sout->prefix = prefix;
     sout->mask = mask;
     sout->need = need;
     sout->pass = pass;
-    sout->pend = pend;
+    sout->pend = next_pend;
     sout->phase = next_phase;
     sout->top = top;
   };
-  // the pick of the pass the previous launch histogrammed: the bin holding
-  // the need-th largest matching key (thread t holds bins RX_BINS - 1 - RX_BPT t
-  // downwards)
-  if (sin->pend) {
-    const int shift = top >= RX_RB - 1 ? top - (RX_RB - 1) : 0;
-    const uint32_t dm = (2u << (top - shift)) - 1u;
-    const uint32_t *gh = a.hist + (gi * RX_PASSES + pass) * RX_BINS;
-    uint32_t h[RX_BPT], csum = 0, all;
+  const TkRow rw = tk_row(p, gi);
+  const int64_t n_v = rw.n_v;
+  const uint32_t K = (uint32_t)rw.K;
+  const bool ord1 = p.order == 1;
+  int32_t *oi = p.out_idx + rw.orow * p.width;
+  const uint64_t lt = lanemask_lt(lane);
+  uint32_t *chunk = a.chunk + gi * a.C * 2;
+
+  // the order keys of chunk x (thread t: keys x * RX_CHUNK + t + 256 j)
+  auto load = [&](int64_t x, uint64_t (&u)[RX_KPT]) {
+    const int64_t x0 = x * RX_CHUNK + tid;
+    const double *rp = p.scores + rw.br * p.row_stride;
+    double v[RX_KPT];
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) v[j] = x0 + (int64_t)j * TK_NT < n_v ? rp[x0 + (int64_t)j * TK_NT] : 0.0;
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) u[j] = ord_key(v[j]);
+  };
+  auto valid = [&](int64_t x, int j) { return x * RX_CHUNK + tid + (int64_t)j * TK_NT < n_v; };
+  // the digit below the fixed bits: its shift and mask
+  auto digit = [&](int &shift, uint32_t &dm) {
+    shift = top >= RX_RB - 1 ? top - (RX_RB - 1) : 0;
+    dm = (2u << (top - shift)) - 1u;
+  };
+  // picks the bin of the need-th largest matching key from a complete
+  // histogram h of the current digit (thread t holds bins RX_BINS - 1 -
+  // RX_BPT t downwards) and moves the state past it
+  auto pick = [&](const uint32_t *h) {
+    int shift;
+    uint32_t dm;
+    digit(shift, dm);
+    uint32_t hv[RX_BPT], csum = 0, all;
 #pragma unroll
     for (int e = 0; e < RX_BPT; ++e) {
-      h[e] = gh[RX_BINS - 1 - RX_BPT * tid - e];
-      csum += h[e];
+      hv[e] = h[RX_BINS - 1 - RX_BPT * tid - e];
+      csum += hv[e];
     }
     const uint32_t incl = tk_block_incl_scan(csum, wtmp[0], all);
     if (incl >= need && incl - csum < need) {
@@ -139,13 +181,13 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch) {
       bool found = false;
 #pragma unroll
       for (int e = 0; e < RX_BPT; ++e) {
-        if (!found && acc + h[e] >= need) {
+        if (!found && acc + hv[e] >= need) {
           s_bin = (uint32_t)(RX_BINS - 1 - RX_BPT * tid - e);
           s_above = acc;
-          s_cnt = h[e];
+          s_cnt = hv[e];
           found = true;
         }
-        acc += h[e];
+        acc += hv[e];
       }
     }
     __syncthreads();
@@ -156,30 +198,137 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch) {
     pass += 1;
     // the whole bin is taken, or every bit is fixed (the rest are index ties)
     phase = (s_cnt == need || shift == 0) ? RX_COUNT : RX_PASS;
-  }
-  const TkRow rw = tk_row(p, gi);
-  const int64_t n_v = rw.n_v;
-  const int64_t c0 = c * RX_CHUNK + tid;
-  auto valid = [&](int j) { return c0 + (int64_t)j * TK_NT < n_v; };
-  uint64_t u[RX_KPT];
-  {
-    const double *rp = p.scores + rw.br * p.row_stride;
-    double v[RX_KPT];
-#pragma unroll
-    for (int j = 0; j < RX_KPT; ++j) v[j] = valid(j) ? rp[c0 + (int64_t)j * TK_NT] : 0.0;
-#pragma unroll
-    for (int j = 0; j < RX_KPT; ++j) u[j] = ord_key(v[j]);
-  }
-  uint32_t *chunk = a.chunk + gi * a.C * 2;
-
-  if (phase == RX_PASS) {
-    const int shift = top >= RX_RB - 1 ? top - (RX_RB - 1) : 0;
-    const uint32_t dm = (2u << (top - shift)) - 1u;
-    for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
-    __syncthreads();
+    __syncthreads();  // s_* are read before they are written again
+  };
+  // adds the chunk's keys that match the prefix to the LDS histogram
+  auto hist_chunk = [&](int64_t x, const uint64_t (&u)[RX_KPT]) {
+    int shift;
+    uint32_t dm;
+    digit(shift, dm);
 #pragma unroll
     for (int j = 0; j < RX_KPT; ++j)
-      if (valid(j) && (u[j] & mask) == prefix) atomicAdd(&hist[(uint32_t)(u[j] >> shift) & dm], 1u);
+      if (valid(x, j) && (u[j] & mask) == prefix) atomicAdd(&hist[(uint32_t)(u[j] >> shift) & dm], 1u);
+  };
+  // the chunk's keys above / equal to the final threshold (workgroup totals)
+  auto count_chunk = [&](int64_t x, const uint64_t (&u)[RX_KPT], uint32_t &gt_c, uint32_t &eq_c) {
+    uint32_t gt = 0, eq = 0;
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) {
+      const uint64_t um = u[j] & mask;
+      gt += valid(x, j) && um > prefix;
+      eq += valid(x, j) && um == prefix;
+    }
+    tk_block_incl_scan(gt, wtmp[0], gt_c);
+    tk_block_incl_scan(eq, wtmp[1], eq_c);
+  };
+  // writes chunk x's selected keys from output position base on, taking its
+  // first take_eq threshold keys (index order within the chunk)
+  auto write_chunk = [&](int64_t x, const uint64_t (&u)[RX_KPT], uint32_t base, uint32_t take_eq) {
+    const int64_t x0 = x * RX_CHUNK + tid;
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) {
+      const uint64_t b = __ballot(valid(x, j) && (u[j] & mask) == prefix);
+      if (lane == 0) eqc[j][w] = (uint32_t)__popcll(b);
+    }
+    __syncthreads();
+    uint32_t take_bits = 0, eq_run = 0;
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) {
+      const uint64_t um = u[j] & mask;
+      const bool is_gt = valid(x, j) && um > prefix;
+      const bool is_eq = valid(x, j) && um == prefix;
+      const uint64_t b = __ballot(is_eq);
+      uint32_t rank = eq_run + (uint32_t)__popcll(b & lt);
+#pragma unroll
+      for (int y = 0; y < TK_NW; ++y) rank += y < w ? eqc[j][y] : 0u;
+#pragma unroll
+      for (int y = 0; y < TK_NW; ++y) eq_run += eqc[j][y];
+      const bool take = is_gt || (is_eq && rank < take_eq);
+      const uint64_t tb = __ballot(take);
+      if (lane == 0) tkc[j][w] = (uint32_t)__popcll(tb);
+      take_bits |= (uint32_t)take << j;
+    }
+    __syncthreads();
+    uint32_t pos_run = base;
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) {
+      const bool take = (take_bits >> j) & 1u;
+      const uint64_t tb = __ballot(take);
+      uint32_t pos = pos_run + (uint32_t)__popcll(tb & lt);
+#pragma unroll
+      for (int y = 0; y < TK_NW; ++y) pos += y < w ? tkc[j][y] : 0u;
+#pragma unroll
+      for (int y = 0; y < TK_NW; ++y) pos_run += tkc[j][y];
+      if (take) {
+        const int64_t i = x0 + (int64_t)j * TK_NT;
+        if (ord1) {
+          if ((int64_t)pos < p.width) oi[pos] = (int32_t)i;
+        } else if (pos < K) {
+          a.cand_sc[gi * p.k + pos] = key_to_double(u[j]);
+          a.cand_id[gi * p.k + pos] = (int32_t)i;
+        }
+      }
+    }
+    __syncthreads();  // eqc / tkc are read before the next chunk writes them
+  };
+  // padding after the K winners (positions first + stride * m), and the count
+  auto pad = [&](int64_t first, int64_t stride) {
+    if (ord1) {
+      for (int64_t y = K + first; y < p.width; y += stride) oi[y] = -1;
+      if (writer && p.out_count) p.out_count[rw.orow] = (int32_t)min((int64_t)K, p.width);
+    } else {
+      // a double whose order key is 0 (below every real score) and index -1
+      for (int64_t y = K + first; y < p.k; y += stride) {
+        a.cand_sc[gi * p.k + y] = __longlong_as_double((long long)0xffffffffffffffffull);
+        a.cand_id[gi * p.k + y] = -1;
+      }
+    }
+  };
+
+  if (last && !(phase == RX_WRITE && !pend)) {
+    // ------------------------------------------- one-workgroup finish --
+    if (c != 0) return;
+    if (pend) pick(a.hist + (gi * RX_PASSES + pass) * RX_BINS);
+    uint64_t u[RX_KPT];
+    while (phase == RX_PASS) {
+      for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
+      __syncthreads();
+      for (int64_t x = 0; x < a.C; ++x) {
+        load(x, u);
+        hist_chunk(x, u);
+      }
+      __syncthreads();
+      pick(hist);
+    }
+    // count and write together, chunk after chunk in index order: chunk x
+    // writes after the keys the chunks before it select and takes the
+    // first need - (threshold keys before it) of its own threshold keys
+    uint32_t gt_before = 0, eq_before = 0;
+    for (int64_t x = 0; x < a.C; ++x) {
+      load(x, u);
+      uint32_t gt_c, eq_c;
+      count_chunk(x, u, gt_c, eq_c);
+      const uint32_t base = gt_before + min(need, eq_before);
+      const uint32_t take_eq = eq_before >= need ? 0u : min(need - eq_before, eq_c);
+      write_chunk(x, u, base, take_eq);
+      gt_before += gt_c;
+      eq_before += eq_c;
+    }
+    pad(tid, TK_NT);
+    if (writer) sout->phase = RX_DONE;
+    return;
+  }
+
+  // the pick of the pass the previous launch histogrammed: every workgroup
+  // of the row reads the complete histogram and makes the same pick
+  if (pend) pick(a.hist + (gi * RX_PASSES + pass) * RX_BINS);
+  uint64_t u[RX_KPT];
+  load(c, u);
+
+  if (phase == RX_PASS) {
+    for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
+    __syncthreads();
+    hist_chunk(c, u);
     __syncthreads();
     uint32_t *gh = a.hist + (gi * RX_PASSES + pass) * RX_BINS;
     for (int b = tid; b < RX_BINS; b += TK_NT) {
@@ -191,16 +340,8 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch) {
   }
 
   if (phase == RX_COUNT) {
-    uint32_t gt = 0, eq = 0;
-#pragma unroll
-    for (int j = 0; j < RX_KPT; ++j) {
-      const uint64_t um = u[j] & mask;
-      gt += valid(j) && um > prefix;
-      eq += valid(j) && um == prefix;
-    }
     uint32_t gt_c, eq_c;
-    tk_block_incl_scan(gt, wtmp[0], gt_c);
-    tk_block_incl_scan(eq, wtmp[1], eq_c);
+    count_chunk(c, u, gt_c, eq_c);
     if (tid == 0) {
       chunk[2 * c] = gt_c;
       chunk[2 * c + 1] = eq_c;
@@ -210,9 +351,8 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch) {
   }
 
   // ---------------------------------------------------------------- write --
-  // this chunk's output offset and the threshold keys it takes: chunk x
-  // writes after the keys the chunks before it select and takes the first
-  // need - (threshold keys before it) of its own threshold keys
+  // this chunk's output offset and the threshold keys it takes, from the
+  // counts of the chunks before it
   {
     uint32_t gb = 0, eb = 0;
     for (int64_t x = tid; x < c; x += TK_NT) {
@@ -229,68 +369,8 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch) {
     }
     __syncthreads();
   }
-  const uint32_t base = s_base, take_eq = s_take;
-  const bool ord1 = p.order == 1;
-  const uint32_t K = (uint32_t)rw.K;
-  int32_t *oi = p.out_idx + rw.orow * p.width;
-  const int64_t stride = a.C * TK_NT;
-  const uint64_t lt = lanemask_lt(lane);
-  // ranks of the threshold keys in index order (slot-major within the chunk)
-#pragma unroll
-  for (int j = 0; j < RX_KPT; ++j) {
-    const uint64_t b = __ballot(valid(j) && (u[j] & mask) == prefix);
-    if (lane == 0) eqc[j][w] = (uint32_t)__popcll(b);
-  }
-  __syncthreads();
-  uint32_t take_bits = 0, eq_run = 0;
-#pragma unroll
-  for (int j = 0; j < RX_KPT; ++j) {
-    const uint64_t um = u[j] & mask;
-    const bool is_gt = valid(j) && um > prefix;
-    const bool is_eq = valid(j) && um == prefix;
-    const uint64_t b = __ballot(is_eq);
-    uint32_t rank = eq_run + (uint32_t)__popcll(b & lt);
-#pragma unroll
-    for (int x = 0; x < TK_NW; ++x) rank += x < w ? eqc[j][x] : 0u;
-#pragma unroll
-    for (int x = 0; x < TK_NW; ++x) eq_run += eqc[j][x];
-    const bool take = is_gt || (is_eq && rank < take_eq);
-    const uint64_t tb = __ballot(take);
-    if (lane == 0) tkc[j][w] = (uint32_t)__popcll(tb);
-    take_bits |= (uint32_t)take << j;
-  }
-  __syncthreads();
-  uint32_t pos_run = base;
-#pragma unroll
-  for (int j = 0; j < RX_KPT; ++j) {
-    const bool take = (take_bits >> j) & 1u;
-    const uint64_t tb = __ballot(take);
-    uint32_t pos = pos_run + (uint32_t)__popcll(tb & lt);
-#pragma unroll
-    for (int x = 0; x < TK_NW; ++x) pos += x < w ? tkc[j][x] : 0u;
-#pragma unroll
-    for (int x = 0; x < TK_NW; ++x) pos_run += tkc[j][x];
-    if (take) {
-      const int64_t i = c0 + (int64_t)j * TK_NT;
-      if (ord1) {
-        if ((int64_t)pos < p.width) oi[pos] = (int32_t)i;
-      } else if (pos < K) {
-        a.cand_sc[gi * p.k + pos] = key_to_double(u[j]);
-        a.cand_id[gi * p.k + pos] = (int32_t)i;
-      }
-    }
-  }
-  // padding after the K winners, and the count
-  if (ord1) {
-    for (int64_t x = K + c * TK_NT + tid; x < p.width; x += stride) oi[x] = -1;
-    if (writer && p.out_count) p.out_count[rw.orow] = (int32_t)min((int64_t)K, p.width);
-  } else {
-    // a double whose order key is 0 (below every real score) and index -1
-    for (int64_t x = K + c * TK_NT + tid; x < p.k; x += stride) {
-      a.cand_sc[gi * p.k + x] = __longlong_as_double((long long)0xffffffffffffffffull);
-      a.cand_id[gi * p.k + x] = -1;
-    }
-  }
+  write_chunk(c, u, s_base, s_take);
+  pad(c * TK_NT + tid, a.C * TK_NT);
   if (writer) sout->phase = RX_DONE;
 }
 
@@ -342,11 +422,13 @@ int topk_radix_finish(const TopkKParams &p, const RadixPlan &R, void *ws, bool h
                       hipStream_t st) {
   const RxKP a = rx_args(p, R, ws);
   const dim3 grid((unsigned)R.C, (unsigned)p.NG);
-  // passes still to histogram (the first may come from the scores' kernel),
-  // then the count and the write
-  const int launches = (hist0_external ? RX_PASSES - 1 : RX_PASSES) + 2;
+  // chunk-parallel launches for the passes that settle the threshold of
+  // scores spread over their leading bits (the first pass may come from the
+  // scores' kernel) and the count; the last launch writes (or finishes a
+  // row whose threshold is still open in one workgroup)
+  const int launches = RX_FAST_PASSES - (hist0_external ? 1 : 0) + 2;
   for (int s = 0; s < launches; ++s) {
-    rx_stage_kernel<<<grid, TK_NT, 0, st>>>(a, s);
+    rx_stage_kernel<<<grid, TK_NT, 0, st>>>(a, s, s == launches - 1 ? 1 : 0);
     LA_LAUNCHED();
   }
   if (p.order == 0) {
