@@ -43,12 +43,15 @@ namespace la {
 constexpr int RX_KPT = 16;                              // keys per thread
 constexpr int64_t RX_CHUNK = (int64_t)TK_NT * RX_KPT;  // keys per workgroup
 constexpr int RX_BPT = RX_BINS / TK_NT;                // bins per thread when picking
-constexpr int RX_PASSES = (64 + RX_RB - 1) / RX_RB;
 enum { RX_PASS = 0, RX_COUNT = 1, RX_WRITE = 2, RX_DONE = 3 };
 // digit passes run chunk-parallel: three settle the threshold of scores
 // spread over their leading bits (33 bits fixed); rows that need more finish
 // in one workgroup in the last launch
 constexpr int RX_FAST_PASSES = 3;
+// digit histograms in the workspace per row: the chunk-parallel passes and
+// the one the last launch picks from (the finishing workgroup keeps its own
+// in LDS)
+constexpr int RX_HISTS = RX_FAST_PASSES + 1;
 
 // Status bits raised by kernels of this library on the current device, read
 // and cleared by la_device_status.
@@ -69,7 +72,7 @@ static_assert(sizeof(RxState) == 48, "RxState layout");
 struct RxKP {
   TopkKParams p;
   RxState *state;     // [2][NG]
-  uint32_t *hist;     // [NG][RX_PASSES][RX_BINS]
+  uint32_t *hist;     // [NG][RX_HISTS][RX_BINS]
   uint32_t *chunk;    // [NG][C][2]: keys above / equal to the final threshold
   double *cand_sc;    // order 0: candidate rows [NG][k], sorted afterwards
   int32_t *cand_id;
@@ -82,8 +85,8 @@ struct RxKP {
 __global__ __launch_bounds__(TK_NT) void rx_setup_kernel(RxKP a, int hist0_external) {
   const int64_t gi = blockIdx.x;
   const TkRow rw = tk_row(a.p, gi);
-  uint4 *h = (uint4 *)(a.hist + gi * RX_PASSES * RX_BINS);
-  for (int i = threadIdx.x; i < RX_PASSES * RX_BINS / 4; i += TK_NT) h[i] = make_uint4(0, 0, 0, 0);
+  uint4 *h = (uint4 *)(a.hist + gi * RX_HISTS * RX_BINS);
+  for (int i = threadIdx.x; i < RX_HISTS * RX_BINS / 4; i += TK_NT) h[i] = make_uint4(0, 0, 0, 0);
   if (threadIdx.x == 0) {
     const uint32_t K = (uint32_t)rw.K, n_v = (uint32_t)rw.n_v;
     RxState s{};
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
   if (last && !(phase == RX_WRITE && !pend)) {
     // ------------------------------------------- one-workgroup finish --
     if (c != 0) return;
-    if (pend) pick(a.hist + (gi * RX_PASSES + pass) * RX_BINS);
+    if (pend) pick(a.hist + (gi * RX_HISTS + pass) * RX_BINS);
     uint64_t u[RX_KPT];
     while (phase == RX_PASS) {
       for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
@@ -321,7 +324,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
 
   // the pick of the pass the previous launch histogrammed: every workgroup
   // of the row reads the complete histogram and makes the same pick
-  if (pend) pick(a.hist + (gi * RX_PASSES + pass) * RX_BINS);
+  if (pend) pick(a.hist + (gi * RX_HISTS + pass) * RX_BINS);
   uint64_t u[RX_KPT];
   load(c, u);
 
@@ -330,7 +333,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     __syncthreads();
     hist_chunk(c, u);
     __syncthreads();
-    uint32_t *gh = a.hist + (gi * RX_PASSES + pass) * RX_BINS;
+    uint32_t *gh = a.hist + (gi * RX_HISTS + pass) * RX_BINS;
     for (int b = tid; b < RX_BINS; b += TK_NT) {
       const uint32_t x = hist[b];
       if (x) __hip_atomic_fetch_add(&gh[b], x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -381,7 +384,7 @@ RadixPlan radix_plan(const TopkKParams &p) {
   if (p.n >= ((int64_t)1 << 31)) return R;
   R.C = ceil_div(p.n, RX_CHUNK);
   R.bytes = align256(2 * p.NG * (int64_t)sizeof(RxState)) +
-            align256(p.NG * RX_PASSES * RX_BINS * 4) + align256(p.NG * R.C * 8);
+            align256(p.NG * RX_HISTS * RX_BINS * 4) + align256(p.NG * R.C * 8);
   if (p.order == 0) R.bytes += align256(p.NG * p.k * 8) + align256(p.NG * p.k * 4);
   return R;
 }
@@ -394,7 +397,7 @@ static RxKP rx_args(const TopkKParams &p, const RadixPlan &R, void *ws) {
   a.state = (RxState *)base;
   base += align256(2 * p.NG * (int64_t)sizeof(RxState));
   a.hist = (uint32_t *)base;
-  base += align256(p.NG * RX_PASSES * RX_BINS * 4);
+  base += align256(p.NG * RX_HISTS * RX_BINS * 4);
   a.chunk = (uint32_t *)base;
   base += align256(p.NG * R.C * 8);
   if (p.order == 0) {
@@ -407,7 +410,7 @@ static RxKP rx_args(const TopkKParams &p, const RadixPlan &R, void *ws) {
 uint32_t *radix_hist0(const TopkKParams &p, void *ws) {
   return (uint32_t *)((char *)ws + align256(2 * p.NG * (int64_t)sizeof(RxState)));
 }
-int64_t radix_hist_stride() { return (int64_t)RX_PASSES * RX_BINS; }
+int64_t radix_hist_stride() { return (int64_t)RX_HISTS * RX_BINS; }
 
 int topk_radix_setup(const TopkKParams &p, const RadixPlan &R, void *ws, bool hist0_external,
                      hipStream_t st) {
