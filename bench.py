@@ -7,8 +7,10 @@ permuted page table, 32 query / 8 KV heads, head_dim 128, a 2048-token budget
 pages (the reference default, variants/selection.py:232-235).
 
 A step = one decode step for all 64 sequences: Quest page scores, top-k page
-selection, split-K attention over the selected pages.  Inputs (query, KV pool,
-page table, page metadata) are resident in HBM before timing starts.
+selection and the GQA union, attention over the selected pages, as one kernel
+(``quest_decode_fused``); the same step as two launches (``quest_select_hip``,
+then the split-K ``sparse_attention``) is timed beside it.  Inputs (query, KV
+pool, page table, page metadata) are resident in HBM before timing starts.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
 
@@ -32,9 +34,11 @@ if str(ROOT) not in sys.path:
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
 
 C4 = dict(B=64, Hq=32, Hkv=8, T=65536, D=128, page=64, topk=32, seed=0)
-ATTN_KERNEL = "sparse_attn_mfma_kernel"  # the dominant kernel of the C4 step
+STEP_KERNEL = "quest_decode_fused_kernel"  # the C4 step: selection and attention in one kernel
+ATTN_KERNEL = "sparse_attn_mfma_kernel"  # the attention launch of the two-launch step
 COPY_MIB = 1024
-TRAFFIC_FILE = "profiles/c4_attention_traffic.json"
+TRAFFIC_FILE = "profiles/c4_step_traffic.json"
+ATTN_TRAFFIC_FILE = "profiles/c4_attention_traffic.json"
 
 
 def parse():
@@ -54,7 +58,7 @@ def parse():
                          "reference); run under rocprofv3 --pmc")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc runs of --pmc-probe (FETCH_SIZE, then "
-                         "WRITE_SIZE) into " + TRAFFIC_FILE)
+                         "WRITE_SIZE) into " + TRAFFIC_FILE + " and " + ATTN_TRAFFIC_FILE)
     return ap.parse_args()
 
 
@@ -456,30 +460,6 @@ def bench_c5(dev, steps, warmup, keep=None):
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def bench_fused_c4(dev, q, pool_k, pool_v, pt, mins, maxs, cfg, ids, counts, step_bytes,
-                   steps, warmup):
-    """The C4 step as one kernel (``quest_decode_fused``: selection and
-    attention per (b, KV head) workgroup), beside the two-launch step of the
-    headline; its lists must equal the headline's."""
-    import torch
-
-    from linattn_amd.kernels.paged_decode import quest_decode_fused
-
-    ps, T = cfg["page"], cfg["T"]
-
-    def step():
-        return quest_decode_fused(q, pool_k, pool_v, pt, mins, maxs, page_size=ps,
-                                  topk=cfg["topk"], pos=T - 1)
-
-    _, fids, fcounts = step()
-    same = bool(torch.equal(fids, ids) and torch.equal(fcounts, counts))
-    ms = time_cuda(step, steps, warmup)
-    gbs = step_bytes / (ms * 1e-3) / 1e9
-    return {"workload": "C4 step as one kernel (quest_decode_fused)", "ms": round(ms, 4),
-            "tok_per_s": round(cfg["B"] / (ms * 1e-3), 1), "GBps": round(gbs, 1),
-            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "lists_equal_two_kernel": same}
-
-
 def bench_page_bounds(dev, pool_k, pt, mins, maxs, cfg, steps, warmup):
     """Quest metadata built from scratch over the whole C4 key pool (64 x 1024
     pages of 8 KV heads): channel min/max of every page (quest_pages.py:38-48),
@@ -630,29 +610,38 @@ def _counter_rows(d):
 
 
 def traffic_from(fetch_dir, write_dir):
-    """HBM bytes per launch of the attention kernel from FETCH_SIZE and
-    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads
-    for the device copy of COPY_MIB MiB that --pmc-probe ends with."""
+    """HBM bytes per launch of the C4 step kernel and of the attention kernel
+    of the two-launch step from FETCH_SIZE and WRITE_SIZE (KiB per dispatch),
+    each scaled by what the same counter reads for the device copy of COPY_MIB
+    MiB that --pmc-probe ends with."""
     copy_bytes = COPY_MIB << 20
-    out = {"kernel": ATTN_KERNEL, "copy_bytes": copy_bytes}
-    for d, name in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
-        rows = [r for r in _counter_rows(d) if r["Counter_Name"] == name]
-        kern = [float(r["Counter_Value"]) for r in rows if ATTN_KERNEL in r["Kernel_Name"]]
-        copies = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
-        if not kern or not copies:
-            raise SystemExit(f"{name}: kernel or copy dispatches missing in {d}")
-        ref = max(copies)  # the COPY_MIB copy is the largest copy in the probe
-        factor = copy_bytes / (ref * 1024.0)
-        out[name] = {"kib_per_launch": sum(kern) / len(kern), "launches": len(kern),
-                     "copy_kib": ref, "scale": round(factor, 4),
-                     "bytes_per_launch": round(sum(kern) / len(kern) * 1024.0 * factor)}
-    out["traffic_bytes"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
-    out["commands"] = [
-        f"rocprofv3 --pmc {c} --output-format csv -d <dir> -o run -- python -u bench.py --pmc-probe"
-        for c in ("FETCH_SIZE", "WRITE_SIZE")]
-    path = ROOT / TRAFFIC_FILE
-    path.write_text(json.dumps(out, indent=1) + "\n")
-    print(json.dumps(out))
+    for kernel, fname in ((STEP_KERNEL, TRAFFIC_FILE), (ATTN_KERNEL, ATTN_TRAFFIC_FILE)):
+        out = {"kernel": kernel, "copy_bytes": copy_bytes}
+        for d, name in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
+            rows = [r for r in _counter_rows(d) if r["Counter_Name"] == name]
+            per = {}  # dispatch -> summed counter (over the counter's dimensions)
+            for r in rows:
+                if kernel in r["Kernel_Name"]:
+                    per[r["Dispatch_Id"]] = per.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+            copies = {}
+            for r in rows:
+                if "copyBuffer" in r["Kernel_Name"]:
+                    copies[r["Dispatch_Id"]] = copies.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+            if not per or not copies:
+                raise SystemExit(f"{name}: {kernel} or copy dispatches missing in {d}")
+            kern = list(per.values())
+            ref = max(copies.values())  # the COPY_MIB copy is the largest copy in the probe
+            factor = copy_bytes / (ref * 1024.0)
+            out[name] = {"kib_per_launch": sum(kern) / len(kern), "launches": len(kern),
+                         "copy_kib": ref, "scale": round(factor, 4),
+                         "bytes_per_launch": round(sum(kern) / len(kern) * 1024.0 * factor)}
+        out["traffic_bytes"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
+        out["commands"] = [
+            f"rocprofv3 --pmc {c} --output-format csv -d <dir> -o run -- python -u bench.py --pmc-probe"
+            for c in ("FETCH_SIZE", "WRITE_SIZE")]
+        path = ROOT / fname
+        path.write_text(json.dumps(out, indent=1) + "\n")
+        print(json.dumps(out))
     return 0
 
 
@@ -667,6 +656,7 @@ def main() -> int:
     import torch
 
     from linattn_amd.kernels.block_sparse import sparse_attention
+    from linattn_amd.kernels.paged_decode import quest_decode_fused
     from linattn_amd.kernels.quest_pages import quest_select_hip
 
     dev = torch.device("cuda:0")
@@ -695,31 +685,43 @@ def main() -> int:
         return sparse_attention(q, pool_k, pool_v, ids, unit=ps, counts=counts, causal=True,
                                 offset=pos, page_table=pt, page_size=ps)
 
-    def c4_step():
+    def two_launch_step():
         ids, counts = select()
         attend(ids, counts)
+
+    def fused_step():
+        return quest_decode_fused(q, pool_k, pool_v, pt, mins, maxs, page_size=ps,
+                                  topk=cfg["topk"], pos=pos)
+
+    # The step: Quest selection and attention of every (b, KV head) in one
+    # kernel (GQA union lists); with per-head lists (--shared) the two launches.
+    c4_step = fused_step if union else two_launch_step
+
+    def loop_ms(fn, n):
+        """n calls with events only around the loop (an event record between
+        kernels costs a few microseconds of idle GPU)."""
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(n):
+            fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / n
 
     settle_calls = settle(c4_step)
     for _ in range(args.warmup):
-        ids, counts = select()
-        attend(ids, counts)
+        c4_step()
     torch.cuda.synchronize()
+    ms_step = loop_ms(c4_step, args.steps)  # the headline
 
-    # Headline: K steps with events only around the whole loop (an event
-    # record between kernels costs a few microseconds of idle GPU).
-    t_all0 = torch.cuda.Event(enable_timing=True)
-    t_all1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_all0.record(stream)
-    for i in range(args.steps):
-        ids, counts = select()
-        attend(ids, counts)
-    t_all1.record(stream)
-    torch.cuda.synchronize()
-    ms_step = t_all0.elapsed_time(t_all1) / args.steps
-
-    # Split and roofline: K more steps with events around each launch on the
-    # launch stream (the event gaps stay inside the per-kernel figures).
+    # The two-launch step beside it (select, then attend): its time, the
+    # split with events around each launch on the launch stream (the event
+    # gaps stay inside the per-kernel figures), and the attention launch
+    # alone back to back on the last selection (kernel and split combine).
+    settle(two_launch_step)
+    ms_two = loop_ms(two_launch_step, args.steps)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -732,19 +734,11 @@ def main() -> int:
     torch.cuda.synchronize()
     ms_sel = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
     ms_att = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
-
-    # Roofline of the attention launch: K back-to-back launches (kernel and
-    # split combine) on the last selection, events only around the loop, so
-    # the average launch duration carries no per-event idle time.
-    t_a0 = torch.cuda.Event(enable_timing=True)
-    t_a1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_a0.record(stream)
-    for i in range(args.steps):
-        attend(ids, counts)
-    t_a1.record(stream)
-    torch.cuda.synchronize()
-    ms_launch = t_a0.elapsed_time(t_a1) / args.steps
+    ms_launch = loop_ms(lambda: attend(ids, counts), args.steps)
+    lists_equal = None
+    if union:
+        _, fids, fcounts = fused_step()
+        lists_equal = bool(torch.equal(fids, ids) and torch.equal(fcounts, counts))
 
     # algorithmic bytes, from the actual selection
     n_pages_read = int(counts.sum())  # distinct (b, list head, page) triples
@@ -765,15 +759,18 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"pmc_probe": True, "attn_bytes": att_bytes, "copy_bytes": COPY_MIB << 20}))
         return 0
-    traffic = None
-    tpath = ROOT / TRAFFIC_FILE
-    if tpath.exists():
-        rec = json.loads(tpath.read_text())
-        if rec.get("kernel") == ATTN_KERNEL:
-            traffic = rec.get("traffic_bytes")
+
+    def traffic_of(fname, kernel):
+        tpath = ROOT / fname
+        if tpath.exists():
+            rec = json.loads(tpath.read_text())
+            if rec.get("kernel") == kernel:
+                return rec.get("traffic_bytes")
+        return None
+
     # selection traffic: page min+max read, q read, lists and counts written;
-    # the fused union selector (one kernel) keeps its fp64 score rows on chip,
-    # the per-head form writes them and reads them back for the top-k
+    # the fused union selector keeps its fp64 score rows on chip, the per-head
+    # form writes them and reads them back for the top-k
     meta_bytes = 2 * mins.numel() * 2 + q.numel() * 2 + ids.numel() * 4 + counts.numel() * 4
     if not (union and Hq > Hkv):
         meta_bytes += B * Hq * (T // ps) * 8 * 2
@@ -781,6 +778,19 @@ def main() -> int:
     tok_s = B / (ms_step * 1e-3)
     att_gbs = att_bytes / (ms_launch * 1e-3) / 1e9
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
+    two_gbs = step_bytes / (ms_two * 1e-3) / 1e9
+    if union:  # the step is one kernel: its roofline is the step's
+        roofline = {"bound": "hbm", "kernel": STEP_KERNEL,
+                    "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                    "traffic": traffic_of(TRAFFIC_FILE, STEP_KERNEL),
+                    "bytes_per_launch": step_bytes, "ms_per_launch": round(ms_step, 4)}
+    else:
+        roofline = {"bound": "hbm", "kernel": ATTN_KERNEL + " (+ split combine)",
+                    "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(att_gbs / HBM_PEAK_GBS, 4),
+                    "traffic": traffic_of(ATTN_TRAFFIC_FILE, ATTN_KERNEL),
+                    "bytes_per_launch": att_bytes, "ms_per_launch": round(ms_launch, 4)}
 
     result = {
         "metric": "sparse decode tok/s (paged Quest, 64K ctx, batch 64)",
@@ -800,22 +810,26 @@ def main() -> int:
         "data": "synthetic N(0,1), seeded; random page table",
         "config": {"workload": "C4 paged Quest sparse decode", "batch": B, "context": T,
                    "page_size": ps, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
-                   "budget_tokens": cfg["topk"] * ps, "gqa": "union" if union else "per-head"},
-        "roofline": {"bound": "hbm", "kernel": ATTN_KERNEL + " (+ split combine)",
-                     "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": att_bytes, "ms_per_launch": round(ms_launch, 4)},
-        "step": {"ms_select": round(ms_sel, 4), "ms_attend": round(ms_att, 4),
-                 "bytes": step_bytes, "GBps": round(step_gbs, 1),
+                   "budget_tokens": cfg["topk"] * ps, "gqa": "union" if union else "per-head",
+                   "step": ("quest_decode_fused: page scores, top-k, GQA union and attention in "
+                            "one kernel" if union else "quest_select_hip + sparse_attention")},
+        "roofline": roofline,
+        "step": {"bytes": step_bytes, "GBps": round(step_gbs, 1),
                  "frac_hbm": round(step_gbs / HBM_PEAK_GBS, 4),
                  "pages_read_per_kv_list": round(n_pages_read / (B * lists_heads), 2)},
+        "two_launch_step": {"ms": round(ms_two, 4), "tok_per_s": round(B / (ms_two * 1e-3), 1),
+                            "GBps": round(two_gbs, 1), "frac_hbm": round(two_gbs / HBM_PEAK_GBS, 4),
+                            "ms_select": round(ms_sel, 4), "ms_attend": round(ms_att, 4),
+                            "lists_equal_fused": lists_equal,
+                            "attention_roofline": {
+                                "kernel": ATTN_KERNEL + " (+ split combine)",
+                                "achieved": round(att_gbs, 1), "frac": round(att_gbs / HBM_PEAK_GBS, 4),
+                                "traffic": traffic_of(ATTN_TRAFFIC_FILE, ATTN_KERNEL),
+                                "bytes_per_launch": att_bytes, "ms_per_launch": round(ms_launch, 4)}},
     }
     # side configurations: a few untimed calls first (clocks settle)
     sub, sub_w = max(3, args.steps // 4), 10
     keep = None if args.no_cpu_baseline else {}
-    if union:
-        result["fused_step"] = bench_fused_c4(dev, q, pool_k, pool_v, pt, mins, maxs, cfg, ids,
-                                              counts, step_bytes, sub, sub_w)
     result["page_bounds"] = bench_page_bounds(dev, pool_k, pt, mins, maxs, cfg, sub, sub_w)
     result["indexer"] = bench_c2(dev, sub, sub_w, keep)
     result["prefill"] = bench_c3(dev, sub, sub_w, keep)
