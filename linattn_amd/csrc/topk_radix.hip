@@ -21,9 +21,10 @@
 // copies, by launch parity), written by the row's chunk-0 workgroup.  Rows
 // that finish early do nothing in the remaining launches.
 //
-// The sequence is short: RX_FAST_PASSES chunk-parallel passes (33 bits
-// fixed, which settles the threshold of scores spread over their leading
-// bits), the count, and a last launch that writes.  A row still undecided by
+// The sequence is short: RX_FAST_PASSES chunk-parallel passes (three, 28
+// bits fixed, settle the threshold of scores spread over their leading bits;
+// the fourth runs only for rows they leave open), the count, and a last
+// launch that writes.  A row still undecided by
 // then (keys tied over most of their bits) is finished in that last launch
 // by one workgroup, which loops over the row's chunks.
 //
@@ -44,14 +45,22 @@ constexpr int RX_KPT = 16;                              // keys per thread
 constexpr int64_t RX_CHUNK = (int64_t)TK_NT * RX_KPT;  // keys per workgroup
 constexpr int RX_BPT = RX_BINS / TK_NT;                // bins per thread when picking
 enum { RX_PASS = 0, RX_COUNT = 1, RX_WRITE = 2, RX_DONE = 3 };
-// digit passes run chunk-parallel: three settle the threshold of scores
-// spread over their leading bits (33 bits fixed); rows that need more finish
-// in one workgroup in the last launch
-constexpr int RX_FAST_PASSES = 3;
+// digit passes run chunk-parallel: up to four (39 bits fixed); rows that
+// need more finish in one workgroup in the last launch.  A row whose
+// threshold the first three settle (28 bits: scores spread over their
+// leading bits) counts and writes a launch early and skips the rest.
+constexpr int RX_FAST_PASSES = 4;
 // digit histograms in the workspace per row: the chunk-parallel passes and
 // the one the last launch picks from (the finishing workgroup keeps its own
 // in LDS)
 constexpr int RX_HISTS = RX_FAST_PASSES + 1;
+// Bits of pass i's digit: RX_RB, except 6 for the second pass.  The first
+// digit (sign and the top of the exponent) leaves a whole binade range of
+// scores in its threshold bin (about 29 000 of the 131 072 keys of a C5 row),
+// which the second pass histograms; at 6 bits each chunk adds at most 64
+// bins into the row's histogram with device atomics instead of ~600 at 11
+// bits.  Three passes fix 28 bits, four 39.
+__device__ __forceinline__ int rx_digit_bits(uint32_t pass) { return pass == 1 ? 6 : RX_RB; }
 
 // Status bits raised by kernels of this library on the current device, read
 // and cleared by la_device_status.
@@ -110,7 +119,10 @@ __global__ __launch_bounds__(TK_NT) void rx_setup_kernel(RxKP a, int hist0_exter
 // which runs the remaining passes, then counts and writes chunk after chunk
 // in index order (one read of the row per pass, one for the count and the
 // write together), while the row's other workgroups exit.
-__global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int last) {
+// `guess`: the pass whose histogram this launch picks from in the common case
+// (-1: none); it is read before the row state, together with the chunk's
+// scores, so that the launch waits for one memory round trip instead of three.
+__global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int last, int guess) {
   __shared__ uint32_t hist[RX_BINS];
   __shared__ uint32_t eqc[RX_KPT][TK_NW];  // per slot and wave: threshold keys
   __shared__ uint32_t tkc[RX_KPT][TK_NW];  // per slot and wave: keys taken
@@ -119,6 +131,24 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const TopkKParams &p = a.p;
   const int64_t c = blockIdx.x, gi = blockIdx.y, NG = p.NG;
+  const TkRow rw = tk_row(p, gi);
+  const int64_t n_v = rw.n_v;
+  // thread t holds bins RX_BINS - 1 - RX_BPT t downwards of a histogram
+  auto read_bins = [&](const uint32_t *h, uint32_t (&hv)[RX_BPT]) {
+#pragma unroll
+    for (int e = 0; e < RX_BPT; ++e) hv[e] = h[RX_BINS - 1 - RX_BPT * tid - e];
+  };
+  // the prefetch: the likely histogram first, then the chunk's scores (loads
+  // complete in order, so the pick below waits for the histogram only)
+  uint32_t hpre[RX_BPT];
+  if (guess >= 0) read_bins(a.hist + (gi * RX_HISTS + guess) * RX_BINS, hpre);
+  double vraw[RX_KPT];
+  {
+    const int64_t x0 = c * RX_CHUNK + tid;
+    const double *rp = p.scores + rw.br * p.row_stride;
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) vraw[j] = x0 + (int64_t)j * TK_NT < n_v ? rp[x0 + (int64_t)j * TK_NT] : 0.0;
+  }
   // the row state as scalars (a copy of the whole struct would live in
   // memory); the row's chunk-0 workgroup writes the next launch's copy
   const RxState *sin = a.state + (launch & 1) * NG + gi;
@@ -141,8 +171,6 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     sout->phase = next_phase;
     sout->top = top;
   };
-  const TkRow rw = tk_row(p, gi);
-  const int64_t n_v = rw.n_v;
   const uint32_t K = (uint32_t)rw.K;
   const bool ord1 = p.order == 1;
   int32_t *oi = p.out_idx + rw.orow * p.width;
@@ -160,24 +188,23 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     for (int j = 0; j < RX_KPT; ++j) u[j] = ord_key(v[j]);
   };
   auto valid = [&](int64_t x, int j) { return x * RX_CHUNK + tid + (int64_t)j * TK_NT < n_v; };
-  // the digit below the fixed bits: its shift and mask
+  // the digit below the fixed bits (the width of pass `pass`): its shift
+  // and mask
   auto digit = [&](int &shift, uint32_t &dm) {
-    shift = top >= RX_RB - 1 ? top - (RX_RB - 1) : 0;
+    const int wd = rx_digit_bits(pass);
+    shift = top >= wd - 1 ? top - (wd - 1) : 0;
     dm = (2u << (top - shift)) - 1u;
   };
-  // picks the bin of the need-th largest matching key from a complete
-  // histogram h of the current digit (thread t holds bins RX_BINS - 1 -
-  // RX_BPT t downwards) and moves the state past it
-  auto pick = [&](const uint32_t *h) {
+  // picks the bin of the need-th largest matching key from the bins hv of a
+  // complete histogram of the current digit (read_bins) and moves the state
+  // past it
+  auto pick_bins = [&](const uint32_t (&hv)[RX_BPT]) {
     int shift;
     uint32_t dm;
     digit(shift, dm);
-    uint32_t hv[RX_BPT], csum = 0, all;
+    uint32_t csum = 0, all;
 #pragma unroll
-    for (int e = 0; e < RX_BPT; ++e) {
-      hv[e] = h[RX_BINS - 1 - RX_BPT * tid - e];
-      csum += hv[e];
-    }
+    for (int e = 0; e < RX_BPT; ++e) csum += hv[e];
     const uint32_t incl = tk_block_incl_scan(csum, wtmp[0], all);
     if (incl >= need && incl - csum < need) {
       uint32_t acc = incl - csum;
@@ -202,6 +229,11 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     // the whole bin is taken, or every bit is fixed (the rest are index ties)
     phase = (s_cnt == need || shift == 0) ? RX_COUNT : RX_PASS;
     __syncthreads();  // s_* are read before they are written again
+  };
+  auto pick = [&](const uint32_t *h) {
+    uint32_t hv[RX_BPT];
+    read_bins(h, hv);
+    pick_bins(hv);
   };
   // adds the chunk's keys that match the prefix to the LDS histogram
   auto hist_chunk = [&](int64_t x, const uint64_t (&u)[RX_KPT]) {
@@ -324,9 +356,15 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
 
   // the pick of the pass the previous launch histogrammed: every workgroup
   // of the row reads the complete histogram and makes the same pick
-  if (pend) pick(a.hist + (gi * RX_HISTS + pass) * RX_BINS);
+  if (pend) {
+    if ((int)pass == guess)
+      pick_bins(hpre);
+    else
+      pick(a.hist + (gi * RX_HISTS + pass) * RX_BINS);
+  }
   uint64_t u[RX_KPT];
-  load(c, u);
+#pragma unroll
+  for (int j = 0; j < RX_KPT; ++j) u[j] = ord_key(vraw[j]);
 
   if (phase == RX_PASS) {
     for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
@@ -431,7 +469,10 @@ int topk_radix_finish(const TopkKParams &p, const RadixPlan &R, void *ws, bool h
   // row whose threshold is still open in one workgroup)
   const int launches = RX_FAST_PASSES - (hist0_external ? 1 : 0) + 2;
   for (int s = 0; s < launches; ++s) {
-    rx_stage_kernel<<<grid, TK_NT, 0, st>>>(a, s, s == launches - 1 ? 1 : 0);
+    // launch s picks pass s (pass 0 histogrammed by the scores' kernel) or
+    // s - 1 in the common case; the last launch only writes
+    const int guess = s == launches - 1 ? -1 : s - (hist0_external ? 0 : 1);
+    rx_stage_kernel<<<grid, TK_NT, 0, st>>>(a, s, s == launches - 1 ? 1 : 0, guess);
     LA_LAUNCHED();
   }
   if (p.order == 0) {
