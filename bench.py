@@ -402,7 +402,8 @@ def bench_c3(dev, steps, warmup, keep=None):
             "TFLOPs_fp8_kv": round(flops / (ms8 * 1e-3) / 1e12, 1),
             "note": "useful FLOPs (bf16 QK^T, fp16 weights x V); ms_prefill includes the fp16 V "
                     "conversion pre-pass; *_fp8_kv: the same lists over an fp8 e4m3 K/V cache "
-                    "(K codes scored by fp16 MFMA, per-key scales, V dequantized)"}
+                    "(K codes scored on the fp8 matrix cores against q as two e4m3 terms, "
+                    "per-key scales, V dequantized to fp16)"}
 
 
 def bench_c5(dev, steps, warmup, keep=None):

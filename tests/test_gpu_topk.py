@@ -66,15 +66,19 @@ def test_topk_radix_long_rows_every_depth(dev, order):
     """Long rows of the multi-workgroup radix select (200000 keys, 49 chunks):
     a row of equal keys (every digit pass runs, then index ties), a row of
     keys equal above their lowest bits, a row whose valid prefix is shorter
-    than k (everything taken), an empty row, and an ordinary row.  The
-    device status stays clean, and a second call on the same scores gives the
-    same result (the per-call state starts from scratch)."""
+    than k (everything taken), an empty row, an ordinary row, and a row whose
+    keys share their leading 28 bits (the three first digits: 11, 6 and 11
+    bits) and spread over the fourth digit's 2048 values (the fourth
+    chunk-parallel pass runs, exact ties remain).  The device status stays
+    clean, and a second call on the same scores gives the same result (the
+    per-call state starts from scratch)."""
     n, k = 200000, 5000
     g = torch.Generator().manual_seed(13)
-    sc = torch.randn(1, 1, 5, n, generator=g, dtype=torch.float64)
+    sc = torch.randn(1, 1, 6, n, generator=g, dtype=torch.float64)
     sc[0, 0, 0] = 0.75
     sc[0, 0, 1] = 1.5 + torch.randint(0, 4, (n,), generator=g).double() * 2.0 ** -51
-    nv = torch.tensor([n, n, k - 7, 0, n - 3], dtype=torch.int32)
+    sc[0, 0, 5] = 1.5 + torch.randint(0, 2048, (n,), generator=g).double() * 2.0 ** -27
+    nv = torch.tensor([n, n, k - 7, 0, n - 3, n], dtype=torch.int32)
     N.device_status(dev)
     for _ in range(2):
         ids, counts, _ = _topk(sc.to(dev), k=k, width=k, group=1, order=order, pos_offset=0,
