@@ -20,6 +20,8 @@ int num_cus();
 // Status bits of prefill.hip's kernels on the current device (read after the
 // caller synchronised), optionally cleared.
 int prefill_status(uint32_t *bits, bool clear, hipStream_t st);
+// The same for indexer.hip's kernels.
+int indexer_status(uint32_t *bits, bool clear, hipStream_t st);
 
 #define LA_REQUIRE(cond, ...)                               \
   do {                                                      \

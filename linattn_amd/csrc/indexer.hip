@@ -22,7 +22,11 @@
 // (topk.hip) selects from them.
 #include <algorithm>
 
+#include <atomic>
+#include <random>
+
 #include "common.h"
+
 #include "topk.h"
 
 namespace la {
@@ -42,7 +46,16 @@ struct IdxKP {
   // histogram of each batch row, [b * hist_stride + bin], fed with the valid keys
   uint32_t *hist0;
   int64_t hist_stride;
+  // with rx_ready: the first workgroup of batch row b clears the row's
+  // hist_stride words of radix records, then stores rx_gen into rx_ready[b];
+  // every workgroup waits for that value before adding into the histogram
+  uint64_t *rx_ready;
+  uint64_t rx_gen;
 };
+
+// Status bits this file's kernels raise on the current device (read through
+// la_device_status).
+__device__ uint32_t la_ix_status;
 
 constexpr int IT_Q = 64, IT_K = 128, IT_D = 64;  // tile, d slice
 constexpr int IT_NT = 256;
@@ -396,7 +409,7 @@ __device__ __forceinline__ void wait_chunks(u32x4 (&v)[CH]) {
 
 static size_t decode16_lds(int64_t tn, int64_t HI, int64_t d, bool hist0) {
   return (size_t)(4 * 64 * (2 * d + 16) + ((tn * HI * d + 3) & ~3) * 4 + tn * HI * 8) +
-         (hist0 ? RX_BINS * 4 : 0);
+         (hist0 ? RX_BINS * 4 + 16 : 0);
 }
 
 // waves per SIMD the registers are sized for (two tiles of 16-byte chunks in
@@ -425,6 +438,7 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
   float *sqf = (float *)(smem + 4 * 64 * hs);            // q [tn][hd] (fp32: exact for 2-byte inputs)
   double *sw = (double *)(sqf + ((tn * hd + 3) & ~3));   // head weights [tn][HI]
   uint32_t *lh = (uint32_t *)(sw + tn * HI);             // first-digit histogram (hist0)
+  uint32_t *s_ok = lh + RX_BINS;                          // the flush's go-ahead (hist0)
   const bool hist = TN1 && p.hist0 != nullptr;
   // the keys the top-k sees: a causal decode query at pos sees keys s <= pos / unit
   int64_t n_v = p.Tk;
@@ -434,6 +448,44 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
   }
   if (hist)
     for (int i = tid; i < RX_BINS; i += 256) lh[i] = 0u;
+  const bool prep = hist && p.rx_ready != nullptr;
+  if (prep && blockIdx.x == 0) {  // the row's radix records start from zero
+    uint4 *r = (uint4 *)(p.hist0 + b * p.hist_stride);
+    for (int64_t i = tid; i < p.hist_stride / 4; i += 256) r[i] = make_uint4(0, 0, 0, 0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // every wave's zeros reach the device
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(&p.rx_ready[b], p.rx_gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // Adds this workgroup's first-digit counts into the row's histogram, after
+  // the row's records are cleared (a wait on the row's first workgroup, which
+  // is dispatched before every other workgroup of the row and clears them
+  // before anything else; the wait is bounded, a hardware-fault guard that
+  // raises LA_DEV_TOPK_TIMEOUT and leaves the counts out).
+  auto flush = [&]() {
+    if (tid == 0) {
+      uint32_t ok = 1, spins = 0;
+      if (prep) {
+        while (__hip_atomic_load(&p.rx_ready[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != p.rx_gen) {
+          if (++spins > (1u << 20)) {
+            ok = 0;
+            __hip_atomic_fetch_or(&la_ix_status, (uint32_t)LA_DEV_TOPK_TIMEOUT, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the zeros before the adds
+      }
+      *s_ok = ok;
+    }
+    __syncthreads();
+    if (!*s_ok) return;
+    for (int i = tid; i < RX_BINS; i += 256) {
+      const uint32_t x = lh[i];
+      if (x) __hip_atomic_fetch_add(&p.hist0[b * p.hist_stride + i], x, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
   const uint16_t *kb = (const uint16_t *)p.k + b * p.k_sb;
   // wave tiles of this workgroup: [wt0, wt0 + 4 * tiles * HI / ... ) interleaved over waves
   const int64_t n_wt = (p.Tk + KW - 1) / KW;
@@ -449,14 +501,7 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
     sw[i] = (double)p.w[b * p.w_sb + (p.t0 + i / HI) * p.w_st + (i % HI) * p.w_sh];
   __syncthreads();
   if (nw == 0) {  // no tiles for this wave: only the histogram's flush remains
-    if (hist) {
-      __syncthreads();
-      for (int i = tid; i < RX_BINS; i += 256) {
-        const uint32_t x = lh[i];
-        if (x) __hip_atomic_fetch_add(&p.hist0[b * p.hist_stride + i], x, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    if (hist) flush();
     return;
   }
   // chunk i of lane l in the coalesced load of a wave tile: c = i*64 + l of
@@ -557,14 +602,7 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
     }
   }
   wait_vmcnt<0>();  // drain the last (repeated) loads before the wave ends
-  if (hist) {
-    __syncthreads();
-    for (int i = tid; i < RX_BINS; i += 256) {
-      const uint32_t x = lh[i];
-      if (x) __hip_atomic_fetch_add(&p.hist0[b * p.hist_stride + i], x, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  if (hist) flush();
 }
 
 template <int HI, bool TN1, bool BF>
@@ -649,6 +687,41 @@ static TopkKParams topk_params(const la_indexer_args *a, double *scores, int64_t
   return tp;
 }
 
+// The status word read (and, with clear, reset) in one atomic exchange on the
+// caller's stream.
+__device__ uint32_t la_ix_status_snap;
+__global__ void ix_status_kernel(int clear) {
+  la_ix_status_snap = clear ? __hip_atomic_exchange(&la_ix_status, 0u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT)
+                            : __hip_atomic_load(&la_ix_status, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+}
+
+namespace la {
+int indexer_status(uint32_t *bits, bool clear, hipStream_t st) {
+  ix_status_kernel<<<1, 1, 0, st>>>(clear ? 1 : 0);
+  LA_LAUNCHED();
+  LA_HIP(hipMemcpyFromSymbolAsync(bits, HIP_SYMBOL(la_ix_status_snap), sizeof(uint32_t), 0,
+                                  hipMemcpyDeviceToHost, st));
+  LA_HIP(hipStreamSynchronize(st));
+  return LA_OK;
+}
+}  // namespace la
+
+// A value unique to each call in this process (never 0), for the rows' ready
+// words: a word left over from an earlier call, or from whatever the
+// workspace held before, never equals it (the counter starts at a random
+// 64-bit value).
+static uint64_t next_radix_gen() {
+  static std::atomic<uint64_t> gen{[] {
+    std::random_device rd;
+    return ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+  }()};
+  uint64_t g = gen.fetch_add(1) + 1;
+  while (g == 0) g = gen.fetch_add(1) + 1;
+  return g;
+}
+
 static int64_t scores_bytes(const la_indexer_args *a, int64_t chunk) {
   return (a->B * chunk * a->Tk * 8 + 255) / 256 * 256;
 }
@@ -704,12 +777,15 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     void *tws = (char *)a->workspace + sc_bytes;
     // a decode step whose rows go to the multi-workgroup radix select: the
     // scores kernel histograms the first digit on the way
+    // and clears the rows' radix records itself (no set-up launch)
     const RadixPlan R = decode16 && p.tn == 1 ? topk_long_plan(tp) : RadixPlan{};
     if (R.C > 0) {
-      rc = topk_radix_setup(tp, R, tws, true, st);
-      if (rc != LA_OK) return rc;
-      p.hist0 = radix_hist0(tp, tws);
-      p.hist_stride = radix_hist_stride();
+      LA_REQUIRE(tp.NG < 65536, "la_indexer_topk: at most 65535 batch rows per call");
+      const RadixRowPrep rp = radix_row_prep(tp, R, tws);
+      p.hist0 = rp.rows;
+      p.hist_stride = rp.row_words;
+      p.rx_ready = rp.ready;
+      p.rx_gen = next_radix_gen();
     }
     if (decode16) {
       switch (a->HI) {
@@ -734,7 +810,7 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
         indexer_tile_kernel<<<grid, IT_NT, 0, st>>>(p);
     }
     LA_LAUNCHED();
-    rc = R.C > 0 ? topk_radix_finish(tp, R, tws, true, st)
+    rc = R.C > 0 ? topk_radix_finish(tp, R, tws, true, true, st)
                  : topk_launch_ws(tp, tws, a->ws_bytes - sc_bytes, st);
     if (rc != LA_OK) return rc;
   }

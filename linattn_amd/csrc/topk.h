@@ -88,15 +88,24 @@ constexpr int RX_RB = 11;  // radix digit bits
 constexpr int RX_BINS = 1 << RX_RB;
 RadixPlan radix_plan(const TopkKParams &p);
 int topk_radix_launch(const TopkKParams &p, const RadixPlan &R, void *ws, hipStream_t st);
-// The same in two parts, for a scores kernel that histograms the first digit
+// The same in parts, for a scores kernel that histograms the first digit
 // (the top RX_RB bits of ord_key of every valid key of row gi, added into
-// radix_hist0(p, ws)[gi * radix_hist_stride() + bin]) between them.
+// rows + gi * row_words + bin of radix_row_prep) in between: set-up, that
+// kernel, then the stage launches.  Or without the set-up launch
+// (state_in_kernel): the scores kernel clears row gi's row_words words and
+// then stores a value unique to the call into ready[gi], before any of its
+// workgroups adds into the row's histogram (each waits for that value
+// first); the first stage launch starts the rows from their initial state.
+struct RadixRowPrep {
+  uint32_t *rows = nullptr;
+  int64_t row_words = 0;
+  uint64_t *ready = nullptr;
+};
+RadixRowPrep radix_row_prep(const TopkKParams &p, const RadixPlan &R, void *ws);
 int topk_radix_setup(const TopkKParams &p, const RadixPlan &R, void *ws, bool hist0_external,
                      hipStream_t st);
 int topk_radix_finish(const TopkKParams &p, const RadixPlan &R, void *ws, bool hist0_external,
-                      hipStream_t st);
-uint32_t *radix_hist0(const TopkKParams &p, void *ws);
-int64_t radix_hist_stride();
+                      bool state_in_kernel, hipStream_t st);
 // The radix plan when topk_launch_ws sends these rows to the radix select
 // (else C = 0).
 RadixPlan topk_long_plan(const TopkKParams &p);

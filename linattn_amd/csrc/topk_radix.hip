@@ -6,31 +6,47 @@
 // selection is an MSB-first radix select over the 64-bit order keys, run as a
 // fixed sequence of launches of one kernel, rx_stage_kernel; every launch
 // moves each row one phase on:
-//   PASS    histogram one RX_RB-bit digit of the keys that match the
-//           threshold prefix (device-scope atomics into the row's histogram
-//           of that pass);
-//   COUNT   count each chunk's keys above / equal to the final threshold;
-//   WRITE   write the selected indices in increasing index order (order 1),
-//           or the candidate (score, index) rows that topk_launch then sorts
-//           (order 0).
+//   PASS    histogram one digit of the keys that match the threshold prefix
+//           (device-scope atomics into the row's histogram of that pass);
+//   CAND    (when at most RX_CAND_CAP keys match the prefix) collect those
+//           keys into the row's candidate list instead;
+//   COUNT   count each chunk's keys above / equal to the final threshold and
+//           write the chunk's selected indices in increasing index order
+//           (order 1), or the candidate (score, index) rows that topk_launch
+//           then sorts (order 0), after the counts of the chunks before it.
 // A launch begins by picking the threshold bin of the pass the previous
 // launch histogrammed: every workgroup of the row reads the complete
-// histogram (the launch boundary orders it) and makes the same pick, so no
-// workgroup ever waits for another and no launch needs the others resident.
-// The row state a launch reads is the one the previous launch wrote (two
-// copies, by launch parity), written by the row's chunk-0 workgroup.  Rows
-// that finish early do nothing in the remaining launches.
+// histogram (the launch boundary orders it) and makes the same pick; a row
+// whose keys were collected is settled instead by every workgroup from the
+// candidate list alone (the remaining digits, histogrammed in LDS), and
+// counts and writes in the same launch.  The row state a launch reads is the
+// one the previous launch wrote (two copies, by launch parity), written by
+// the row's chunk-0 workgroup.  Rows that finish early do nothing in the
+// remaining launches.
 //
-// The sequence is short: RX_FAST_PASSES chunk-parallel passes (three, 28
-// bits fixed, settle the threshold of scores spread over their leading bits;
-// the fourth runs only for rows they leave open), the count, and a last
-// launch that writes.  A row still undecided by
-// then (keys tied over most of their bits) is finished in that last launch
-// by one workgroup, which loops over the row's chunks.
+// The output offset of a chunk is the number of keys the chunks before it
+// select: each chunk publishes its counts in one 64-bit record, then its
+// inclusive prefix, and looks back over the records of the chunks before it
+// (decoupled look-back).  Workgroup (c, r) waits only for workgroups (x, r),
+// x < c, of lower linear id; those are dispatched before it and publish
+// before they wait themselves, so no wait depends on a workgroup that is not
+// yet running, and no launch needs its workgroups resident together.  The
+// waits are bounded (a hardware-fault guard: past the bound the chunk's
+// output is skipped and LA_DEV_TOPK_TIMEOUT raised).
+//
+// The sequence is short: RX_FAST_PASSES chunk-parallel passes at most (28
+// bits: digits of 11, 6 and 11 bits), then one launch more.  Scores spread
+// over their leading bits leave a few hundred keys in the threshold bin
+// after two digits: they are collected, and the last launch settles, counts
+// and writes.  A row still undecided after the last chunk-parallel pass and
+// never collected (over RX_CAND_CAP keys tied over 28 bits) is finished in
+// the last launch by one workgroup, which loops over the row's chunks.
 //
 // The first pass's histogram (the top RX_RB bits) may come from the kernel
 // that writes the scores (the decode indexer, indexer_decode16_kernel),
-// which saves a launch and a read of the scores.
+// which saves a launch and a read of the scores; that kernel may also clear
+// the rows' records and the first launch start from the initial state, which
+// saves the set-up launch.  C5 then runs the indexer and three launches.
 //
 // The selection equals tk_select's over the whole row: the K largest keys,
 // threshold ties taken lowest index first.
@@ -44,16 +60,29 @@ namespace la {
 constexpr int RX_KPT = 16;                              // keys per thread
 constexpr int64_t RX_CHUNK = (int64_t)TK_NT * RX_KPT;  // keys per workgroup
 constexpr int RX_BPT = RX_BINS / TK_NT;                // bins per thread when picking
-enum { RX_PASS = 0, RX_COUNT = 1, RX_WRITE = 2, RX_DONE = 3 };
-// digit passes run chunk-parallel: up to four (39 bits fixed); rows that
-// need more finish in one workgroup in the last launch.  A row whose
-// threshold the first three settle (28 bits: scores spread over their
-// leading bits) counts and writes a launch early and skips the rest.
-constexpr int RX_FAST_PASSES = 4;
-// digit histograms in the workspace per row: the chunk-parallel passes and
-// the one the last launch picks from (the finishing workgroup keeps its own
-// in LDS)
-constexpr int RX_HISTS = RX_FAST_PASSES + 1;
+enum { RX_PASS = 0, RX_COUNT = 1, RX_CAND = 2, RX_DONE = 3 };
+// Chunk records (64 bits): the flag in bits 62-63 (0 none, RX_AGG the chunk's
+// own counts, RX_INC the counts of chunks 0..c), keys above the threshold in
+// bits 31-61, keys equal to it in bits 0-30 (a row holds < 2^31 keys).
+constexpr uint64_t RX_AGG = 1ull << 62, RX_INC = 2ull << 62;
+constexpr uint32_t RX_SPIN_LIMIT = 1u << 20;  // polls before a wait is given up
+// digit passes run chunk-parallel: up to three (28 bits fixed); a row that
+// needs more, and whose keys matching the threshold prefix were not few
+// enough to be collected (RX_CAND_CAP), finishes in one workgroup in the
+// last launch.
+constexpr int RX_FAST_PASSES = 3;
+// When at most this many keys of a row match the threshold prefix after a
+// pick, the row's workgroups collect them (the keys only) instead of
+// histogramming the next digit, and in the next launch every workgroup of the
+// row settles the threshold from them alone, in LDS, then counts and writes:
+// the remaining passes cost no launches.  (About 450 keys of a C5 row match
+// after the first two digits.)
+constexpr int RX_CAND_CAP = 4096;
+constexpr int RX_CPT = RX_CAND_CAP / TK_NT;  // candidates per thread
+constexpr int RX_CPRE = 4;  // of them read before the row state in the last launch
+// digit histograms in the workspace per row, one per chunk-parallel pass (the
+// finishing workgroup keeps its own in LDS)
+constexpr int RX_HISTS = RX_FAST_PASSES;
 // Bits of pass i's digit: RX_RB, except 6 for the second pass.  The first
 // digit (sign and the top of the exponent) leaves a whole binade range of
 // scores in its threshold bin (about 29 000 of the 131 072 keys of a C5 row),
@@ -72,56 +101,79 @@ struct RxState {
   uint32_t need;          // keys equal to the prefix still to take (lowest index first)
   uint32_t pass;          // the pass histogrammed next (or last, while pend)
   uint32_t pend;          // pass `pass`'s histogram is complete and not yet picked
-  uint32_t phase;         // RX_PASS, RX_COUNT, RX_WRITE or RX_DONE
+  uint32_t phase;         // RX_PASS, RX_COUNT or RX_DONE
   int32_t top;            // highest bit of pass `pass`'s digit
-  uint32_t pad[3];
+  uint32_t ncand;         // RX_CAND: keys collected (those matching the prefix)
+  uint32_t pad[2];
 };
 static_assert(sizeof(RxState) == 48, "RxState layout");
 
 struct RxKP {
   TopkKParams p;
   RxState *state;     // [2][NG]
-  uint32_t *hist;     // [NG][RX_HISTS][RX_BINS]
-  uint32_t *chunk;    // [NG][C][2]: keys above / equal to the final threshold
+  // per row, row_words 32-bit words: the digit histograms [RX_HISTS][RX_BINS],
+  // the chunk records (uint64_t [C]), the candidates' count (4 words) and the
+  // candidate keys (uint64_t [RX_CAND_CAP])
+  uint32_t *rows;
+  int64_t row_words;
   double *cand_sc;    // order 0: candidate rows [NG][k], sorted afterwards
   int32_t *cand_id;
   int64_t C;
+  int32_t state_in_kernel;  // launch 0 starts from the initial state (no set-up launch)
 };
 
-// Zeroes a row's histograms and sets its first phase: the radix passes
-// (pass 0 pending a pick when the scores' kernel histograms it), or straight
-// to counting when every valid key is taken.  One workgroup per row.
+__device__ __forceinline__ uint32_t *rx_hist(const RxKP &a, int64_t gi, uint32_t pass) {
+  return a.rows + gi * a.row_words + (int64_t)pass * RX_BINS;
+}
+__device__ __forceinline__ uint64_t *rx_rec(const RxKP &a, int64_t gi) {
+  return (uint64_t *)(a.rows + gi * a.row_words + RX_HISTS * RX_BINS);
+}
+__device__ __forceinline__ uint32_t *rx_ccount(const RxKP &a, int64_t gi) {
+  return a.rows + gi * a.row_words + RX_HISTS * RX_BINS + 2 * a.C;
+}
+__device__ __forceinline__ uint64_t *rx_cand(const RxKP &a, int64_t gi) {
+  return (uint64_t *)(a.rows + gi * a.row_words + RX_HISTS * RX_BINS + 2 * a.C + 4);
+}
+
+// The state a row starts from: the radix passes (pass 0 pending a pick when
+// the scores' kernel histograms it), or straight to counting when every
+// valid key is taken.
+__device__ __forceinline__ RxState rx_initial(const TkRow &rw, bool hist0_external) {
+  const uint32_t K = (uint32_t)rw.K, n_v = (uint32_t)rw.n_v;
+  RxState s{};
+  s.top = 63;
+  s.need = K;
+  if (K == 0 || K >= n_v) {  // none or every valid key taken: the empty prefix decides
+    s.phase = RX_COUNT;
+  } else {
+    s.phase = RX_PASS;
+    s.pend = hist0_external ? 1u : 0u;
+  }
+  return s;
+}
+
+// Zeroes a row's histograms and chunk records and sets its first phase.  One
+// workgroup per row.
 __global__ __launch_bounds__(TK_NT) void rx_setup_kernel(RxKP a, int hist0_external) {
   const int64_t gi = blockIdx.x;
   const TkRow rw = tk_row(a.p, gi);
-  uint4 *h = (uint4 *)(a.hist + gi * RX_HISTS * RX_BINS);
-  for (int i = threadIdx.x; i < RX_HISTS * RX_BINS / 4; i += TK_NT) h[i] = make_uint4(0, 0, 0, 0);
-  if (threadIdx.x == 0) {
-    const uint32_t K = (uint32_t)rw.K, n_v = (uint32_t)rw.n_v;
-    RxState s{};
-    s.top = 63;
-    s.need = K;
-    if (K == 0 || K >= n_v) {  // none or every valid key taken: the empty prefix decides
-      s.phase = RX_COUNT;
-    } else {
-      s.phase = RX_PASS;
-      s.pend = hist0_external ? 1u : 0u;
-    }
-    a.state[gi] = s;
-  }
+  uint4 *h = (uint4 *)(a.rows + gi * a.row_words);
+  for (int64_t i = threadIdx.x; i < a.row_words / 4; i += TK_NT) h[i] = make_uint4(0, 0, 0, 0);
+  if (threadIdx.x == 0) a.state[gi] = rx_initial(rw, hist0_external != 0);
 }
 
-// Launch `launch` of a row's stage sequence.  Launches before the last one
-// run the phases chunk-parallel (above).  The last launch writes the rows
-// that have reached the write phase the same way; a row that has not (its
-// threshold still undecided after the chunk-parallel passes: keys tied over
-// many of their leading bits) is finished by its chunk-0 workgroup alone,
-// which runs the remaining passes, then counts and writes chunk after chunk
-// in index order (one read of the row per pass, one for the count and the
-// write together), while the row's other workgroups exit.
+// Launch `launch` of a row's stage sequence, chunk-parallel (above).  In the
+// last launch, a row whose threshold is still undecided after the
+// chunk-parallel passes (keys tied over many of their leading bits) is
+// finished by its chunk-0 workgroup alone, which runs the remaining passes,
+// then counts and writes chunk after chunk in index order (one read of the
+// row per pass, one for the count and the write together), while the row's
+// other workgroups exit.
 // `guess`: the pass whose histogram this launch picks from in the common case
 // (-1: none); it is read before the row state, together with the chunk's
 // scores, so that the launch waits for one memory round trip instead of three.
+// The last launch reads the first RX_CPRE * TK_NT candidate slots that way
+// instead (rows collected by the launch before it, the common case).
 __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int last, int guess) {
   __shared__ uint32_t hist[RX_BINS];
   __shared__ uint32_t eqc[RX_KPT][TK_NW];  // per slot and wave: threshold keys
@@ -141,7 +193,13 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
   // the prefetch: the likely histogram first, then the chunk's scores (loads
   // complete in order, so the pick below waits for the histogram only)
   uint32_t hpre[RX_BPT];
-  if (guess >= 0) read_bins(a.hist + (gi * RX_HISTS + guess) * RX_BINS, hpre);
+  if (guess >= 0) read_bins(rx_hist(a, gi, (uint32_t)guess), hpre);
+  uint64_t cpre[RX_CPRE];
+  if (last) {
+    const uint64_t *cd = rx_cand(a, gi);
+#pragma unroll
+    for (int e = 0; e < RX_CPRE; ++e) cpre[e] = cd[tid + e * TK_NT];
+  }
   double vraw[RX_KPT];
   {
     const int64_t x0 = c * RX_CHUNK + tid;
@@ -154,15 +212,19 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
   const RxState *sin = a.state + (launch & 1) * NG + gi;
   RxState *sout = a.state + ((launch + 1) & 1) * NG + gi;
   const bool writer = c == 0 && tid == 0;
-  uint32_t phase = sin->phase;
+  const bool init = a.state_in_kernel && launch == 0;
+  const RxState s0 = init ? rx_initial(rw, true) : RxState{};
+  uint32_t phase = init ? s0.phase : sin->phase;
   if (phase == RX_DONE) {
     if (writer) sout->phase = RX_DONE;
     return;
   }
-  uint64_t prefix = sin->prefix, mask = sin->mask;
-  uint32_t need = sin->need, pass = sin->pass, pend = sin->pend;
-  int top = sin->top;
-  auto publish = [&](uint32_t next_phase, uint32_t next_pend) {
+  uint64_t prefix = init ? s0.prefix : sin->prefix, mask = init ? s0.mask : sin->mask;
+  uint32_t need = init ? s0.need : sin->need, pass = init ? s0.pass : sin->pass;
+  uint32_t pend = init ? s0.pend : sin->pend;
+  int top = init ? s0.top : sin->top;
+  const uint32_t ncand = init ? 0u : sin->ncand;
+  auto publish = [&](uint32_t next_phase, uint32_t next_pend, uint32_t next_ncand) {
     sout->prefix = prefix;
     sout->mask = mask;
     sout->need = need;
@@ -170,12 +232,16 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     sout->pend = next_pend;
     sout->phase = next_phase;
     sout->top = top;
+    sout->ncand = next_ncand;
   };
+  // the keys matching the prefix: all valid keys before any pick, the
+  // picked bin's count after one (unknown otherwise)
+  uint32_t nmatch = mask == 0 ? (uint32_t)n_v : 0xffffffffu;
   const uint32_t K = (uint32_t)rw.K;
   const bool ord1 = p.order == 1;
   int32_t *oi = p.out_idx + rw.orow * p.width;
   const uint64_t lt = lanemask_lt(lane);
-  uint32_t *chunk = a.chunk + gi * a.C * 2;
+  uint64_t *rec = rx_rec(a, gi);
 
   // the order keys of chunk x (thread t: keys x * RX_CHUNK + t + 256 j)
   auto load = [&](int64_t x, uint64_t (&u)[RX_KPT]) {
@@ -222,6 +288,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     }
     __syncthreads();
     need -= s_above;
+    nmatch = s_cnt;
     prefix |= (uint64_t)s_bin << shift;
     mask |= (uint64_t)dm << shift;
     top = shift - 1;
@@ -320,10 +387,18 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     }
   };
 
-  if (last && !(phase == RX_WRITE && !pend)) {
+  // the pick of the pass the previous launch histogrammed: every workgroup
+  // of the row reads the complete histogram and makes the same pick
+  if (pend) {
+    if ((int)pass == guess)
+      pick_bins(hpre);
+    else
+      pick(rx_hist(a, gi, pass));
+  }
+
+  if (phase == RX_PASS && last) {
     // ------------------------------------------- one-workgroup finish --
     if (c != 0) return;
-    if (pend) pick(a.hist + (gi * RX_HISTS + pass) * RX_BINS);
     uint64_t u[RX_KPT];
     while (phase == RX_PASS) {
       for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
@@ -354,62 +429,138 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     return;
   }
 
-  // the pick of the pass the previous launch histogrammed: every workgroup
-  // of the row reads the complete histogram and makes the same pick
-  if (pend) {
-    if ((int)pass == guess)
-      pick_bins(hpre);
-    else
-      pick(a.hist + (gi * RX_HISTS + pass) * RX_BINS);
-  }
   uint64_t u[RX_KPT];
 #pragma unroll
   for (int j = 0; j < RX_KPT; ++j) u[j] = ord_key(vraw[j]);
+
+  if (phase == RX_PASS && nmatch <= (uint32_t)RX_CAND_CAP) {
+    // ------------------------------------------------ collect candidates --
+    // the chunk's keys that match the prefix, appended to the row's
+    // candidates (in any order: the next launch needs the multiset only)
+    uint32_t mine = 0, tot;
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) mine += valid(c, j) && (u[j] & mask) == prefix;
+    const uint32_t incl = tk_block_incl_scan(mine, wtmp[0], tot);
+    if (tid == 0 && tot)
+      s_base = __hip_atomic_fetch_add(rx_ccount(a, gi), tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (tot) {
+      uint64_t *cd = rx_cand(a, gi);
+      uint32_t pos = s_base + incl - mine;
+#pragma unroll
+      for (int j = 0; j < RX_KPT; ++j)
+        if (valid(c, j) && (u[j] & mask) == prefix) {
+          if (pos < (uint32_t)RX_CAND_CAP) cd[pos] = u[j];  // (the bin's count bounds pos)
+          ++pos;
+        }
+    }
+    if (writer) publish(RX_CAND, 0u, nmatch);
+    return;
+  }
+
+  if (phase == RX_CAND) {
+    // ------------------------------------------- settle from candidates --
+    // the remaining digits over the collected keys, each workgroup of the
+    // row on its own (the same keys, the same picks), then the count and the
+    // write below
+    const uint32_t nc = min(ncand, (uint32_t)RX_CAND_CAP);
+    const uint64_t *cd = rx_cand(a, gi);
+    uint64_t ck[RX_CPT];
+#pragma unroll
+    for (int e = 0; e < RX_CPT; ++e) {
+      const uint32_t i = (uint32_t)(tid + e * TK_NT);
+      ck[e] = e < RX_CPRE && last ? cpre[e] : i < nc ? cd[i] : 0ull;
+    }
+    phase = RX_PASS;
+    while (phase == RX_PASS) {
+      for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
+      __syncthreads();
+      int shift;
+      uint32_t dm;
+      digit(shift, dm);
+#pragma unroll
+      for (int e = 0; e < RX_CPT; ++e)
+        if ((uint32_t)(tid + e * TK_NT) < nc && (ck[e] & mask) == prefix)
+          atomicAdd(&hist[(uint32_t)(ck[e] >> shift) & dm], 1u);
+      __syncthreads();
+      pick(hist);
+    }
+  }
 
   if (phase == RX_PASS) {
     for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
     __syncthreads();
     hist_chunk(c, u);
     __syncthreads();
-    uint32_t *gh = a.hist + (gi * RX_HISTS + pass) * RX_BINS;
+    uint32_t *gh = rx_hist(a, gi, pass);
     for (int b = tid; b < RX_BINS; b += TK_NT) {
       const uint32_t x = hist[b];
       if (x) __hip_atomic_fetch_add(&gh[b], x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (writer) publish(RX_PASS, 1u);
+    if (writer) publish(RX_PASS, 1u, 0u);
     return;
   }
 
-  if (phase == RX_COUNT) {
-    uint32_t gt_c, eq_c;
-    count_chunk(c, u, gt_c, eq_c);
-    if (tid == 0) {
-      chunk[2 * c] = gt_c;
-      chunk[2 * c + 1] = eq_c;
+  // ------------------------------------------------------ count and write --
+  // The chunk's counts, then its output offset and the threshold keys it
+  // takes from the counts of the chunks before it (decoupled look-back by
+  // wave 0: lanes read the records of chunks c - 1 - lane of a 64-record
+  // window, nearest first; a window is summed up to its nearest inclusive
+  // record, or whole when it holds only aggregates, then the next window).
+  uint32_t gt_c, eq_c;
+  count_chunk(c, u, gt_c, eq_c);
+  if (w == 0) {
+    const uint64_t own = ((uint64_t)gt_c << 31) | (uint64_t)eq_c;
+    // (the records carry their data in the word itself: relaxed device-scope
+    // atomics suffice, and no fence writes back or drops the caches)
+    if (lane == 0 && c > 0) __hip_atomic_store(&rec[c], RX_AGG | own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t gb = 0, eb = 0, spins = 0;
+    bool ok = true;
+    int64_t hi = c - 1;  // the window's nearest chunk
+    while (hi >= 0) {
+      const int64_t x = hi - lane;
+      uint64_t r = x >= 0 ? __hip_atomic_load(&rec[x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : RX_INC;
+      const uint64_t inc = __ballot((r & RX_INC) != 0);
+      const uint64_t none = __ballot((r >> 62) == 0);
+      // lanes up to and including the nearest inclusive record (all of them
+      // when there is none) must have published
+      const uint64_t upto = inc ? (inc & (~inc + 1)) * 2 - 1 : ~0ull;
+      if (none & upto) {
+        if (++spins > RX_SPIN_LIMIT) {
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        continue;
+      }
+      const bool mine = ((upto >> lane) & 1) != 0;
+      uint32_t g = mine ? (uint32_t)((r >> 31) & 0x7fffffffu) : 0u;
+      uint32_t e = mine ? (uint32_t)(r & 0x7fffffffu) : 0u;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        g += (uint32_t)__shfl_xor((int)g, o, 64);
+        e += (uint32_t)__shfl_xor((int)e, o, 64);
+      }
+      gb += g;
+      eb += e;
+      if (inc) break;
+      hi -= 64;
     }
-    if (writer) publish(RX_WRITE, 0u);
-    return;
+    if (lane == 0) {
+      if (ok) {
+        __hip_atomic_store(&rec[c], RX_INC | (((uint64_t)(gb + gt_c)) << 31) | (uint64_t)(eb + eq_c),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_base = gb + min(need, eb);
+        s_take = eb >= need ? 0u : min(need - eb, eq_c);
+      } else {
+        __hip_atomic_fetch_or(&la_dev_status, (uint32_t)LA_DEV_TOPK_TIMEOUT, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+        s_base = 0xffffffffu;
+      }
+    }
   }
-
-  // ---------------------------------------------------------------- write --
-  // this chunk's output offset and the threshold keys it takes, from the
-  // counts of the chunks before it
-  {
-    uint32_t gb = 0, eb = 0;
-    for (int64_t x = tid; x < c; x += TK_NT) {
-      gb += chunk[2 * x];
-      eb += chunk[2 * x + 1];
-    }
-    uint32_t gtot, etot;
-    tk_block_incl_scan(gb, wtmp[0], gtot);
-    tk_block_incl_scan(eb, wtmp[1], etot);
-    if (tid == 0) {
-      const uint32_t ex = chunk[2 * c + 1];
-      s_base = gtot + min(need, etot);
-      s_take = etot >= need ? 0u : min(need - etot, ex);
-    }
-    __syncthreads();
-  }
+  __syncthreads();
+  if (s_base == 0xffffffffu) return;  // the wait was given up: this chunk writes nothing
   write_chunk(c, u, s_base, s_take);
   pad(c * TK_NT + tid, a.C * TK_NT);
   if (writer) sout->phase = RX_DONE;
@@ -417,12 +568,18 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
 
 static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
+// 32-bit words per row: the digit histograms, then the chunk records (a
+// multiple of 4 words, so rows stay 16-byte aligned)
+static int64_t rx_row_words(int64_t C) {
+  return (RX_HISTS * RX_BINS + 2 * C + 4 + 2 * RX_CAND_CAP + 3) / 4 * 4;
+}
+
 RadixPlan radix_plan(const TopkKParams &p) {
   RadixPlan R;
   if (p.n >= ((int64_t)1 << 31)) return R;
   R.C = ceil_div(p.n, RX_CHUNK);
-  R.bytes = align256(2 * p.NG * (int64_t)sizeof(RxState)) +
-            align256(p.NG * RX_HISTS * RX_BINS * 4) + align256(p.NG * R.C * 8);
+  R.bytes = align256(2 * p.NG * (int64_t)sizeof(RxState)) + align256(p.NG * rx_row_words(R.C) * 4) +
+            align256(p.NG * 8);
   if (p.order == 0) R.bytes += align256(p.NG * p.k * 8) + align256(p.NG * p.k * 4);
   return R;
 }
@@ -434,10 +591,10 @@ static RxKP rx_args(const TopkKParams &p, const RadixPlan &R, void *ws) {
   a.C = R.C;
   a.state = (RxState *)base;
   base += align256(2 * p.NG * (int64_t)sizeof(RxState));
-  a.hist = (uint32_t *)base;
-  base += align256(p.NG * RX_HISTS * RX_BINS * 4);
-  a.chunk = (uint32_t *)base;
-  base += align256(p.NG * R.C * 8);
+  a.rows = (uint32_t *)base;
+  a.row_words = rx_row_words(R.C);
+  base += align256(p.NG * a.row_words * 4);
+  base += align256(p.NG * 8);  // the rows' ready words (RadixRowPrep)
   if (p.order == 0) {
     a.cand_sc = (double *)base;
     a.cand_id = (int32_t *)(base + align256(p.NG * p.k * 8));
@@ -445,10 +602,14 @@ static RxKP rx_args(const TopkKParams &p, const RadixPlan &R, void *ws) {
   return a;
 }
 
-uint32_t *radix_hist0(const TopkKParams &p, void *ws) {
-  return (uint32_t *)((char *)ws + align256(2 * p.NG * (int64_t)sizeof(RxState)));
+RadixRowPrep radix_row_prep(const TopkKParams &p, const RadixPlan &R, void *ws) {
+  const RxKP a = rx_args(p, R, ws);
+  RadixRowPrep r;
+  r.rows = a.rows;
+  r.row_words = a.row_words;
+  r.ready = (uint64_t *)((char *)a.rows + align256(p.NG * a.row_words * 4));
+  return r;
 }
-int64_t radix_hist_stride() { return (int64_t)RX_HISTS * RX_BINS; }
 
 int topk_radix_setup(const TopkKParams &p, const RadixPlan &R, void *ws, bool hist0_external,
                      hipStream_t st) {
@@ -460,17 +621,21 @@ int topk_radix_setup(const TopkKParams &p, const RadixPlan &R, void *ws, bool hi
 }
 
 int topk_radix_finish(const TopkKParams &p, const RadixPlan &R, void *ws, bool hist0_external,
-                      hipStream_t st) {
-  const RxKP a = rx_args(p, R, ws);
+                      bool state_in_kernel, hipStream_t st) {
+  if ((uintptr_t)ws % 16 != 0) return fail(LA_ERR_INVALID, "topk: workspace not 16-byte aligned");
+  LA_REQUIRE(p.NG < 65536, "topk: at most 65535 long rows per call");
+  LA_REQUIRE(!state_in_kernel || hist0_external,
+             "topk: the rows start in the first launch only after an external first pass");
+  RxKP a = rx_args(p, R, ws);
+  a.state_in_kernel = state_in_kernel ? 1 : 0;
   const dim3 grid((unsigned)R.C, (unsigned)p.NG);
-  // chunk-parallel launches for the passes that settle the threshold of
-  // scores spread over their leading bits (the first pass may come from the
-  // scores' kernel) and the count; the last launch writes (or finishes a
-  // row whose threshold is still open in one workgroup)
-  const int launches = RX_FAST_PASSES - (hist0_external ? 1 : 0) + 2;
+  // one launch per chunk-parallel pass (the first may come from the scores'
+  // kernel); a row counts and writes in the launch whose pick settles it, and
+  // the last launch finishes a row still open in one workgroup
+  const int launches = RX_FAST_PASSES + (hist0_external ? 0 : 1);
   for (int s = 0; s < launches; ++s) {
     // launch s picks pass s (pass 0 histogrammed by the scores' kernel) or
-    // s - 1 in the common case; the last launch only writes
+    // s - 1; the last one mostly settles collected rows (no histogram read)
     const int guess = s == launches - 1 ? -1 : s - (hist0_external ? 0 : 1);
     rx_stage_kernel<<<grid, TK_NT, 0, st>>>(a, s, s == launches - 1 ? 1 : 0, guess);
     LA_LAUNCHED();
@@ -493,7 +658,7 @@ int topk_radix_finish(const TopkKParams &p, const RadixPlan &R, void *ws, bool h
 int topk_radix_launch(const TopkKParams &p, const RadixPlan &R, void *ws, hipStream_t st) {
   const int rc = topk_radix_setup(p, R, ws, false, st);
   if (rc != LA_OK) return rc;
-  return topk_radix_finish(p, R, ws, false, st);
+  return topk_radix_finish(p, R, ws, false, false, st);
 }
 
 }  // namespace la
@@ -521,7 +686,11 @@ extern "C" int la_device_status(uint32_t *bits, int32_t clear, void *stream) {
   LA_HIP(hipStreamSynchronize(st));
   // status words of the other source files (each holds its own device symbol)
   uint32_t more = 0;
-  const int rc = prefill_status(&more, clear != 0, st);
+  int rc = prefill_status(&more, clear != 0, st);
+  if (rc != LA_OK) return rc;
+  *bits |= more;
+  more = 0;
+  rc = indexer_status(&more, clear != 0, st);
   if (rc != LA_OK) return rc;
   *bits |= more;
   return LA_OK;

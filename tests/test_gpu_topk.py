@@ -67,11 +67,11 @@ def test_topk_radix_long_rows_every_depth(dev, order):
     a row of equal keys (every digit pass runs, then index ties), a row of
     keys equal above their lowest bits, a row whose valid prefix is shorter
     than k (everything taken), an empty row, an ordinary row, and a row whose
-    keys share their leading 28 bits (the three first digits: 11, 6 and 11
-    bits) and spread over the fourth digit's 2048 values (the fourth
-    chunk-parallel pass runs, exact ties remain).  The device status stays
-    clean, and a second call on the same scores gives the same result (the
-    per-call state starts from scratch)."""
+    keys share their leading 28 bits (the three chunk-parallel digits: 11, 6
+    and 11 bits) and spread over the next digit's 2048 values (too many to
+    collect: the one-workgroup finish runs, exact ties remain).  The device
+    status stays clean, and a second call on the same scores gives the same
+    result (the per-call state starts from scratch)."""
     n, k = 200000, 5000
     g = torch.Generator().manual_seed(13)
     sc = torch.randn(1, 1, 6, n, generator=g, dtype=torch.float64)
@@ -88,6 +88,39 @@ def test_topk_radix_long_rows_every_depth(dev, order):
         want = ri if order == 0 else np.sort(np.where(ri < 0, n, ri), axis=-1)
         if order == 1:
             want = np.where(want == n, -1, want)
+        assert np.array_equal(ids[0, 0].cpu().numpy(), want)
+        assert np.array_equal(counts[0, 0].cpu().numpy(), np.minimum(nv.numpy(), k))
+
+
+@pytest.mark.parametrize("order", [1, 0])
+def test_topk_radix_candidates(dev, order):
+    """Long rows whose keys matching the threshold prefix are few enough to
+    collect (at most 4096): every workgroup of the row then settles the
+    remaining digits from the collected keys alone.  Valid prefixes of 3000
+    and 4096 keys (collected before any pass), 4097 (one pass first); 4096
+    keys in one first-digit bin above small noise, over 8 values (the
+    settle runs down to the last bit, then index ties), and 4097 such keys
+    (too many: the chunk-parallel passes and the one-workgroup finish); 4096
+    distinct keys in that bin; a row of negative keys."""
+    n, k = 200000, 1000
+    g = torch.Generator().manual_seed(17)
+    sc = torch.randn(1, 1, 7, n, generator=g, dtype=torch.float64)
+    for r, (m, vals) in {3: (4096, 8), 4: (4097, 8), 5: (4096, None)}.items():
+        sc[0, 0, r] *= 0.01  # below 0.5: outside the [2, 8) bin of the first digit
+        pos = torch.randperm(n, generator=g)[:m]
+        if vals is None:
+            sc[0, 0, r, pos] = 3.0 + torch.randperm(m, generator=g).double() * 2.0 ** -30
+        else:
+            sc[0, 0, r, pos] = 3.0 + torch.randint(0, vals, (m,), generator=g).double() * 2.0 ** -40
+    sc[0, 0, 6] = -1.0 - sc[0, 0, 6].abs()
+    nv = torch.tensor([3000, 4096, 4097, n, n, n, n], dtype=torch.int32)
+    N.device_status(dev)
+    for _ in range(2):
+        ids, counts, _ = _topk(sc.to(dev), k=k, width=k, group=1, order=order, pos_offset=0,
+                               pos_unit=0, force_own=False, n_valid=nv.to(dev))
+        assert N.device_status(dev) == 0
+        ri, _ = oracle.topk_rows(sc[0, 0].numpy(), k, n_valid=nv.numpy())
+        want = ri if order == 0 else np.sort(ri, axis=-1)
         assert np.array_equal(ids[0, 0].cpu().numpy(), want)
         assert np.array_equal(counts[0, 0].cpu().numpy(), np.minimum(nv.numpy(), k))
 
