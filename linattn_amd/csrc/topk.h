@@ -46,26 +46,38 @@ struct TkRow {
   bool force;
 };
 
+// Quotient of a non-negative a by a positive b; with S32 (the caller has
+// checked that both fit in 32 bits) in 32-bit arithmetic, a few instructions
+// instead of the long 64-bit division sequence.
+template <bool S32>
+__device__ __forceinline__ int64_t tk_div(int64_t a, int64_t b) {
+  return S32 ? (int64_t)((uint32_t)a / (uint32_t)b) : a / b;
+}
+
+// S32: every quotient taken here has a dividend and divisor below 2^32
+// (tk_row_fits_32).
+template <bool S32 = false>
 __device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
   TkRow r;
   // Segmented mode: group gi handles segment gi % nseg of row gi / nseg.
-  r.br = p.seg_len > 0 ? gi / p.nseg : gi;
-  const int64_t seg = p.seg_len > 0 ? gi % p.nseg : 0;
+  r.br = p.seg_len > 0 ? tk_div<S32>(gi, p.nseg) : gi;
+  const int64_t seg = p.seg_len > 0 ? gi - r.br * p.nseg : 0;
   r.seg0 = seg * p.seg_len;
-  r.tl = r.br % p.Tq;
+  const int64_t bq = tk_div<S32>(r.br, p.Tq);
+  r.tl = r.br - bq * p.Tq;
   r.t = r.tl + p.t_base;
-  r.orow = p.seg_len > 0 ? gi : (r.br / p.Tq) * p.out_tq + r.t;
+  r.orow = p.seg_len > 0 ? gi : bq * p.out_tq + r.t;
   int64_t n_v = p.n;
   int64_t own = -1;
   if (p.pos_unit > 0) {
     const int64_t pos = p.pos_off + r.t;
-    const int64_t u = pos >= 0 ? pos / p.pos_unit : -1;
+    const int64_t u = pos >= 0 ? tk_div<S32>(pos, p.pos_unit) : -1;
     n_v = min(p.n, u + 1);
     own = min(u, p.n - 1);
   }
   if (p.n_valid_tab) n_v = min(p.n, (int64_t)p.n_valid_tab[r.t]);
   if (p.own_tab) own = (int64_t)p.own_tab[r.t];
-  if (p.b_lens && r.t * p.b_len_unit >= (int64_t)p.b_lens[r.br / p.rows_per_b]) {
+  if (p.b_lens && r.t * p.b_len_unit >= (int64_t)p.b_lens[tk_div<S32>(r.br, p.rows_per_b)]) {
     n_v = 0;
     own = -1;
   }
@@ -75,6 +87,14 @@ __device__ __forceinline__ TkRow tk_row(const TopkKParams &p, int64_t gi) {
   r.force = p.force_own && own >= 0 && own < r.n_v;
   r.K = min(p.k, r.n_v);
   return r;
+}
+
+// Whether tk_row<true> is exact for every group of p: the dividends (group
+// and row numbers, positions pos_off + t) and the divisors below 2^32.
+inline bool tk_row_fits_32(const TopkKParams &p) {
+  const int64_t lim = (int64_t)1 << 32;
+  return p.NG < lim && p.nseg < lim && p.Tq < lim && p.pos_unit < lim && p.rows_per_b < lim &&
+         p.pos_off + p.t_base + p.Tq < lim;
 }
 
 // Long plain rows split over several workgroups per row (topk_radix.hip): C

@@ -51,6 +51,7 @@
 // The selection equals tk_select's over the whole row: the K largest keys,
 // threshold ties taken lowest index first.
 #include <algorithm>
+#include <cstddef>
 
 #include "topk.h"
 #include "topk_select.h"
@@ -78,8 +79,12 @@ constexpr int RX_FAST_PASSES = 3;
 // the remaining passes cost no launches.  (About 450 keys of a C5 row match
 // after the first two digits.)
 constexpr int RX_CAND_CAP = 4096;
-constexpr int RX_CPT = RX_CAND_CAP / TK_NT;  // candidates per thread
-constexpr int RX_CPRE = 4;  // of them read before the row state in the last launch
+constexpr int RX_CPT = RX_CAND_CAP / TK_NT;  // candidates per thread (workgroup settle)
+// Up to RX_WCAP candidates (the common case) every wave settles alone, with
+// 8-bit digits and a 256-bin histogram of its own: no workgroup barrier.
+constexpr int RX_WCAP = 1024;
+constexpr int RX_WCPL = RX_WCAP / 64;  // candidates per lane (wave settle)
+constexpr int RX_CPRE = 8;             // of them read before the row state in the last launch
 // digit histograms in the workspace per row, one per chunk-parallel pass (the
 // finishing workgroup keeps its own in LDS)
 constexpr int RX_HISTS = RX_FAST_PASSES;
@@ -120,6 +125,7 @@ struct RxKP {
   int32_t *cand_id;
   int64_t C;
   int32_t state_in_kernel;  // launch 0 starts from the initial state (no set-up launch)
+  int32_t row32;            // tk_row's quotients fit 32-bit arithmetic
 };
 
 __device__ __forceinline__ uint32_t *rx_hist(const RxKP &a, int64_t gi, uint32_t pass) {
@@ -156,7 +162,7 @@ __device__ __forceinline__ RxState rx_initial(const TkRow &rw, bool hist0_extern
 // workgroup per row.
 __global__ __launch_bounds__(TK_NT) void rx_setup_kernel(RxKP a, int hist0_external) {
   const int64_t gi = blockIdx.x;
-  const TkRow rw = tk_row(a.p, gi);
+  const TkRow rw = a.row32 ? tk_row<true>(a.p, gi) : tk_row<false>(a.p, gi);
   uint4 *h = (uint4 *)(a.rows + gi * a.row_words);
   for (int64_t i = threadIdx.x; i < a.row_words / 4; i += TK_NT) h[i] = make_uint4(0, 0, 0, 0);
   if (threadIdx.x == 0) a.state[gi] = rx_initial(rw, hist0_external != 0);
@@ -172,10 +178,16 @@ __global__ __launch_bounds__(TK_NT) void rx_setup_kernel(RxKP a, int hist0_exter
 // `guess`: the pass whose histogram this launch picks from in the common case
 // (-1: none); it is read before the row state, together with the chunk's
 // scores, so that the launch waits for one memory round trip instead of three.
-// The last launch reads the first RX_CPRE * TK_NT candidate slots that way
+// The last launch reads the first RX_CPRE * 64 candidate slots that way
 // instead (rows collected by the launch before it, the common case).
-__global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int last, int guess) {
+// R32: the row arithmetic in 32 bits (RxKP::row32).  LAST: the last launch
+// of the sequence.  Every prefetch load is issued unconditionally (clamped
+// addresses), so that the compiler can wait for the early ones alone.
+template <bool R32, bool LAST>
+__global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int guess) {
+  constexpr bool last = LAST;
   __shared__ uint32_t hist[RX_BINS];
+  __shared__ __align__(16) uint32_t whist[TK_NW][256];  // per wave (wave settle)
   __shared__ uint32_t eqc[RX_KPT][TK_NW];  // per slot and wave: threshold keys
   __shared__ uint32_t tkc[RX_KPT][TK_NW];  // per slot and wave: keys taken
   __shared__ uint32_t wtmp[2][TK_NW];
@@ -183,47 +195,70 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const TopkKParams &p = a.p;
   const int64_t c = blockIdx.x, gi = blockIdx.y, NG = p.NG;
-  const TkRow rw = tk_row(p, gi);
+  // the row state, read first and whole (48 bytes in three 16-byte words, so
+  // that the loads are issued together and their round trip overlaps the
+  // row's index arithmetic); the row's chunk-0 workgroup writes the next
+  // launch's copy
+  const RxState *sin = a.state + (launch & 1) * NG + gi;
+  RxState *sout = a.state + ((launch + 1) & 1) * NG + gi;
+  const bool init = a.state_in_kernel && launch == 0;
+  // (read in the first launch too, where the initial state replaces it:
+  // no branch keeps the loads apart from their use)
+  uint4 sv[3];
+  {
+    const uint4 *sp = (const uint4 *)sin;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) sv[i] = sp[i];
+  }
+  static_assert(offsetof(RxState, prefix) == 0 && offsetof(RxState, mask) == 8 &&
+                    offsetof(RxState, need) == 16 && offsetof(RxState, pass) == 20 &&
+                    offsetof(RxState, pend) == 24 && offsetof(RxState, phase) == 28 &&
+                    offsetof(RxState, top) == 32 && offsetof(RxState, ncand) == 36,
+                "RxState words");
+  const TkRow rw = tk_row<R32>(p, gi);
   const int64_t n_v = rw.n_v;
   // thread t holds bins RX_BINS - 1 - RX_BPT t downwards of a histogram
   auto read_bins = [&](const uint32_t *h, uint32_t (&hv)[RX_BPT]) {
 #pragma unroll
     for (int e = 0; e < RX_BPT; ++e) hv[e] = h[RX_BINS - 1 - RX_BPT * tid - e];
   };
-  // the prefetch: the likely histogram first, then the chunk's scores (loads
-  // complete in order, so the pick below waits for the histogram only)
+  // the state as scalars (a copy of the whole struct would live in memory)
+  const bool writer = c == 0 && tid == 0;
+  const RxState s0 = init ? rx_initial(rw, true) : RxState{};
+  uint32_t phase = init ? s0.phase : sv[1].w;
+  uint64_t prefix = init ? s0.prefix : ((uint64_t)sv[0].y << 32 | sv[0].x);
+  uint64_t mask = init ? s0.mask : ((uint64_t)sv[0].w << 32 | sv[0].z);
+  uint32_t need = init ? s0.need : sv[1].x, pass = init ? s0.pass : sv[1].y;
+  uint32_t pend = init ? s0.pend : sv[1].z;
+  int top = init ? s0.top : (int)sv[2].x;
+  const uint32_t ncand = init ? 0u : sv[2].y;
+  // the prefetch: the likely histogram, then the candidates, then the
+  // chunk's scores (the pick waits for the histogram only, the settle for
+  // the candidates)
   uint32_t hpre[RX_BPT];
-  if (guess >= 0) read_bins(rx_hist(a, gi, (uint32_t)guess), hpre);
+  if (!LAST) read_bins(rx_hist(a, gi, (uint32_t)max(guess, 0)), hpre);
   uint64_t cpre[RX_CPRE];
-  if (last) {
+  if (LAST) {
     const uint64_t *cd = rx_cand(a, gi);
 #pragma unroll
-    for (int e = 0; e < RX_CPRE; ++e) cpre[e] = cd[tid + e * TK_NT];
+    for (int e = 0; e < RX_CPRE; ++e) cpre[e] = cd[lane + e * 64];  // (every wave: the same)
   }
+  __builtin_amdgcn_sched_barrier(0);  // (issued before the scores)
   double vraw[RX_KPT];
   {
+    // (keys past the valid prefix read key 0 of the row, then count as invalid)
     const int64_t x0 = c * RX_CHUNK + tid;
     const double *rp = p.scores + rw.br * p.row_stride;
 #pragma unroll
-    for (int j = 0; j < RX_KPT; ++j) vraw[j] = x0 + (int64_t)j * TK_NT < n_v ? rp[x0 + (int64_t)j * TK_NT] : 0.0;
+    for (int j = 0; j < RX_KPT; ++j) {
+      const int64_t i = x0 + (int64_t)j * TK_NT;
+      vraw[j] = rp[i < n_v ? i : 0];
+    }
   }
-  // the row state as scalars (a copy of the whole struct would live in
-  // memory); the row's chunk-0 workgroup writes the next launch's copy
-  const RxState *sin = a.state + (launch & 1) * NG + gi;
-  RxState *sout = a.state + ((launch + 1) & 1) * NG + gi;
-  const bool writer = c == 0 && tid == 0;
-  const bool init = a.state_in_kernel && launch == 0;
-  const RxState s0 = init ? rx_initial(rw, true) : RxState{};
-  uint32_t phase = init ? s0.phase : sin->phase;
   if (phase == RX_DONE) {
     if (writer) sout->phase = RX_DONE;
     return;
   }
-  uint64_t prefix = init ? s0.prefix : sin->prefix, mask = init ? s0.mask : sin->mask;
-  uint32_t need = init ? s0.need : sin->need, pass = init ? s0.pass : sin->pass;
-  uint32_t pend = init ? s0.pend : sin->pend;
-  int top = init ? s0.top : sin->top;
-  const uint32_t ncand = init ? 0u : sin->ncand;
   auto publish = [&](uint32_t next_phase, uint32_t next_pend, uint32_t next_ncand) {
     sout->prefix = prefix;
     sout->mask = mask;
@@ -271,7 +306,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     uint32_t csum = 0, all;
 #pragma unroll
     for (int e = 0; e < RX_BPT; ++e) csum += hv[e];
-    const uint32_t incl = tk_block_incl_scan(csum, wtmp[0], all);
+    const uint32_t incl = tk_block_incl_scan<TK_NT, true>(csum, wtmp[0], all);
     if (incl >= need && incl - csum < need) {
       uint32_t acc = incl - csum;
       bool found = false;
@@ -286,7 +321,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
         acc += hv[e];
       }
     }
-    __syncthreads();
+    lds_barrier();
     need -= s_above;
     nmatch = s_cnt;
     prefix |= (uint64_t)s_bin << shift;
@@ -295,7 +330,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     pass += 1;
     // the whole bin is taken, or every bit is fixed (the rest are index ties)
     phase = (s_cnt == need || shift == 0) ? RX_COUNT : RX_PASS;
-    __syncthreads();  // s_* are read before they are written again
+    lds_barrier();  // s_* are read before they are written again
   };
   auto pick = [&](const uint32_t *h) {
     uint32_t hv[RX_BPT];
@@ -311,56 +346,94 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     for (int j = 0; j < RX_KPT; ++j)
       if (valid(x, j) && (u[j] & mask) == prefix) atomicAdd(&hist[(uint32_t)(u[j] >> shift) & dm], 1u);
   };
-  // the chunk's keys above / equal to the final threshold (workgroup totals)
+  // the chunk's keys above / equal to the final threshold (workgroup totals:
+  // one reduction of both counts, each below 2^16, packed in a word)
   auto count_chunk = [&](int64_t x, const uint64_t (&u)[RX_KPT], uint32_t &gt_c, uint32_t &eq_c) {
-    uint32_t gt = 0, eq = 0;
+    uint32_t v = 0;
 #pragma unroll
     for (int j = 0; j < RX_KPT; ++j) {
       const uint64_t um = u[j] & mask;
-      gt += valid(x, j) && um > prefix;
-      eq += valid(x, j) && um == prefix;
+      v += valid(x, j) ? (um > prefix ? 0x10000u : um == prefix ? 1u : 0u) : 0u;
     }
-    tk_block_incl_scan(gt, wtmp[0], gt_c);
-    tk_block_incl_scan(eq, wtmp[1], eq_c);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
+    if (lane == 0) wtmp[0][w] = v;
+    lds_barrier();
+    uint32_t t = 0;
+#pragma unroll
+    for (int y = 0; y < TK_NW; ++y) t += wtmp[0][y];
+    lds_barrier();  // wtmp is read before it is written again
+    gt_c = t >> 16;
+    eq_c = t & 0xffffu;
+  };
+  // the exclusive prefix of per-(slot, wave) counts cnt[j][y] in key order
+  // (slot-major): lane l of every wave reads entry l (RX_KPT x TK_NW = 64)
+  // after the barrier, the wave scans them, and entry (j, w) is then read
+  // from lane 4 j + w
+  static_assert(RX_KPT * TK_NW == 64, "one count per lane");
+  const int wu = __builtin_amdgcn_readfirstlane(w);  // (w as a uniform value)
+  // stores the wave's per-slot counts (uniform) into cnt[j][w]: lane j writes
+  // slot j's
+  auto put_counts = [&](uint32_t (&cnt)[RX_KPT][TK_NW], const uint32_t (&v)[RX_KPT]) {
+    uint32_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < RX_KPT; ++j) mine = lane == j ? v[j] : mine;
+    if (lane < RX_KPT) cnt[lane][w] = mine;
+  };
+  auto slot_scan = [&](const uint32_t (&cnt)[RX_KPT][TK_NW]) {
+    const uint32_t v = (&cnt[0][0])[lane];
+    uint32_t incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = (uint32_t)__shfl_up((int)incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    return incl - v;
   };
   // writes chunk x's selected keys from output position base on, taking its
-  // first take_eq threshold keys (index order within the chunk)
-  auto write_chunk = [&](int64_t x, const uint64_t (&u)[RX_KPT], uint32_t base, uint32_t take_eq) {
+  // first take_eq of its eq_c threshold keys (index order within the chunk);
+  // more: another chunk follows (the LDS counts are reused)
+  auto write_chunk = [&](int64_t x, const uint64_t (&u)[RX_KPT], uint32_t base, uint32_t take_eq,
+                         uint32_t eq_c, bool more) {
     const int64_t x0 = x * RX_CHUNK + tid;
+    uint32_t take_bits = 0;
+    if (take_eq == 0 || take_eq >= eq_c) {  // all or none of the threshold keys
 #pragma unroll
-    for (int j = 0; j < RX_KPT; ++j) {
-      const uint64_t b = __ballot(valid(x, j) && (u[j] & mask) == prefix);
-      if (lane == 0) eqc[j][w] = (uint32_t)__popcll(b);
+      for (int j = 0; j < RX_KPT; ++j) {
+        const uint64_t um = u[j] & mask;
+        const bool take = valid(x, j) && (um > prefix || (um == prefix && take_eq != 0));
+        take_bits |= (uint32_t)take << j;
+      }
+    } else {  // the first take_eq threshold keys in index order
+      uint32_t ce[RX_KPT];
+#pragma unroll
+      for (int j = 0; j < RX_KPT; ++j) ce[j] = (uint32_t)__popcll(__ballot(valid(x, j) && (u[j] & mask) == prefix));
+      put_counts(eqc, ce);
+      lds_barrier();
+      const uint32_t ex = slot_scan(eqc);
+#pragma unroll
+      for (int j = 0; j < RX_KPT; ++j) {
+        const uint64_t um = u[j] & mask;
+        const bool is_eq = valid(x, j) && um == prefix;
+        const uint64_t b = __ballot(is_eq);
+        const uint32_t rank =
+            (uint32_t)__builtin_amdgcn_readlane((int)ex, j * TK_NW + wu) + (uint32_t)__popcll(b & lt);
+        const bool take = (valid(x, j) && um > prefix) || (is_eq && rank < take_eq);
+        take_bits |= (uint32_t)take << j;
+      }
     }
-    __syncthreads();
-    uint32_t take_bits = 0, eq_run = 0;
+    uint32_t ct[RX_KPT];
 #pragma unroll
-    for (int j = 0; j < RX_KPT; ++j) {
-      const uint64_t um = u[j] & mask;
-      const bool is_gt = valid(x, j) && um > prefix;
-      const bool is_eq = valid(x, j) && um == prefix;
-      const uint64_t b = __ballot(is_eq);
-      uint32_t rank = eq_run + (uint32_t)__popcll(b & lt);
-#pragma unroll
-      for (int y = 0; y < TK_NW; ++y) rank += y < w ? eqc[j][y] : 0u;
-#pragma unroll
-      for (int y = 0; y < TK_NW; ++y) eq_run += eqc[j][y];
-      const bool take = is_gt || (is_eq && rank < take_eq);
-      const uint64_t tb = __ballot(take);
-      if (lane == 0) tkc[j][w] = (uint32_t)__popcll(tb);
-      take_bits |= (uint32_t)take << j;
-    }
-    __syncthreads();
-    uint32_t pos_run = base;
+    for (int j = 0; j < RX_KPT; ++j) ct[j] = (uint32_t)__popcll(__ballot((take_bits >> j) & 1u));
+    put_counts(tkc, ct);
+    lds_barrier();
+    const uint32_t ex = slot_scan(tkc);
 #pragma unroll
     for (int j = 0; j < RX_KPT; ++j) {
       const bool take = (take_bits >> j) & 1u;
       const uint64_t tb = __ballot(take);
-      uint32_t pos = pos_run + (uint32_t)__popcll(tb & lt);
-#pragma unroll
-      for (int y = 0; y < TK_NW; ++y) pos += y < w ? tkc[j][y] : 0u;
-#pragma unroll
-      for (int y = 0; y < TK_NW; ++y) pos_run += tkc[j][y];
+      const uint32_t pos =
+          base + (uint32_t)__builtin_amdgcn_readlane((int)ex, j * TK_NW + wu) + (uint32_t)__popcll(tb & lt);
       if (take) {
         const int64_t i = x0 + (int64_t)j * TK_NT;
         if (ord1) {
@@ -371,7 +444,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
         }
       }
     }
-    __syncthreads();  // eqc / tkc are read before the next chunk writes them
+    if (more) lds_barrier();  // eqc / tkc are read before the next chunk writes them
   };
   // padding after the K winners (positions first + stride * m), and the count
   auto pad = [&](int64_t first, int64_t stride) {
@@ -402,12 +475,12 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     uint64_t u[RX_KPT];
     while (phase == RX_PASS) {
       for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
-      __syncthreads();
+      lds_barrier();
       for (int64_t x = 0; x < a.C; ++x) {
         load(x, u);
         hist_chunk(x, u);
       }
-      __syncthreads();
+      lds_barrier();
       pick(hist);
     }
     // count and write together, chunk after chunk in index order: chunk x
@@ -420,7 +493,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
       count_chunk(x, u, gt_c, eq_c);
       const uint32_t base = gt_before + min(need, eq_before);
       const uint32_t take_eq = eq_before >= need ? 0u : min(need - eq_before, eq_c);
-      write_chunk(x, u, base, take_eq);
+      write_chunk(x, u, base, take_eq, eq_c, true);
       gt_before += gt_c;
       eq_before += eq_c;
     }
@@ -440,10 +513,10 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     uint32_t mine = 0, tot;
 #pragma unroll
     for (int j = 0; j < RX_KPT; ++j) mine += valid(c, j) && (u[j] & mask) == prefix;
-    const uint32_t incl = tk_block_incl_scan(mine, wtmp[0], tot);
+    const uint32_t incl = tk_block_incl_scan<TK_NT, true>(mine, wtmp[0], tot);
     if (tid == 0 && tot)
       s_base = __hip_atomic_fetch_add(rx_ccount(a, gi), tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
+    lds_barrier();
     if (tot) {
       uint64_t *cd = rx_cand(a, gi);
       uint32_t pos = s_base + incl - mine;
@@ -465,33 +538,99 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     // write below
     const uint32_t nc = min(ncand, (uint32_t)RX_CAND_CAP);
     const uint64_t *cd = rx_cand(a, gi);
-    uint64_t ck[RX_CPT];
-#pragma unroll
-    for (int e = 0; e < RX_CPT; ++e) {
-      const uint32_t i = (uint32_t)(tid + e * TK_NT);
-      ck[e] = e < RX_CPRE && last ? cpre[e] : i < nc ? cd[i] : 0ull;
-    }
     phase = RX_PASS;
-    while (phase == RX_PASS) {
-      for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
-      __syncthreads();
-      int shift;
-      uint32_t dm;
-      digit(shift, dm);
+    // every wave alone: lane l holds candidates l + 64 e (ck: an array of
+    // uint64_t, e below its length); 8-bit digits, bins counted in the wave's
+    // own LDS histogram (a wave's LDS operations complete in order), picked
+    // with a wave scan
+    auto wave_settle = [&](const auto &ck) {
+      constexpr int NPL = (int)(sizeof(ck) / sizeof(ck[0]));
+      uint32_t *wh = whist[w];
+      while (phase == RX_PASS) {
+        const int shift = top >= 7 ? top - 7 : 0;
+        const uint32_t dm = (2u << (top - shift)) - 1u;
+        *(uint4 *)&wh[4 * lane] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-      for (int e = 0; e < RX_CPT; ++e)
-        if ((uint32_t)(tid + e * TK_NT) < nc && (ck[e] & mask) == prefix)
-          atomicAdd(&hist[(uint32_t)(ck[e] >> shift) & dm], 1u);
-      __syncthreads();
-      pick(hist);
+        for (int e = 0; e < NPL; ++e)
+          if ((uint32_t)(lane + 64 * e) < nc && (ck[e] & mask) == prefix)
+            atomicAdd(&wh[(uint32_t)(ck[e] >> shift) & dm], 1u);
+        // lane l: bins 255 - 4 l downwards (.w the highest of its four)
+        const uint4 hv = *(const uint4 *)&wh[252 - 4 * lane];
+        const uint32_t cs = hv.x + hv.y + hv.z + hv.w;
+        uint32_t incl = cs;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t y = (uint32_t)__shfl_up((int)incl, off, 64);
+          if (lane >= off) incl += y;
+        }
+        const uint64_t hit = __ballot(incl >= need && incl - cs < need);
+        if (hit == 0) {  // (cannot happen: need <= the keys matching the prefix)
+          phase = RX_COUNT;
+          break;
+        }
+        const int L = __builtin_ctzll(hit);
+        uint32_t acc = (uint32_t)__builtin_amdgcn_readlane((int)(incl - cs), L);
+        const uint32_t h3 = (uint32_t)__builtin_amdgcn_readlane((int)hv.w, L);
+        const uint32_t h2 = (uint32_t)__builtin_amdgcn_readlane((int)hv.z, L);
+        const uint32_t h1 = (uint32_t)__builtin_amdgcn_readlane((int)hv.y, L);
+        const uint32_t h0 = (uint32_t)__builtin_amdgcn_readlane((int)hv.x, L);
+        uint32_t bin, cnt;
+        if (acc + h3 >= need) {
+          bin = 255 - 4 * L, cnt = h3;
+        } else if (acc += h3, acc + h2 >= need) {
+          bin = 254 - 4 * L, cnt = h2;
+        } else if (acc += h2, acc + h1 >= need) {
+          bin = 253 - 4 * L, cnt = h1;
+        } else {
+          acc += h1;
+          bin = 252 - 4 * L, cnt = h0;
+        }
+        need -= acc;
+        prefix |= (uint64_t)bin << shift;
+        mask |= (uint64_t)dm << shift;
+        top = shift - 1;
+        phase = (cnt == need || shift == 0) ? RX_COUNT : RX_PASS;
+      }
+    };
+    if (LAST && nc <= (uint32_t)(RX_CPRE * 64)) {
+      wave_settle(cpre);  // the prefetched slots hold them all
+    } else if (nc <= (uint32_t)RX_WCAP) {
+      uint64_t ck[RX_WCPL];
+#pragma unroll
+      for (int e = 0; e < RX_WCPL; ++e) {
+        const uint32_t i = (uint32_t)(lane + 64 * e);
+        ck[e] = i < nc ? cd[i] : 0ull;
+      }
+      wave_settle(ck);
+    } else {
+      // the whole workgroup: thread t holds candidates t + 256 e
+      uint64_t ck[RX_CPT];
+#pragma unroll
+      for (int e = 0; e < RX_CPT; ++e) {
+        const uint32_t i = (uint32_t)(tid + e * TK_NT);
+        ck[e] = i < nc ? cd[i] : 0ull;
+      }
+      while (phase == RX_PASS) {
+        for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
+        lds_barrier();
+        int shift;
+        uint32_t dm;
+        digit(shift, dm);
+#pragma unroll
+        for (int e = 0; e < RX_CPT; ++e)
+          if ((uint32_t)(tid + e * TK_NT) < nc && (ck[e] & mask) == prefix)
+            atomicAdd(&hist[(uint32_t)(ck[e] >> shift) & dm], 1u);
+        lds_barrier();
+        pick(hist);
+      }
     }
   }
 
   if (phase == RX_PASS) {
     for (int b = tid; b < RX_BINS; b += TK_NT) hist[b] = 0u;
-    __syncthreads();
+    lds_barrier();
     hist_chunk(c, u);
-    __syncthreads();
+    lds_barrier();
     uint32_t *gh = rx_hist(a, gi, pass);
     for (int b = tid; b < RX_BINS; b += TK_NT) {
       const uint32_t x = hist[b];
@@ -559,9 +698,9 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (s_base == 0xffffffffu) return;  // the wait was given up: this chunk writes nothing
-  write_chunk(c, u, s_base, s_take);
+  write_chunk(c, u, s_base, s_take, eq_c, false);
   pad(c * TK_NT + tid, a.C * TK_NT);
   if (writer) sout->phase = RX_DONE;
 }
@@ -593,6 +732,7 @@ static RxKP rx_args(const TopkKParams &p, const RadixPlan &R, void *ws) {
   base += align256(2 * p.NG * (int64_t)sizeof(RxState));
   a.rows = (uint32_t *)base;
   a.row_words = rx_row_words(R.C);
+  a.row32 = tk_row_fits_32(p) ? 1 : 0;
   base += align256(p.NG * a.row_words * 4);
   base += align256(p.NG * 8);  // the rows' ready words (RadixRowPrep)
   if (p.order == 0) {
@@ -636,8 +776,16 @@ int topk_radix_finish(const TopkKParams &p, const RadixPlan &R, void *ws, bool h
   for (int s = 0; s < launches; ++s) {
     // launch s picks pass s (pass 0 histogrammed by the scores' kernel) or
     // s - 1; the last one mostly settles collected rows (no histogram read)
-    const int guess = s == launches - 1 ? -1 : s - (hist0_external ? 0 : 1);
-    rx_stage_kernel<<<grid, TK_NT, 0, st>>>(a, s, s == launches - 1 ? 1 : 0, guess);
+    const bool lst = s == launches - 1;
+    const int guess = lst ? -1 : s - (hist0_external ? 0 : 1);
+    if (a.row32 && lst)
+      rx_stage_kernel<true, true><<<grid, TK_NT, 0, st>>>(a, s, guess);
+    else if (a.row32)
+      rx_stage_kernel<true, false><<<grid, TK_NT, 0, st>>>(a, s, guess);
+    else if (lst)
+      rx_stage_kernel<false, true><<<grid, TK_NT, 0, st>>>(a, s, guess);
+    else
+      rx_stage_kernel<false, false><<<grid, TK_NT, 0, st>>>(a, s, guess);
     LA_LAUNCHED();
   }
   if (p.order == 0) {

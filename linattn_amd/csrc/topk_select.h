@@ -16,8 +16,9 @@ __device__ __forceinline__ uint64_t lanemask_lt(int lane) {
 }
 
 // Inclusive scan of one value per thread across a workgroup of NT threads
-// (wtmp holds NT / 64 words).
-template <int NT = TK_NT>
+// (wtmp holds NT / 64 words).  LDS_ONLY: its barriers order LDS alone (global
+// loads and stores in flight stay in flight).
+template <int NT = TK_NT, bool LDS_ONLY = false>
 __device__ __forceinline__ uint32_t tk_block_incl_scan(uint32_t v, uint32_t *wtmp, uint32_t &total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
@@ -26,7 +27,10 @@ __device__ __forceinline__ uint32_t tk_block_incl_scan(uint32_t v, uint32_t *wtm
     if (lane >= off) v += y;
   }
   if (lane == 63) wtmp[w] = v;
-  __syncthreads();
+  if (LDS_ONLY)
+    lds_barrier();
+  else
+    __syncthreads();
   uint32_t base = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < NT / 64; ++i) {
@@ -34,7 +38,10 @@ __device__ __forceinline__ uint32_t tk_block_incl_scan(uint32_t v, uint32_t *wtm
     base += (i < w) ? x : 0u;
     tot += x;
   }
-  __syncthreads();
+  if (LDS_ONLY)
+    lds_barrier();
+  else
+    __syncthreads();
   total = tot;
   return v + base;
 }

@@ -96,16 +96,18 @@ def test_topk_radix_long_rows_every_depth(dev, order):
 def test_topk_radix_candidates(dev, order):
     """Long rows whose keys matching the threshold prefix are few enough to
     collect (at most 4096): every workgroup of the row then settles the
-    remaining digits from the collected keys alone.  Valid prefixes of 3000
-    and 4096 keys (collected before any pass), 4097 (one pass first); 4096
-    keys in one first-digit bin above small noise, over 8 values (the
-    settle runs down to the last bit, then index ties), and 4097 such keys
-    (too many: the chunk-parallel passes and the one-workgroup finish); 4096
-    distinct keys in that bin; a row of negative keys."""
+    remaining digits from the collected keys alone (each wave on its own up
+    to 1024 keys, the whole workgroup above).  Valid prefixes of 3000 and
+    4096 keys (collected before any pass), 4097 (one pass first), 1024 and
+    1025; 4096 keys in one first-digit bin above small noise, over 8 values
+    (the settle runs down to the last bit, then index ties), 4097 such keys
+    (too many: the chunk-parallel passes and the one-workgroup finish) and
+    1020 (the wave settle, ties); 4096 distinct keys in that bin; a row of
+    negative keys."""
     n, k = 200000, 1000
     g = torch.Generator().manual_seed(17)
-    sc = torch.randn(1, 1, 7, n, generator=g, dtype=torch.float64)
-    for r, (m, vals) in {3: (4096, 8), 4: (4097, 8), 5: (4096, None)}.items():
+    sc = torch.randn(1, 1, 10, n, generator=g, dtype=torch.float64)
+    for r, (m, vals) in {3: (4096, 8), 4: (4097, 8), 5: (4096, None), 9: (1020, 8)}.items():
         sc[0, 0, r] *= 0.01  # below 0.5: outside the [2, 8) bin of the first digit
         pos = torch.randperm(n, generator=g)[:m]
         if vals is None:
@@ -113,7 +115,7 @@ def test_topk_radix_candidates(dev, order):
         else:
             sc[0, 0, r, pos] = 3.0 + torch.randint(0, vals, (m,), generator=g).double() * 2.0 ** -40
     sc[0, 0, 6] = -1.0 - sc[0, 0, 6].abs()
-    nv = torch.tensor([3000, 4096, 4097, n, n, n, n], dtype=torch.int32)
+    nv = torch.tensor([3000, 4096, 4097, n, n, n, n, 1024, 1025, n], dtype=torch.int32)
     N.device_status(dev)
     for _ in range(2):
         ids, counts, _ = _topk(sc.to(dev), k=k, width=k, group=1, order=order, pos_offset=0,
