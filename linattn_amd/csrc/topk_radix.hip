@@ -428,19 +428,28 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     put_counts(tkc, ct);
     lds_barrier();
     const uint32_t ex = slot_scan(tkc);
+    // position of slot j's key among the chunk's taken keys, from base on
+    auto slot_pos = [&](int j) {
+      const uint64_t tb = __ballot((take_bits >> j) & 1u);
+      return base + (uint32_t)__builtin_amdgcn_readlane((int)ex, j * TK_NW + wu) + (uint32_t)__popcll(tb & lt);
+    };
+    const int32_t i0 = (int32_t)x0;  // (a row holds < 2^31 keys)
+    if (ord1) {
+      const uint32_t wmax = (uint32_t)min(p.width, (int64_t)0xffffffff);
 #pragma unroll
-    for (int j = 0; j < RX_KPT; ++j) {
-      const bool take = (take_bits >> j) & 1u;
-      const uint64_t tb = __ballot(take);
-      const uint32_t pos =
-          base + (uint32_t)__builtin_amdgcn_readlane((int)ex, j * TK_NW + wu) + (uint32_t)__popcll(tb & lt);
-      if (take) {
-        const int64_t i = x0 + (int64_t)j * TK_NT;
-        if (ord1) {
-          if ((int64_t)pos < p.width) oi[pos] = (int32_t)i;
-        } else if (pos < K) {
-          a.cand_sc[gi * p.k + pos] = key_to_double(u[j]);
-          a.cand_id[gi * p.k + pos] = (int32_t)i;
+      for (int j = 0; j < RX_KPT; ++j) {
+        const uint32_t pos = slot_pos(j);
+        if (((take_bits >> j) & 1u) && pos < wmax) oi[pos] = i0 + j * TK_NT;
+      }
+    } else {
+      double *csc = a.cand_sc + gi * p.k;
+      int32_t *cid = a.cand_id + gi * p.k;
+#pragma unroll
+      for (int j = 0; j < RX_KPT; ++j) {
+        const uint32_t pos = slot_pos(j);
+        if (((take_bits >> j) & 1u) && pos < K) {
+          csc[pos] = key_to_double(u[j]);
+          cid[pos] = i0 + j * TK_NT;
         }
       }
     }
