@@ -47,9 +47,10 @@ enum {
 
 /* device status bits (la_device_status) */
 enum {
-  LA_DEV_TOPK_TIMEOUT = 1,  /* the multi-workgroup top-k's last workgroup of a stage waited
-                               past its bound for atomics already issued (a hardware fault
-                               guard: that wait depends on no other workgroup running) */
+  LA_DEV_TOPK_TIMEOUT = 1,  /* a wait of the multi-workgroup top-k (a chunk's look-back over
+                               the row's earlier chunks) or of the decode indexer (for the
+                               row's first workgroup) passed its bound (a hardware fault
+                               guard: each waits only for workgroups dispatched before it) */
   LA_DEV_PREFILL_RANGE = 2  /* la_block_sparse_prefill met a finite |v| >= 2^22 (outputs inf;
                               the Python wrapper raises ValueError) */
 };
@@ -65,7 +66,7 @@ int la_abi_version(void);
  * Kernels report failures they detect on the device here instead of through a
  * return code (a launch returns before the kernel runs): a long row of
  * la_topk_rows / la_indexer_topk whose multi-workgroup selection hit that
- * guard comes back with -1 ids (and count -1 in index order), and
+ * guard comes back incomplete (the chunk that gave up writes no ids), and
  * LA_DEV_TOPK_TIMEOUT is raised.
  * No counterpart in the reference (its kernels report nothing).  Synchronous.
  */
