@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 12
+#define LA_ABI_VERSION 13
 
 /* element types */
 enum {
@@ -71,6 +71,14 @@ int la_abi_version(void);
  * No counterpart in the reference (its kernels report nothing).  Synchronous.
  */
 int la_device_status(uint32_t *bits, int32_t clear, void *stream);
+
+/*
+ * Testing hook, no counterpart in the reference: the number of polls after
+ * which the library's bounded waits on other workgroups (LA_DEV_TOPK_TIMEOUT)
+ * give up, process-wide; 2^20 by default, 0 gives every such wait up at once
+ * (so a test can drive the timeout path while every kernel still ends).
+ */
+int la_test_set_spin_limit(uint32_t polls);
 
 /* Message describing the last non-zero status returned on this thread. */
 const char *la_last_error(void);

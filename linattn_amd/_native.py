@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblinattn_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 LA_F32, LA_BF16, LA_F16, LA_FP8_E4M3, LA_F64 = 0, 1, 2, 3, 4
 LA_OK, LA_ERR_INVALID, LA_ERR_UNSUPPORTED, LA_ERR_HIP, LA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -46,6 +46,7 @@ EXPORTED = (
     "la_xattn_select_workspace",
     "la_xattn_select",
     "la_device_status",
+    "la_test_set_spin_limit",
 )
 
 LA_DEV_TOPK_TIMEOUT = 1
@@ -216,6 +217,7 @@ def load() -> ctypes.CDLL:
     L.la_xattn_select.argtypes = [P(LaXattnSelectArgs), _vp]
     L.la_xattn_select.restype = ctypes.c_int
     L.la_device_status.argtypes = [ctypes.POINTER(ctypes.c_uint32), _i32, _vp]
+    L.la_test_set_spin_limit.argtypes = [ctypes.c_uint32]
     for name in EXPORTED:
         fn = getattr(L, name)
         if fn.restype is None or fn.restype is ctypes.c_int:

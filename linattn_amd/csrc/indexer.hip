@@ -51,6 +51,7 @@ struct IdxKP {
   // every workgroup waits for that value before adding into the histogram
   uint64_t *rx_ready;
   uint64_t rx_gen;
+  uint32_t spin_limit;  // polls before that wait is given up (0: at once)
 };
 
 // Status bits this file's kernels raise on the current device (read through
@@ -465,13 +466,16 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
     if (tid == 0) {
       uint32_t ok = 1, spins = 0;
       if (prep) {
-        while (__hip_atomic_load(&p.rx_ready[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != p.rx_gen) {
-          if (++spins > (1u << 20)) {
+        for (;;) {
+          if (spins >= p.spin_limit) {
             ok = 0;
             __hip_atomic_fetch_or(&la_ix_status, (uint32_t)LA_DEV_TOPK_TIMEOUT, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT);
             break;
           }
+          if (__hip_atomic_load(&p.rx_ready[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.rx_gen)
+            break;
+          ++spins;
           __builtin_amdgcn_s_sleep(2);
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the zeros before the adds
@@ -786,6 +790,7 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
       p.hist_stride = rp.row_words;
       p.rx_ready = rp.ready;
       p.rx_gen = next_radix_gen();
+      p.spin_limit = rx_spin_limit();
     }
     if (decode16) {
       switch (a->HI) {

@@ -116,6 +116,10 @@ int topk_radix_launch(const TopkKParams &p, const RadixPlan &R, void *ws, hipStr
 // then stores a value unique to the call into ready[gi], before any of its
 // workgroups adds into the row's histogram (each waits for that value
 // first); the first stage launch starts the rows from their initial state.
+// Polls after which the radix select's and the decode indexer's waits on
+// other workgroups give up (2^20 unless la_test_set_spin_limit changed it).
+uint32_t rx_spin_limit();
+
 struct RadixRowPrep {
   uint32_t *rows = nullptr;
   int64_t row_words = 0;

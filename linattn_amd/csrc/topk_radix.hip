@@ -51,6 +51,7 @@
 // The selection equals tk_select's over the whole row: the K largest keys,
 // threshold ties taken lowest index first.
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 
 #include "topk.h"
@@ -66,7 +67,7 @@ enum { RX_PASS = 0, RX_COUNT = 1, RX_CAND = 2, RX_DONE = 3 };
 // own counts, RX_INC the counts of chunks 0..c), keys above the threshold in
 // bits 31-61, keys equal to it in bits 0-30 (a row holds < 2^31 keys).
 constexpr uint64_t RX_AGG = 1ull << 62, RX_INC = 2ull << 62;
-constexpr uint32_t RX_SPIN_LIMIT = 1u << 20;  // polls before a wait is given up
+constexpr uint32_t RX_SPIN_LIMIT = 1u << 20;  // polls before a wait is given up (default)
 // digit passes run chunk-parallel: up to three (28 bits fixed); a row that
 // needs more, and whose keys matching the threshold prefix were not few
 // enough to be collected (RX_CAND_CAP), finishes in one workgroup in the
@@ -99,6 +100,10 @@ __device__ __forceinline__ int rx_digit_bits(uint32_t pass) { return pass == 1 ?
 // Status bits raised by kernels of this library on the current device, read
 // and cleared by la_device_status.
 __device__ uint32_t la_dev_status;
+__device__ __forceinline__ void raise_timeout() {
+  __hip_atomic_fetch_or(&la_dev_status, (uint32_t)LA_DEV_TOPK_TIMEOUT, __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Per-row state between launches.
 struct RxState {
@@ -126,6 +131,7 @@ struct RxKP {
   int64_t C;
   int32_t state_in_kernel;  // launch 0 starts from the initial state (no set-up launch)
   int32_t row32;            // tk_row's quotients fit 32-bit arithmetic
+  uint32_t spin_limit;      // polls before a cross-workgroup wait is given up
 };
 
 __device__ __forceinline__ uint32_t *rx_hist(const RxKP &a, int64_t gi, uint32_t pass) {
@@ -306,6 +312,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     uint32_t csum = 0, all;
 #pragma unroll
     for (int e = 0; e < RX_BPT; ++e) csum += hv[e];
+    if (tid == 0) s_cnt = 0;  // a found bin holds at least one key
     const uint32_t incl = tk_block_incl_scan<TK_NT, true>(csum, wtmp[0], all);
     if (incl >= need && incl - csum < need) {
       uint32_t acc = incl - csum;
@@ -330,6 +337,10 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     pass += 1;
     // the whole bin is taken, or every bit is fixed (the rest are index ties)
     phase = (s_cnt == need || shift == 0) ? RX_COUNT : RX_PASS;
+    if (s_cnt == 0) {  // a histogram short of need keys: counts were left out
+      phase = RX_DONE;
+      if (tid == 0) raise_timeout();
+    }
     lds_barrier();  // s_* are read before they are written again
   };
   auto pick = [&](const uint32_t *h) {
@@ -477,6 +488,11 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     else
       pick(rx_hist(a, gi, pass));
   }
+  // a row whose histogram came out short (a wait given up): nothing more
+  auto give_up = [&]() {
+    if (writer) sout->phase = RX_DONE;
+  };
+  if (phase == RX_DONE) return give_up();
 
   if (phase == RX_PASS && last) {
     // ------------------------------------------- one-workgroup finish --
@@ -492,6 +508,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
       lds_barrier();
       pick(hist);
     }
+    if (phase == RX_DONE) return give_up();
     // count and write together, chunk after chunk in index order: chunk x
     // writes after the keys the chunks before it select and takes the
     // first need - (threshold keys before it) of its own threshold keys
@@ -573,8 +590,9 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
           if (lane >= off) incl += y;
         }
         const uint64_t hit = __ballot(incl >= need && incl - cs < need);
-        if (hit == 0) {  // (cannot happen: need <= the keys matching the prefix)
-          phase = RX_COUNT;
+        if (hit == 0) {  // a candidate list short of need keys: counts were left out
+          phase = RX_DONE;
+          if (lane == 0) raise_timeout();
           break;
         }
         const int L = __builtin_ctzll(hit);
@@ -633,6 +651,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
         pick(hist);
       }
     }
+    if (phase == RX_DONE) return give_up();
   }
 
   if (phase == RX_PASS) {
@@ -663,9 +682,9 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
     // atomics suffice, and no fence writes back or drops the caches)
     if (lane == 0 && c > 0) __hip_atomic_store(&rec[c], RX_AGG | own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t gb = 0, eb = 0, spins = 0;
-    bool ok = true;
+    bool ok = a.spin_limit > 0 || c == 0;  // (a limit of 0 gives every wait up at once)
     int64_t hi = c - 1;  // the window's nearest chunk
-    while (hi >= 0) {
+    while (ok && hi >= 0) {
       const int64_t x = hi - lane;
       uint64_t r = x >= 0 ? __hip_atomic_load(&rec[x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : RX_INC;
       const uint64_t inc = __ballot((r & RX_INC) != 0);
@@ -674,7 +693,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
       // when there is none) must have published
       const uint64_t upto = inc ? (inc & (~inc + 1)) * 2 - 1 : ~0ull;
       if (none & upto) {
-        if (++spins > RX_SPIN_LIMIT) {
+        if (++spins > a.spin_limit) {
           ok = false;
           break;
         }
@@ -701,8 +720,7 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
         s_base = gb + min(need, eb);
         s_take = eb >= need ? 0u : min(need - eb, eq_c);
       } else {
-        __hip_atomic_fetch_or(&la_dev_status, (uint32_t)LA_DEV_TOPK_TIMEOUT, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
+        raise_timeout();
         s_base = 0xffffffffu;
       }
     }
@@ -715,6 +733,10 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
 }
 
 static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Polls after which a cross-workgroup wait gives up (la_test_set_spin_limit).
+static std::atomic<uint32_t> g_spin_limit{RX_SPIN_LIMIT};
+uint32_t rx_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
 // 32-bit words per row: the digit histograms, then the chunk records (a
 // multiple of 4 words, so rows stay 16-byte aligned)
@@ -742,6 +764,7 @@ static RxKP rx_args(const TopkKParams &p, const RadixPlan &R, void *ws) {
   a.rows = (uint32_t *)base;
   a.row_words = rx_row_words(R.C);
   a.row32 = tk_row_fits_32(p) ? 1 : 0;
+  a.spin_limit = rx_spin_limit();
   base += align256(p.NG * a.row_words * 4);
   base += align256(p.NG * 8);  // the rows' ready words (RadixRowPrep)
   if (p.order == 0) {
@@ -831,6 +854,11 @@ __global__ void dev_status_kernel(int clear) {
                                                      __HIP_MEMORY_SCOPE_AGENT)
                              : __hip_atomic_load(&la_dev_status, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
+}
+
+extern "C" int la_test_set_spin_limit(uint32_t polls) {
+  g_spin_limit.store(polls, std::memory_order_relaxed);
+  return LA_OK;
 }
 
 extern "C" int la_device_status(uint32_t *bits, int32_t clear, void *stream) {

@@ -246,3 +246,49 @@ def test_topk_union_sink_window(dev, n, group):
             got = ids[0, hg, t].cpu().numpy()
             assert list(got[:len(want)]) == want and (got[len(want):] == -1).all(), (hg, t)
             assert int(counts[0, hg, t]) == len(want)
+
+
+def test_radix_waits_give_up_when_forced(dev):
+    """The bounded waits between workgroups (a chunk's look-back over the
+    row's earlier chunks in the multi-workgroup top-k, the decode indexer's
+    wait for a row's first workgroup) are forced to give up at once through
+    the testing hook (a limit of 0 polls): every kernel still ends,
+    LA_DEV_TOPK_TIMEOUT is raised, and with the default limit restored the
+    same calls return the oracle's selection with a clean status."""
+    from linattn_amd.kernels.fused_indexer import indexer_topk
+
+    lib = N.load()
+    n, k = 200000, 5000
+    g = torch.Generator().manual_seed(23)
+    sc = torch.randn(1, 1, 3, n, generator=g, dtype=torch.float64)
+    nv = torch.tensor([n, 3000, n - 5], dtype=torch.int32)
+    q = torch.randn(1, 1, 4, 64, generator=g).bfloat16()
+    kk = torch.randn(1, 70000, 4, 64, generator=g).bfloat16()
+    w = torch.rand(1, 1, 4, generator=g)
+
+    def run_topk():
+        return _topk(sc.to(dev), k=k, width=k, group=1, order=1, pos_offset=0, pos_unit=0,
+                     force_own=False, n_valid=nv.to(dev))
+
+    def run_indexer():
+        return indexer_topk(q.to(dev), kk.to(dev), w.to(dev), 4096, sorted=False)
+
+    N.device_status(dev)
+    try:
+        assert lib.la_test_set_spin_limit(0) == N.LA_OK
+        run_topk()
+        assert N.device_status(dev) & N.LA_DEV_TOPK_TIMEOUT
+        run_indexer()
+        assert N.device_status(dev) & N.LA_DEV_TOPK_TIMEOUT
+    finally:
+        lib.la_test_set_spin_limit(1 << 20)
+    ids, counts, _ = run_topk()
+    assert N.device_status(dev) == 0
+    ri, _ = oracle.topk_rows(sc[0, 0].numpy(), k, n_valid=nv.numpy())
+    want = np.sort(np.where(ri < 0, n, ri), axis=-1)
+    assert np.array_equal(ids[0, 0].cpu().numpy(), np.where(want == n, -1, want))
+    _, idx = run_indexer()
+    assert N.device_status(dev) == 0
+    _, r2 = oracle.indexer_topk(q, kk, w, 4096)
+    want2 = np.sort(r2.reshape(-1))
+    assert np.array_equal(idx.cpu().numpy().reshape(-1), want2)
