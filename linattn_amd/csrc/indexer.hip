@@ -47,9 +47,14 @@ struct IdxKP {
   uint32_t *hist0;
   int64_t hist_stride;
   // with rx_ready: the first workgroup of batch row b clears the row's
-  // hist_stride words of radix records, then stores rx_gen into rx_ready[b];
-  // every workgroup waits for that value before adding into the histogram
+  // hist_stride words of radix records, then stores the call's value
+  // *rx_epoch + rx_gen into rx_ready[b]; every workgroup waits for that value
+  // before adding into the histogram.  rx_gen is a per-call value of the
+  // host (a word left over in the workspace does not hold it by chance), and
+  // the epoch word is advanced by the radix select's first launch (after this
+  // kernel), so a replayed graph of the call waits for a value of its own too.
   uint64_t *rx_ready;
+  const uint64_t *rx_epoch;
   uint64_t rx_gen;
   uint32_t spin_limit;  // polls before that wait is given up (0: at once)
 };
@@ -455,7 +460,8 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
     for (int64_t i = tid; i < p.hist_stride / 4; i += 256) r[i] = make_uint4(0, 0, 0, 0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // every wave's zeros reach the device
     __syncthreads();
-    if (tid == 0) __hip_atomic_store(&p.rx_ready[b], p.rx_gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0)
+      __hip_atomic_store(&p.rx_ready[b], *p.rx_epoch + p.rx_gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
   }
   // Adds this workgroup's first-digit counts into the row's histogram, after
   // the row's records are cleared (a wait on the row's first workgroup, which
@@ -466,6 +472,7 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
     if (tid == 0) {
       uint32_t ok = 1, spins = 0;
       if (prep) {
+        const uint64_t want = *p.rx_epoch + p.rx_gen;
         for (;;) {
           if (spins >= p.spin_limit) {
             ok = 0;
@@ -473,7 +480,7 @@ __global__ __launch_bounds__(256, idf_waves_per_eu<HI>()) void indexer_decode16_
                                   __HIP_MEMORY_SCOPE_AGENT);
             break;
           }
-          if (__hip_atomic_load(&p.rx_ready[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.rx_gen)
+          if (__hip_atomic_load(&p.rx_ready[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == want)
             break;
           ++spins;
           __builtin_amdgcn_s_sleep(2);
@@ -712,18 +719,15 @@ int indexer_status(uint32_t *bits, bool clear, hipStream_t st) {
 }
 }  // namespace la
 
-// A value unique to each call in this process (never 0), for the rows' ready
-// words: a word left over from an earlier call, or from whatever the
-// workspace held before, never equals it (the counter starts at a random
-// 64-bit value).
+// A value of each call (the counter starts at a random 64-bit value and
+// steps by one), for the rows' ready words: with the epoch added, no word
+// left over in the workspace holds the value a call waits for.
 static uint64_t next_radix_gen() {
   static std::atomic<uint64_t> gen{[] {
     std::random_device rd;
     return ((uint64_t)rd() << 32) ^ (uint64_t)rd();
   }()};
-  uint64_t g = gen.fetch_add(1) + 1;
-  while (g == 0) g = gen.fetch_add(1) + 1;
-  return g;
+  return gen.fetch_add(1) + 1;
 }
 
 static int64_t scores_bytes(const la_indexer_args *a, int64_t chunk) {
@@ -789,6 +793,7 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
       p.hist0 = rp.rows;
       p.hist_stride = rp.row_words;
       p.rx_ready = rp.ready;
+      p.rx_epoch = rp.epoch;
       p.rx_gen = next_radix_gen();
       p.spin_limit = rx_spin_limit();
     }

@@ -113,9 +113,11 @@ int topk_radix_launch(const TopkKParams &p, const RadixPlan &R, void *ws, hipStr
 // rows + gi * row_words + bin of radix_row_prep) in between: set-up, that
 // kernel, then the stage launches.  Or without the set-up launch
 // (state_in_kernel): the scores kernel clears row gi's row_words words and
-// then stores a value unique to the call into ready[gi], before any of its
-// workgroups adds into the row's histogram (each waits for that value
-// first); the first stage launch starts the rows from their initial state.
+// then stores *epoch plus a value of the call into ready[gi], before any of
+// its workgroups adds into the row's histogram (each waits for that value
+// first); the first stage launch starts the rows from their initial state
+// and advances *epoch (one word for all rows), so a replay of the same
+// launches waits for a value of its own.
 // Polls after which the radix select's and the decode indexer's waits on
 // other workgroups give up (2^20 unless la_test_set_spin_limit changed it).
 uint32_t rx_spin_limit();
@@ -124,6 +126,7 @@ struct RadixRowPrep {
   uint32_t *rows = nullptr;
   int64_t row_words = 0;
   uint64_t *ready = nullptr;
+  uint64_t *epoch = nullptr;
 };
 RadixRowPrep radix_row_prep(const TopkKParams &p, const RadixPlan &R, void *ws);
 int topk_radix_setup(const TopkKParams &p, const RadixPlan &R, void *ws, bool hist0_external,

@@ -131,6 +131,7 @@ struct RxKP {
   int64_t C;
   int32_t state_in_kernel;  // launch 0 starts from the initial state (no set-up launch)
   int32_t row32;            // tk_row's quotients fit 32-bit arithmetic
+  uint64_t *epoch;          // the scores kernel's ready-word epoch (RadixRowPrep)
   uint32_t spin_limit;      // polls before a cross-workgroup wait is given up
 };
 
@@ -208,6 +209,9 @@ __global__ __launch_bounds__(TK_NT) void rx_stage_kernel(RxKP a, int launch, int
   const RxState *sin = a.state + (launch & 1) * NG + gi;
   RxState *sout = a.state + ((launch + 1) & 1) * NG + gi;
   const bool init = a.state_in_kernel && launch == 0;
+  // the scores kernel's ready-word epoch moves on (it read it before this
+  // launch began), so the next call waits for a value of its own
+  if (init && c == 0 && gi == 0 && tid == 0) *a.epoch += 1;
   // (read in the first launch too, where the initial state replaces it:
   // no branch keeps the loads apart from their use)
   uint4 sv[3];
@@ -749,7 +753,7 @@ RadixPlan radix_plan(const TopkKParams &p) {
   if (p.n >= ((int64_t)1 << 31)) return R;
   R.C = ceil_div(p.n, RX_CHUNK);
   R.bytes = align256(2 * p.NG * (int64_t)sizeof(RxState)) + align256(p.NG * rx_row_words(R.C) * 4) +
-            align256(p.NG * 8);
+            align256((p.NG + 1) * 8);
   if (p.order == 0) R.bytes += align256(p.NG * p.k * 8) + align256(p.NG * p.k * 4);
   return R;
 }
@@ -766,7 +770,8 @@ static RxKP rx_args(const TopkKParams &p, const RadixPlan &R, void *ws) {
   a.row32 = tk_row_fits_32(p) ? 1 : 0;
   a.spin_limit = rx_spin_limit();
   base += align256(p.NG * a.row_words * 4);
-  base += align256(p.NG * 8);  // the rows' ready words (RadixRowPrep)
+  a.epoch = (uint64_t *)base + p.NG;
+  base += align256((p.NG + 1) * 8);  // the rows' ready words and the epoch (RadixRowPrep)
   if (p.order == 0) {
     a.cand_sc = (double *)base;
     a.cand_id = (int32_t *)(base + align256(p.NG * p.k * 8));
@@ -780,6 +785,7 @@ RadixRowPrep radix_row_prep(const TopkKParams &p, const RadixPlan &R, void *ws) 
   r.rows = a.rows;
   r.row_words = a.row_words;
   r.ready = (uint64_t *)((char *)a.rows + align256(p.NG * a.row_words * 4));
+  r.epoch = a.epoch;
   return r;
 }
 
