@@ -57,6 +57,12 @@ struct IdxKP {
   const uint64_t *rx_epoch;
   uint64_t rx_gen;
   uint32_t spin_limit;  // polls before that wait is given up (0: at once)
+  // the integer-limb form of bf16 q and k (indexer_limb_kernel, d == 64): per
+  // 16-row block, head and limb, the block in the matrix-core operand order;
+  // per row and head the packed exponent word (lm_* in the limb kernel)
+  const int8_t *lq, *lk;
+  const int32_t *xq, *xk;
+  int64_t nqb, nkb;  // 16-row blocks per batch row of q (the chunk) and of k
 };
 
 // Status bits this file's kernels raise on the current device (read through
@@ -312,6 +318,271 @@ __global__ __launch_bounds__(IM_NT, 3) void indexer_mfma_kernel(IdxKP p) {
         const int64_t s = k0 + 32 * kw + 16 * ib + 4 * e + kq;
         if (s < p.Tk) row[s] = score[ib][jb][e];
       }
+  }
+}
+
+// ------------------------------------------------ integer-limb scores ----
+// The same scores on the int8 matrix cores, exact: a bf16 value is
+// x = m 2^(e - 134) with an integer m < 256 (sign included), so over the 64
+// values of one (row, head) with least exponent E, x = X 2^(E - 134) with the
+// integer X = m 2^(e - E), |X| < 2^(8 + R), R the row's exponent range.  For
+// R <= 22, X is four balanced base-256 digits (limbs, int8), and the head's
+// dot of a query row and a key row is the integer sum over the 16 limb pairs
+// of int8 dots (v_mfma_i32_16x16x64_i8, exact in int32), scaled by
+// 2^(Eq + Ek - 268).  That integer equals the fp64 sequential sum of the
+// (exact) products whenever every partial sum is exact, which holds when
+// Rq + Rk <= 30 (the partial sums stay below 64 * 2^(16 + Rq + Rk) <= 2^52
+// units of the least product bit).  A pair outside that bound (or a row with
+// an inf / nan, or R > 22) takes the sequential fp64 sum of the bf16 values
+// instead, in the same order as the oracle.  The heads are then added in
+// order as in the fp64 kernel.
+
+// Packed exponent word of a (row, head): E + 1024 in bits 0-15, R in bits
+// 16-23 (255: no limbs, the sequential sum is taken).
+constexpr int LM_NOLIMB = 255;
+
+// One wave per (batch, row, head): lane d converts element d.  Rows past n
+// (the padding of the last 64-row tile) get zero limbs.
+__global__ __launch_bounds__(256) void indexer_limb_kernel(const uint16_t *src, int64_t sb, int64_t st,
+                                                           int64_t sh, int64_t r0, int64_t n,
+                                                           int64_t n_pad, int64_t HI, int8_t *limbs,
+                                                           int32_t *xw) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t h = gw % HI, rr = gw / HI;
+  const int64_t row = rr % n_pad, b = rr / n_pad;
+  const uint32_t x = row < n ? (uint32_t)src[b * sb + (r0 + row) * st + h * sh + lane] : 0u;
+  const uint32_t E = (x >> 7) & 0xffu, f = x & 0x7fu;
+  const int m = E ? (int)(128u + f) : (int)f;
+  const int e = E ? (int)E : 1;
+  const bool nz = m != 0;
+  const bool special = E == 255u;
+  int emin = nz ? e : 1 << 20, emax = nz ? e : -1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    emin = min(emin, __shfl_xor(emin, o, 64));
+    emax = max(emax, __shfl_xor(emax, o, 64));
+  }
+  const bool any_special = __ballot(special) != 0;
+  if (emax < 0) emin = emax = 0;  // all zero
+  const int R = emax - emin;
+  const bool nolimb = any_special || R > 22;
+  int X = nolimb ? 0 : m << (e - emin);  // |X| < 2^30
+  if (x >> 15) X = -X;
+  int8_t dg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int di = ((X + 128) & 255) - 128;
+    dg[i] = (int8_t)di;
+    X = (X - di) >> 8;
+  }
+  // block (row / 16), lane position (row % 16) + 16 (d / 16), byte d % 16
+  int8_t *blk = limbs + ((b * (n_pad / 16) + row / 16) * HI + h) * 4096;
+  const int pos = (int)(row % 16) + 16 * (lane / 16);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) blk[i * 1024 + pos * 16 + (lane % 16)] = dg[i];
+  if (lane == 0) xw[(b * n_pad + row) * HI + h] = (emin + 1024) | ((nolimb ? LM_NOLIMB : R) << 16);
+}
+
+// A workgroup covers 64 queries x 64 keys (the fp64 kernel's tiles; two
+// workgroups per CU, for its registers); wave w keys [k0 + 32 (w % 2), +32) x
+// queries [q0 + 32 (w / 2), +32) as 2 x 2 tiles of 16 x 16.  Lane l supplies
+// key / query row l % 16 of a tile, d = 16 (l / 16) .. + 15 (the limb blocks
+// are stored in that order), and receives D[4 (l / 16) + i][l % 16]: key
+// 4 (l / 16) + i, query l % 16.
+template <int HIc>
+__global__ __launch_bounds__(IM_NT, 2) void indexer_i8_kernel(IdxKP p) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  // the limb blocks of one head: 4 key and 4 query 16-row blocks x 4 limbs,
+  // 1 KiB each, copied by the LDS-DMA loads; every wave takes its operands
+  // into registers first, and the next head's copy is issued then
+  __shared__ __align__(16) int8_t sl[2][4][4][1024];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t b = blockIdx.z;
+  const int64_t q0 = (int64_t)blockIdx.y * IT_Q;  // within the chunk
+  const int64_t k0 = (int64_t)blockIdx.x * IM_K;
+  if (q0 >= p.tn) return;
+  if (p.causal) {
+    const int64_t last_q = p.offset + p.t0 + min(q0 + IT_Q, p.tn) - 1;
+    if (k0 * p.unit > last_q) return;
+  }
+  constexpr int HI = HIc;
+  const int kw = w & 1, qw = w >> 1;
+  const int g4 = lane >> 4, c16 = lane & 15;
+  const int64_t kbw = k0 / 16, qbw = q0 / 16;  // the workgroup's first blocks
+  // wave w copies blocks 8 w .. 8 w + 7 of a head's 32 (k blocks, then q)
+  auto copy_head = [&](int h) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = 8 * w + u, side = j >> 4, blk = (j >> 2) & 3, limb = j & 3;
+      const int8_t *src = side == 0 ? p.lk + ((b * p.nkb + kbw + blk) * HI + h) * 4096
+                                    : p.lq + ((b * p.nqb + qbw + blk) * HI + h) * 4096;
+      dma16(src + limb * 1024 + lane * 16, &sl[side][blk][limb][0]);
+    }
+  };
+  // the head weights of this lane's two queries (registers, loaded now and
+  // used one head after another)
+  float wq[2][HI];
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb) {
+    const int64_t t = p.t0 + min(q0 + 32 * qw + 16 * jb + c16, p.tn - 1);
+#pragma unroll
+    for (int hh = 0; hh < HI; ++hh) wq[jb][hh] = p.w[b * p.w_sb + t * p.w_st + hh * p.w_sh];
+  }
+  double score[2][2][4];
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) score[ib][jb][i] = 0.0;
+  const uint16_t *qg = (const uint16_t *)p.q + b * p.q_sb;
+  const uint16_t *kg = (const uint16_t *)p.k + b * p.k_sb;
+  // a double 2^e (normal range)
+  auto pow2 = [](int e) { return __longlong_as_double((long long)(e + 1023) << 52); };
+  copy_head(0);
+#pragma unroll
+  for (int h = 0; h < HI; ++h) {
+    // this lane's exponent words: its 4 keys of each key tile, its query of
+    // each query tile (issued before the wait, landing with the copies)
+    int32_t xk[2][4], xq[2];
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xk[ib][i] = p.xk[((b * p.nkb + kbw + 2 * kw + ib) * 16 + 4 * g4 + i) * HI + h];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) xq[jb] = p.xq[((b * p.nqb + qbw + 2 * qw + jb) * 16 + c16) * HI + h];
+    wait_vmcnt<0>();  // this wave's copies of head h (and the words)
+    __syncthreads();  // every wave's copies
+    v4i A[2][4], B[2][4];
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int l = 0; l < 4; ++l) A[ib][l] = *(const v4i *)&sl[0][2 * kw + ib][l][lane * 16];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int l = 0; l < 4; ++l) B[jb][l] = *(const v4i *)&sl[1][2 * qw + jb][l][lane * 16];
+    if (h + 1 < HI) {
+      __syncthreads();  // every wave holds its operands: the buffer is free
+      copy_head(h + 1);
+    }
+    // a 16-row block whose rows all have R <= 14 has a zero fourth limb
+    // (|X| < 2^22): tiles of two such blocks take 3 x 3 limb pairs, and no
+    // pair of theirs can leave the exact bound (R + R <= 28)
+    bool kbig[2], qbig[2];
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      bool big = false;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) big |= ((xk[ib][i] >> 16) & 0xff) > 14;
+      kbig[ib] = __ballot(big) != 0;
+    }
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) qbig[jb] = __ballot(((xq[jb] >> 16) & 0xff) > 14) != 0;
+    double wsq[2];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) wsq[jb] = (double)wq[jb][h] * pow2((xq[jb] & 0xffff) - 1024 - 134);
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        double prod[4];
+        if (!kbig[ib] && !qbig[jb]) {
+          v4i acc[5];
+#pragma unroll
+          for (int g = 0; g < 5; ++g) acc[g] = v4i{0, 0, 0, 0};
+#pragma unroll
+          for (int la = 0; la < 3; ++la)
+#pragma unroll
+            for (int lb = 0; lb < 3; ++lb)
+              acc[la + lb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ib][la], B[jb][lb], acc[la + lb], 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // lo + m1 2^16 + top 2^32, each part within int32
+            const int32_t lo = acc[0][i] + acc[1][i] * 256;
+            const int32_t m1 = acc[2][i] + acc[3][i] * 256;
+            double v = (double)acc[4][i];
+            v = __builtin_fma(v, 65536.0, (double)m1);
+            v = __builtin_fma(v, 65536.0, (double)lo);
+            const double x = v * pow2((xk[ib][i] & 0xffff) - 1024 - 134);
+            prod[i] = wsq[jb] * (x > 0.0 ? x : 0.0);
+          }
+        } else {
+          v4i acc[7];
+#pragma unroll
+          for (int g = 0; g < 7; ++g) acc[g] = v4i{0, 0, 0, 0};
+#pragma unroll
+          for (int la = 0; la < 4; ++la)
+#pragma unroll
+            for (int lb = 0; lb < 4; ++lb)
+              acc[la + lb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ib][la], B[jb][lb], acc[la + lb], 0, 0, 0);
+          bool bad[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // lo + m1 2^16 + m2 2^32 + top 2^48, each part within int32
+            const int32_t lo = acc[0][i] + acc[1][i] * 256;
+            const int32_t m1 = acc[2][i] + acc[3][i] * 256;
+            const int32_t m2 = acc[4][i] + acc[5][i] * 256;
+            double v = (double)acc[6][i];
+            v = __builtin_fma(v, 65536.0, (double)m2);
+            v = __builtin_fma(v, 65536.0, (double)m1);
+            v = __builtin_fma(v, 65536.0, (double)lo);
+            const double x = v * pow2((xk[ib][i] & 0xffff) - 1024 - 134);
+            prod[i] = wsq[jb] * (x > 0.0 ? x : 0.0);
+            bad[i] = ((xk[ib][i] >> 16) & 0xff) + ((xq[jb] >> 16) & 0xff) > 30;
+          }
+          if (__ballot(bad[0] || bad[1] || bad[2] || bad[3])) {
+            // outside the exact bound: the sequential fp64 sum of the values
+            const int64_t ql = q0 + 32 * qw + 16 * jb + c16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int64_t s = k0 + 32 * kw + 16 * ib + 4 * g4 + i;
+              if (bad[i] && ql < p.tn && s < p.Tk) {
+                const uint4 *qr = (const uint4 *)(qg + (p.t0 + ql) * p.q_st + h * p.q_sh);
+                const uint4 *kr = (const uint4 *)(kg + s * p.k_st + h * p.k_sh);
+                double a = 0.0;
+#pragma unroll 1
+                for (int c = 0; c < 8; ++c) {  // 8 values per 16-byte load, in order
+                  const uint4 qv = qr[c], kv = kr[c];
+                  const uint32_t qw4[4] = {qv.x, qv.y, qv.z, qv.w}, kw4[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) {
+                    a = __builtin_fma((double)bf16lo(qw4[e]), (double)bf16lo(kw4[e]), a);
+                    a = __builtin_fma((double)bf16hi(qw4[e]), (double)bf16hi(kw4[e]), a);
+                  }
+                }
+                prod[i] = (double)wq[jb][h] * (a > 0.0 ? a : 0.0);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) score[ib][jb][i] = score[ib][jb][i] + prod[i];
+      }
+  }
+  // the 64 x 64 scores leave through LDS (the limb buffer, free now), each
+  // query row written as one contiguous 512-byte run; column k of row q sits
+  // at k ^ 4 (q % 16), so that the 16 rows a store instruction touches fall
+  // in different banks
+  __syncthreads();
+  double *st = (double *)&sl[0][0][0][0];
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = 32 * qw + 16 * jb + c16, k = 32 * kw + 16 * ib + 4 * g4 + i;
+        st[q * IM_K + (k ^ (4 * (q & 15)))] = score[ib][jb][i];
+      }
+  __syncthreads();
+  const int64_t s = k0 + lane;
+#pragma unroll 4
+  for (int r = w; r < IT_Q; r += 4) {
+    const int64_t ql = q0 + r;
+    if (ql < p.tn && s < p.Tk) p.scores[(b * p.tn + ql) * p.Tk + s] = st[r * IM_K + (lane ^ (4 * (r & 15)))];
   }
 }
 
@@ -734,10 +1005,32 @@ static int64_t scores_bytes(const la_indexer_args *a, int64_t chunk) {
   return (a->B * chunk * a->Tk * 8 + 255) / 256 * 256;
 }
 
+// The integer-limb score kernel applies: bf16 q and k in 16-byte aligned
+// (head, 64-d) rows, a few queries or more (not the decode forms).
+static bool use_limbs(const la_indexer_args *a) {
+  const bool decode = a->Tq <= ID_MAXQ && a->HI * a->d <= ID_MAXHD;
+  return !decode && a->in_dtype == LA_BF16 && a->d == 64 &&
+         (a->HI == 1 || a->HI == 2 || a->HI == 4 || a->HI == 8) && a->q_st % 8 == 0 &&
+         a->q_sh % 8 == 0 && a->q_sb % 8 == 0 && a->k_st % 8 == 0 && a->k_sh % 8 == 0 &&
+         a->k_sb % 8 == 0 && (uintptr_t)a->q % 16 == 0 && (uintptr_t)a->kk % 16 == 0;
+}
+
+// 16-row blocks of a padded (64-row multiple) run of n rows
+static int64_t limb_blocks(int64_t n) { return ceil_div(n, 64) * 4; }
+
+// Bytes of the limb form: the blocks (4 KiB per block and head) and the
+// exponent words (4 bytes per row and head) of q (one chunk) and of k.
+static int64_t limbs_bytes(const la_indexer_args *a, int64_t chunk) {
+  if (!use_limbs(a)) return 0;
+  const int64_t nq = limb_blocks(chunk), nk = limb_blocks(a->Tk);
+  return (a->B * (nq + nk) * a->HI * (4096 + 16 * 4) + 255) / 256 * 256;
+}
+
 extern "C" size_t la_indexer_topk_workspace(const la_indexer_args *a) {
   if (validate(a) != LA_OK) return 0;
   const int64_t chunk = pick_chunk(a);
-  return (size_t)(scores_bytes(a, chunk) + topk_workspace_bytes(topk_params(a, nullptr, 0, chunk)));
+  return (size_t)(scores_bytes(a, chunk) + topk_workspace_bytes(topk_params(a, nullptr, 0, chunk)) +
+                  limbs_bytes(a, chunk));
 }
 
 extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
@@ -745,7 +1038,8 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
   if (rc != LA_OK) return rc;
   const int64_t chunk = pick_chunk(a);
   const int64_t sc_bytes = scores_bytes(a, chunk);
-  const size_t need = (size_t)(sc_bytes + topk_workspace_bytes(topk_params(a, nullptr, 0, chunk)));
+  const int64_t tk_bytes = topk_workspace_bytes(topk_params(a, nullptr, 0, chunk));
+  const size_t need = (size_t)(sc_bytes + tk_bytes + limbs_bytes(a, chunk));
   if (!a->workspace || (size_t)a->ws_bytes < need)
     return fail(LA_ERR_WORKSPACE, "la_indexer_topk: workspace %lld < %zu bytes",
                 (long long)a->ws_bytes, need);
@@ -761,6 +1055,22 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
                       a->q_st % 8 == 0 && a->q_sh % 8 == 0 && a->q_sb % 8 == 0 &&
                       a->k_st % 8 == 0 && a->k_sh % 8 == 0 && a->k_sb % 8 == 0 &&
                       (uintptr_t)a->q % 16 == 0 && (uintptr_t)a->kk % 16 == 0;
+  // the limb form of k (once per call) and its buffers; q's per chunk below
+  const bool limbs = use_limbs(a);
+  const int64_t nqb = limb_blocks(chunk), nkb = limb_blocks(a->Tk);
+  int8_t *lk = nullptr, *lq = nullptr;
+  int32_t *xk = nullptr, *xq = nullptr;
+  if (limbs) {
+    char *base = (char *)a->workspace + sc_bytes + (tk_bytes + 255) / 256 * 256;
+    lk = (int8_t *)base;
+    lq = lk + a->B * nkb * a->HI * 4096;
+    xk = (int32_t *)(lq + a->B * nqb * a->HI * 4096);
+    xq = xk + a->B * nkb * 16 * a->HI;
+    const int64_t waves = a->B * nkb * 16 * a->HI;
+    indexer_limb_kernel<<<dim3((unsigned)(waves / 4)), 256, 0, st>>>(
+        (const uint16_t *)a->kk, a->k_sb, a->k_st, a->k_sh, 0, a->Tk, nkb * 16, a->HI, lk, xk);
+    LA_LAUNCHED();
+  }
   for (int64_t t0 = 0; t0 < a->Tq; t0 += chunk) {
     IdxKP p{};
     p.q = a->q;
@@ -812,7 +1122,24 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
       const dim3 grid((unsigned)ceil_div(a->Tk, IT_K), (unsigned)ceil_div(p.tn, IT_Q), (unsigned)a->B);
       const dim3 grid_m((unsigned)ceil_div(a->Tk, IM_K), (unsigned)ceil_div(p.tn, IT_Q),
                         (unsigned)a->B);
-      if (tile16 && a->in_dtype == LA_BF16)
+      if (limbs) {
+        const int64_t waves = a->B * nqb * 16 * a->HI;
+        indexer_limb_kernel<<<dim3((unsigned)(waves / 4)), 256, 0, st>>>(
+            (const uint16_t *)a->q, a->q_sb, a->q_st, a->q_sh, t0, p.tn, nqb * 16, a->HI, lq, xq);
+        LA_LAUNCHED();
+        p.lq = lq;
+        p.lk = lk;
+        p.xq = xq;
+        p.xk = xk;
+        p.nqb = nqb;
+        p.nkb = nkb;
+        switch (a->HI) {
+          case 1: indexer_i8_kernel<1><<<grid_m, IM_NT, 0, st>>>(p); break;
+          case 2: indexer_i8_kernel<2><<<grid_m, IM_NT, 0, st>>>(p); break;
+          case 4: indexer_i8_kernel<4><<<grid_m, IM_NT, 0, st>>>(p); break;
+          default: indexer_i8_kernel<8><<<grid_m, IM_NT, 0, st>>>(p); break;
+        }
+      } else if (tile16 && a->in_dtype == LA_BF16)
         indexer_mfma_kernel<true><<<grid_m, IM_NT, 0, st>>>(p);
       else if (tile16)
         indexer_mfma_kernel<false><<<grid_m, IM_NT, 0, st>>>(p);
@@ -821,7 +1148,7 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     }
     LA_LAUNCHED();
     rc = R.C > 0 ? topk_radix_finish(tp, R, tws, true, true, st)
-                 : topk_launch_ws(tp, tws, a->ws_bytes - sc_bytes, st);
+                 : topk_launch_ws(tp, tws, tk_bytes, st);
     if (rc != LA_OK) return rc;
   }
   return LA_OK;
