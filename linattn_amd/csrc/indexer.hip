@@ -341,47 +341,61 @@ __global__ __launch_bounds__(IM_NT, 3) void indexer_mfma_kernel(IdxKP p) {
 // 16-23 (255: no limbs, the sequential sum is taken).
 constexpr int LM_NOLIMB = 255;
 
-// One wave per (batch, row, head): lane d converts element d.  Rows past n
-// (the padding of the last 64-row tile) get zero limbs.
+// Sixteen lanes per (batch, row, head): lane j converts elements 4 j .. 4 j + 3
+// and stores their limbs as one 4-byte word per limb.  Rows past n (the
+// padding of the last 64-row tile) get zero limbs.
 __global__ __launch_bounds__(256) void indexer_limb_kernel(const uint16_t *src, int64_t sb, int64_t st,
                                                            int64_t sh, int64_t r0, int64_t n,
                                                            int64_t n_pad, int64_t HI, int8_t *limbs,
                                                            int32_t *xw) {
-  const int lane = threadIdx.x & 63;
-  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t h = gw % HI, rr = gw / HI;
+  const int64_t gt = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int j = (int)(gt & 15);
+  const int64_t rh = gt >> 4;
+  const int64_t h = rh % HI, rr = rh / HI;
   const int64_t row = rr % n_pad, b = rr / n_pad;
-  const uint32_t x = row < n ? (uint32_t)src[b * sb + (r0 + row) * st + h * sh + lane] : 0u;
-  const uint32_t E = (x >> 7) & 0xffu, f = x & 0x7fu;
-  const int m = E ? (int)(128u + f) : (int)f;
-  const int e = E ? (int)E : 1;
-  const bool nz = m != 0;
-  const bool special = E == 255u;
-  int emin = nz ? e : 1 << 20, emax = nz ? e : -1;
+  uint2 raw = make_uint2(0u, 0u);
+  if (row < n) raw = *(const uint2 *)(src + b * sb + (r0 + row) * st + h * sh + 4 * j);
+  const uint32_t xs[4] = {raw.x & 0xffffu, raw.x >> 16, raw.y & 0xffffu, raw.y >> 16};
+  int m[4], e[4];
+  int emin = 1 << 20, emax = -1, special = 0;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t E = (xs[u] >> 7) & 0xffu, f = xs[u] & 0x7fu;
+    m[u] = E ? (int)(128u + f) : (int)f;
+    e[u] = E ? (int)E : 1;
+    special |= E == 255u;
+    if (m[u] != 0) {
+      emin = min(emin, e[u]);
+      emax = max(emax, e[u]);
+    }
+  }
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) {  // over the row's 16 lanes
     emin = min(emin, __shfl_xor(emin, o, 64));
     emax = max(emax, __shfl_xor(emax, o, 64));
+    special |= __shfl_xor(special, o, 64);
   }
-  const bool any_special = __ballot(special) != 0;
   if (emax < 0) emin = emax = 0;  // all zero
   const int R = emax - emin;
-  const bool nolimb = any_special || R > 22;
-  int X = nolimb ? 0 : m << (e - emin);  // |X| < 2^30
-  if (x >> 15) X = -X;
-  int8_t dg[4];
+  const bool nolimb = special || R > 22;
+  uint32_t word[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int di = ((X + 128) & 255) - 128;
-    dg[i] = (int8_t)di;
-    X = (X - di) >> 8;
+  for (int u = 0; u < 4; ++u) {
+    int X = nolimb ? 0 : m[u] << (e[u] - emin);  // |X| < 2^30
+    if (xs[u] >> 15) X = -X;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int di = ((X + 128) & 255) - 128;
+      word[i] |= (uint32_t)(di & 255) << (8 * u);
+      X = (X - di) >> 8;
+    }
   }
   // block (row / 16), lane position (row % 16) + 16 (d / 16), byte d % 16
   int8_t *blk = limbs + ((b * (n_pad / 16) + row / 16) * HI + h) * 4096;
-  const int pos = (int)(row % 16) + 16 * (lane / 16);
+  const int pos = (int)(row % 16) + 16 * (j / 4);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) blk[i * 1024 + pos * 16 + (lane % 16)] = dg[i];
-  if (lane == 0) xw[(b * n_pad + row) * HI + h] = (emin + 1024) | ((nolimb ? LM_NOLIMB : R) << 16);
+  for (int i = 0; i < 4; ++i) *(uint32_t *)(blk + i * 1024 + pos * 16 + 4 * (j % 4)) = word[i];
+  if (j == 0) xw[(b * n_pad + row) * HI + h] = (emin + 1024) | ((nolimb ? LM_NOLIMB : R) << 16);
 }
 
 // A workgroup covers 64 queries x 64 keys (the fp64 kernel's tiles; two
@@ -394,9 +408,8 @@ template <int HIc>
 __global__ __launch_bounds__(IM_NT, 2) void indexer_i8_kernel(IdxKP p) {
   typedef int v4i __attribute__((ext_vector_type(4)));
   // the limb blocks of one head: 4 key and 4 query 16-row blocks x 4 limbs,
-  // 1 KiB each, copied by the LDS-DMA loads; every wave takes its operands
-  // into registers first, and the next head's copy is issued then
-  __shared__ __align__(16) int8_t sl[2][4][4][1024];
+  // 1 KiB each, copied by the LDS-DMA loads a head ahead (two buffers)
+  __shared__ __align__(16) int8_t sl[2][2][4][4][1024];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t b = blockIdx.z;
   const int64_t q0 = (int64_t)blockIdx.y * IT_Q;  // within the chunk
@@ -417,7 +430,7 @@ __global__ __launch_bounds__(IM_NT, 2) void indexer_i8_kernel(IdxKP p) {
       const int j = 8 * w + u, side = j >> 4, blk = (j >> 2) & 3, limb = j & 3;
       const int8_t *src = side == 0 ? p.lk + ((b * p.nkb + kbw + blk) * HI + h) * 4096
                                     : p.lq + ((b * p.nqb + qbw + blk) * HI + h) * 4096;
-      dma16(src + limb * 1024 + lane * 16, &sl[side][blk][limb][0]);
+      dma16(src + limb * 1024 + lane * 16, &sl[h & 1][side][blk][limb][0]);
     }
   };
   // the head weights of this lane's two queries (registers, loaded now and
@@ -440,12 +453,9 @@ __global__ __launch_bounds__(IM_NT, 2) void indexer_i8_kernel(IdxKP p) {
   const uint16_t *kg = (const uint16_t *)p.k + b * p.k_sb;
   // a double 2^e (normal range)
   auto pow2 = [](int e) { return __longlong_as_double((long long)(e + 1023) << 52); };
-  copy_head(0);
-#pragma unroll
-  for (int h = 0; h < HI; ++h) {
-    // this lane's exponent words: its 4 keys of each key tile, its query of
-    // each query tile (issued before the wait, landing with the copies)
-    int32_t xk[2][4], xq[2];
+  // this lane's exponent words of a head: its 4 keys of each key tile, its
+  // query of each query tile (loaded with the head's copies, a head ahead)
+  auto load_x = [&](int h, int32_t (&xk)[2][4], int32_t (&xq)[2]) {
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
@@ -453,21 +463,35 @@ __global__ __launch_bounds__(IM_NT, 2) void indexer_i8_kernel(IdxKP p) {
         xk[ib][i] = p.xk[((b * p.nkb + kbw + 2 * kw + ib) * 16 + 4 * g4 + i) * HI + h];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) xq[jb] = p.xq[((b * p.nqb + qbw + 2 * qw + jb) * 16 + c16) * HI + h];
+  };
+  int32_t xk[2][4], xq[2], nxk[2][4], nxq[2];
+  copy_head(0);
+  load_x(0, xk, xq);
+#pragma unroll
+  for (int h = 0; h < HI; ++h) {
+    if (h > 0) {
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xk[ib][i] = nxk[ib][i];
+      xq[0] = nxq[0];
+      xq[1] = nxq[1];
+    }
     wait_vmcnt<0>();  // this wave's copies of head h (and the words)
-    __syncthreads();  // every wave's copies
+    __syncthreads();  // every wave's copies; head h - 1's buffer is free
+    if (h + 1 < HI) {
+      copy_head(h + 1);
+      load_x(h + 1, nxk, nxq);
+    }
     v4i A[2][4], B[2][4];
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-      for (int l = 0; l < 4; ++l) A[ib][l] = *(const v4i *)&sl[0][2 * kw + ib][l][lane * 16];
+      for (int l = 0; l < 4; ++l) A[ib][l] = *(const v4i *)&sl[h & 1][0][2 * kw + ib][l][lane * 16];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int l = 0; l < 4; ++l) B[jb][l] = *(const v4i *)&sl[1][2 * qw + jb][l][lane * 16];
-    if (h + 1 < HI) {
-      __syncthreads();  // every wave holds its operands: the buffer is free
-      copy_head(h + 1);
-    }
+      for (int l = 0; l < 4; ++l) B[jb][l] = *(const v4i *)&sl[h & 1][1][2 * qw + jb][l][lane * 16];
     // a 16-row block whose rows all have R <= 14 has a zero fourth limb
     // (|X| < 2^22): tiles of two such blocks take 3 x 3 limb pairs, and no
     // pair of theirs can leave the exact bound (R + R <= 28)
@@ -567,7 +591,7 @@ __global__ __launch_bounds__(IM_NT, 2) void indexer_i8_kernel(IdxKP p) {
   // at k ^ 4 (q % 16), so that the 16 rows a store instruction touches fall
   // in different banks
   __syncthreads();
-  double *st = (double *)&sl[0][0][0][0];
+  double *st = (double *)&sl[0][0][0][0][0];
 #pragma unroll
   for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
@@ -1066,8 +1090,8 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     lq = lk + a->B * nkb * a->HI * 4096;
     xk = (int32_t *)(lq + a->B * nqb * a->HI * 4096);
     xq = xk + a->B * nkb * 16 * a->HI;
-    const int64_t waves = a->B * nkb * 16 * a->HI;
-    indexer_limb_kernel<<<dim3((unsigned)(waves / 4)), 256, 0, st>>>(
+    const int64_t groups = a->B * nkb * 16 * a->HI;  // 16 lanes each
+    indexer_limb_kernel<<<dim3((unsigned)(groups / 16)), 256, 0, st>>>(
         (const uint16_t *)a->kk, a->k_sb, a->k_st, a->k_sh, 0, a->Tk, nkb * 16, a->HI, lk, xk);
     LA_LAUNCHED();
   }
@@ -1123,8 +1147,8 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
       const dim3 grid_m((unsigned)ceil_div(a->Tk, IM_K), (unsigned)ceil_div(p.tn, IT_Q),
                         (unsigned)a->B);
       if (limbs) {
-        const int64_t waves = a->B * nqb * 16 * a->HI;
-        indexer_limb_kernel<<<dim3((unsigned)(waves / 4)), 256, 0, st>>>(
+        const int64_t groups = a->B * nqb * 16 * a->HI;  // 16 lanes each
+        indexer_limb_kernel<<<dim3((unsigned)(groups / 16)), 256, 0, st>>>(
             (const uint16_t *)a->q, a->q_sb, a->q_st, a->q_sh, t0, p.tn, nqb * 16, a->HI, lq, xq);
         LA_LAUNCHED();
         p.lq = lq;
