@@ -423,7 +423,9 @@ __global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 3 : 1) void topk_re
 
   const int tid = threadIdx.x, lane = tid & 63;
   const uint64_t lt = lanemask_lt(lane);
-  const TkRow rw = tk_row(p, blockIdx.x);
+  // groups taken last first: in causal rows the valid prefix grows with the
+  // group, so the longest rows start first and the short ones fill the tail
+  const TkRow rw = tk_row(p, (int64_t)gridDim.x - 1 - blockIdx.x);
   const int32_t n_v = (int32_t)rw.n_v;  // n_v <= 256*KPT
   const int32_t own = (int32_t)rw.own;
   uint32_t *bm = nullptr;
@@ -589,12 +591,14 @@ __global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 3 : 1) void topk_re
     const uint64_t range = mn2 <= mx ? tmx - img(mn2) : 0ull;
     const int nbits = range ? 64 - __clzll((long long)range) : 0;
     const int shift = nbits > TKB_BITS ? nbits - TKB_BITS : 0;
+    auto bucket = [&](uint64_t k) -> uint32_t {
+      return k == KEY_FORCED ? 0u : k == mn ? (uint32_t)TKB_N + 1u : 1u + (uint32_t)((tmx - img(k)) >> shift);
+    };
     uint32_t bk[E], slot[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       if (bidx[e] >= 0) {
-        const uint64_t k = bkey[e];
-        bk[e] = k == KEY_FORCED ? 0u : k == mn ? (uint32_t)TKB_N + 1u : 1u + (uint32_t)((tmx - img(k)) >> shift);
+        bk[e] = bucket(bkey[e]);
         slot[e] = atomicAdd(&s_bins[bk[e]], 1u);
         if (bk[e] == (uint32_t)TKB_N + 1u) atomicOr(&s_tie[bidx[e] >> 5], 1u << (bidx[e] & 31));
       }
@@ -640,6 +644,16 @@ __global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 3 : 1) void topk_re
         }
       }
       __syncthreads();
+      // thread t now ranks the keys at bucket-order positions t + 256 e: the
+      // 64 lanes of a wave take neighbouring buckets, of similar sizes, so
+      // the rank loops below diverge less than over keys in arrival order
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int i = tid + TK_NT * e;
+        bkey[e] = i < K ? skey[i] : 0ull;
+        bidx[e] = i < K ? sidx[i] : -1;
+        bk[e] = i < K ? bucket(bkey[e]) : 0u;
+      }
       uint32_t pos[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) {
