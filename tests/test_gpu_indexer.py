@@ -151,6 +151,57 @@ def test_indexer_summation_order_is_sequential(dev):
     assert np.array_equal(val[0, -1].cpu().numpy(), want)
 
 
+def limb_rows(n, hi, d, ranges, seed):
+    """bf16 rows whose (row, head) exponent range R (largest minus least
+    exponent of the non-zero values) is one of `ranges`, cycled over rows and
+    heads; -1 gives an all-zero row, -2 a row of subnormals only, -3 a row
+    mixing subnormals with values near 1 (R above 120)."""
+    r = np.random.default_rng(seed)
+    x = np.zeros((n, hi, d))
+    for i in range(n):
+        for h in range(hi):
+            R = ranges[(i * hi + h) % len(ranges)]
+            sign = r.choice([-1.0, 1.0], size=d)
+            mant = 1.0 + r.integers(0, 128, size=d) / 128.0
+            if R == -1:
+                continue
+            if R == -2:
+                x[i, h] = sign * r.integers(1, 128, size=d) * 2.0 ** -133
+                continue
+            e = r.integers(0, max(R, 0) + 1, size=d)
+            e[0], e[-1] = 0, max(R, 0)
+            if R == -3:
+                e = np.where(r.random(d) < 0.5, 0, 1)
+                x[i, h] = sign * mant * np.where(e == 0, 2.0 ** -130, 1.0)
+                continue
+            x[i, h] = sign * mant * 2.0 ** (e - R // 2 - r.integers(-3, 4))
+    return torch.tensor(x, dtype=torch.float64).to(torch.bfloat16).unsqueeze(0)
+
+
+@pytest.mark.parametrize("hi", [1, 4, 8])
+@pytest.mark.parametrize("causal", [False, True])
+def test_indexer_limb_exponent_ranges(dev, hi, causal):
+    """The integer-limb score path (bf16, d = 64) at every branch of its
+    exactness rule, bit for bit against the oracle's sequential fp64 sums:
+    16-row blocks whose rows all have R <= 14 (three limbs a side) next to
+    blocks of R 15-22 (four limbs), query/key pairs with Rq + Rk <= 30 and
+    pairs above it (the sequential sum), rows with R > 22, subnormal rows,
+    all-zero rows and mixed signs; rows are ranked in full (k = Tk), so a
+    wrong score of any key moves it."""
+    Tq, Tk = 160, 192
+    narrow = [0, 3, 7, 10, 14]
+    wide = [15, 16, 18, 20, 22]
+    odd = [23, 30, -1, -2, -3, 14, 9]
+    q = torch.cat([limb_rows(64, hi, 64, narrow, seed=11),
+                   limb_rows(64, hi, 64, wide + narrow, seed=12),
+                   limb_rows(32, hi, 64, odd, seed=13)], dim=1)
+    k = torch.cat([limb_rows(64, hi, 64, wide, seed=14),
+                   limb_rows(64, hi, 64, narrow, seed=15),
+                   limb_rows(64, hi, 64, odd + narrow, seed=16)], dim=1)
+    w = torch.rand(1, Tq, hi, generator=torch.Generator().manual_seed(17))
+    check(q, k, w, Tk, dev, causal=causal, offset=Tk - Tq if causal else 0)
+
+
 def test_config2_indexer_full_size(dev):
     """C2: B=1, T=8192, 4 heads of dim 64, bf16 q/k, w ~ U(0,1), causal top-2048,
     int32 indices.  Every one of the 8192 rows against the oracle bit for bit
