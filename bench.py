@@ -351,7 +351,10 @@ def bench_c2(dev, steps, warmup, keep=None):
     return {"workload": "C2 indexer top-2048, causal, T=8192, 4x64 heads, bf16",
             "queries_per_s": round(T / (ms * 1e-3), 1), "ms": round(ms, 4),
             "score_tflops_fp64": round(tflops, 2),
-            "frac_fp64_valu_peak": round(tflops / FP64_VALU_PEAK_TFLOPS, 4)}
+            "frac_fp64_valu_peak": round(tflops / FP64_VALU_PEAK_TFLOPS, 4),
+            "note": "score_tflops_fp64: the exact fp64 q.k product work (512 FLOP per causal "
+                    "pair) over the whole call, scores and top-k; bf16 scores are computed "
+                    "exactly as int8 limb products on the matrix cores"}
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, AMD public spec
