@@ -443,7 +443,10 @@ __global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 3 : 1) void topk_re
   // the scores of the (single) row of the sorted form
   const double *rp_row = p.scores + ((rw.br / p.Tq) * p.G * p.Tq + rw.tl) * p.row_stride + rw.seg0;
 
-  for (int64_t g = 0; g < p.G; ++g) {
+  // the sorted form has one row per group (bitmap rows take the GQA groups):
+  // no loop there, so nothing of the row's loads is kept across iterations
+  const int64_t n_groups = BITMAP ? p.G : 1;
+  for (int64_t g = 0; g < n_groups; ++g) {
     const int64_t row = ((rw.br / p.Tq) * p.G + g) * p.Tq + rw.tl;
     const double *rp = p.scores + row * p.row_stride + rw.seg0;
     // raw fp64 bits, mapped in place to order keys (ord_key: -0 reads as +0)
