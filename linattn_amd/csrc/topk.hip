@@ -408,11 +408,13 @@ __device__ __forceinline__ void tk_bitonic_desc(uint64_t (&c)[E], int tid, uint6
 // (key desc, index asc) with a bitonic network over E registers per thread:
 // partners in the same thread are swapped in place, in other lanes of the
 // wave they are exchanged by shuffles, in other waves through LDS.
-// Sorted rows of the longest kind (KPT 32: the indexer's) are held to three
-// waves per SIMD (168 registers, two of them spilled): their steps are short
-// and barrier-bound, so a third resident workgroup per CU pays.
+// Sorted rows of the longest kind (KPT 32: the indexer's) are held to four
+// waves per SIMD (128 registers, 16 of them spilled; 40 KiB of LDS each, so
+// four workgroups fill a CU's LDS): their steps are short and barrier-bound,
+// so every further resident workgroup per CU pays (two: +22 %, three: +2 %
+// on the C2 top-k against four).
 template <int KPT, int E, bool BITMAP>
-__global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 3 : 1) void topk_reg_kernel(TopkKParams p) {
+__global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 4 : 1) void topk_reg_kernel(TopkKParams p) {
   constexpr int P = TK_NT * E;  // sort width (sorted form)
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ TkRegShared<KPT> sr;
