@@ -344,15 +344,30 @@ constexpr int LM_NOLIMB = 255;
 // Sixteen lanes per (batch, row, head): lane j converts elements 4 j .. 4 j + 3
 // and stores their limbs as one 4-byte word per limb.  Rows past n (the
 // padding of the last 64-row tile) get zero limbs.
-__global__ __launch_bounds__(256) void indexer_limb_kernel(const uint16_t *src, int64_t sb, int64_t st,
-                                                           int64_t sh, int64_t r0, int64_t n,
-                                                           int64_t n_pad, int64_t HI, int8_t *limbs,
-                                                           int32_t *xw) {
-  const int64_t gt = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// One launch converts two runs of rows (k and the first query chunk): the
+// first blocks_a workgroups take run a, the rest run b.
+struct LimbRun {
+  const uint16_t *src;
+  int64_t sb, st, sh, r0, n, n_pad;
+  int8_t *limbs;
+  int32_t *xw;
+};
+__global__ __launch_bounds__(256) void indexer_limb_kernel(LimbRun ra, LimbRun rb, int64_t HI,
+                                                           uint32_t blocks_a) {
+  const bool in_a = blockIdx.x < blocks_a;
+  const LimbRun &r = in_a ? ra : rb;
+  const uint16_t *src = r.src;
+  const int64_t sb = r.sb, st = r.st, sh = r.sh, r0 = r.r0, n = r.n, n_pad = r.n_pad;
+  int8_t *limbs = r.limbs;
+  int32_t *xw = r.xw;
+  const uint32_t blk_x = in_a ? blockIdx.x : blockIdx.x - blocks_a;
+  // a wave takes 4 consecutive rows of one head, so that its limb stores
+  // fill 64-byte runs of one block
+  const int64_t gt = (int64_t)blk_x * 256 + threadIdx.x;
   const int j = (int)(gt & 15);
   const int64_t rh = gt >> 4;
-  const int64_t h = rh % HI, rr = rh / HI;
-  const int64_t row = rr % n_pad, b = rr / n_pad;
+  const int64_t r4 = rh >> 2, h = r4 % HI, rq = r4 / HI;
+  const int64_t row = (rq % (n_pad / 4)) * 4 + (rh & 3), b = rq / (n_pad / 4);
   uint2 raw = make_uint2(0u, 0u);
   if (row < n) raw = *(const uint2 *)(src + b * sb + (r0 + row) * st + h * sh + 4 * j);
   const uint32_t xs[4] = {raw.x & 0xffffu, raw.x >> 16, raw.y & 0xffffu, raw.y >> 16};
@@ -1090,11 +1105,10 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
     lq = lk + a->B * nkb * a->HI * 4096;
     xk = (int32_t *)(lq + a->B * nqb * a->HI * 4096);
     xq = xk + a->B * nkb * 16 * a->HI;
-    const int64_t groups = a->B * nkb * 16 * a->HI;  // 16 lanes each
-    indexer_limb_kernel<<<dim3((unsigned)(groups / 16)), 256, 0, st>>>(
-        (const uint16_t *)a->kk, a->k_sb, a->k_st, a->k_sh, 0, a->Tk, nkb * 16, a->HI, lk, xk);
-    LA_LAUNCHED();
   }
+  // k's limbs go with the first query chunk's, in one launch
+  const LimbRun run_k{(const uint16_t *)a->kk, a->k_sb, a->k_st, a->k_sh, 0, a->Tk, nkb * 16, lk, xk};
+  const uint32_t blocks_k = (uint32_t)(a->B * nkb * 16 * a->HI / 16);  // 16 lanes per (row, head)
   for (int64_t t0 = 0; t0 < a->Tq; t0 += chunk) {
     IdxKP p{};
     p.q = a->q;
@@ -1147,9 +1161,12 @@ extern "C" int la_indexer_topk(const la_indexer_args *a, void *stream) {
       const dim3 grid_m((unsigned)ceil_div(a->Tk, IM_K), (unsigned)ceil_div(p.tn, IT_Q),
                         (unsigned)a->B);
       if (limbs) {
-        const int64_t groups = a->B * nqb * 16 * a->HI;  // 16 lanes each
-        indexer_limb_kernel<<<dim3((unsigned)(groups / 16)), 256, 0, st>>>(
-            (const uint16_t *)a->q, a->q_sb, a->q_st, a->q_sh, t0, p.tn, nqb * 16, a->HI, lq, xq);
+        const LimbRun run_q{(const uint16_t *)a->q, a->q_sb, a->q_st, a->q_sh, t0, p.tn, nqb * 16, lq, xq};
+        const uint32_t blocks_q = (uint32_t)(a->B * nqb * 16 * a->HI / 16);
+        if (t0 == 0)
+          indexer_limb_kernel<<<dim3(blocks_k + blocks_q), 256, 0, st>>>(run_k, run_q, a->HI, blocks_k);
+        else
+          indexer_limb_kernel<<<dim3(blocks_q), 256, 0, st>>>(run_q, run_q, a->HI, blocks_q);
         LA_LAUNCHED();
         p.lq = lq;
         p.lk = lk;
