@@ -691,8 +691,10 @@ __global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 4 : 1) void topk_re
       const int64_t kw = min((int64_t)K, p.width);
       for (int64_t jj = tid; jj < p.width; jj += TK_NT) {
         const uint64_t x = jj < kw ? skey[jj] : 0xff800000ffffffffull;  // -1, -inf past K
-        oi[jj] = (int32_t)(uint32_t)x;
-        if (p.out_val) p.out_val[rw.orow * p.width + jj] = __uint_as_float((uint32_t)(x >> 32));
+        // streamed out (nontemporal): the lists are not read again here
+        __builtin_nontemporal_store((int32_t)(uint32_t)x, oi + jj);
+        if (p.out_val)
+          __builtin_nontemporal_store(__uint_as_float((uint32_t)(x >> 32)), p.out_val + rw.orow * p.width + jj);
       }
       __syncthreads();
       if (p.out_count && tid == 0) p.out_count[rw.orow] = (int32_t)s_first_pad;
