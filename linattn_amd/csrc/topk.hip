@@ -457,7 +457,7 @@ __global__ __launch_bounds__(TK_NT, (!BITMAP && KPT >= 32) ? 4 : 1) void topk_re
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       const int32_t i = tid + TK_NT * j;
-      u[j] = i < n_v ? rb[i] : 0ull;
+      u[j] = i < n_v ? __builtin_nontemporal_load(rb + i) : 0ull;  // read once
     }
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
