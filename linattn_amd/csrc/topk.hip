@@ -25,7 +25,7 @@ constexpr int TK_BATCH = 8;  // keys read per thread before they are used
 constexpr int TKB_BITS = 11, TKB_N = 1 << TKB_BITS, TKB_PT = 9, TKB_S = TKB_PT * 256;
 constexpr int TKB_MAX = 256;
 // undecided keys the bitwise search copies to LDS once that few remain
-constexpr int TK_CAND_CAP = 256;
+constexpr int TK_CAND_CAP = 128;
 
 struct TkShared {
   uint32_t hist[256];

@@ -8,7 +8,7 @@
 namespace la {
 
 constexpr int TK_NT = 256;  // threads of a selecting workgroup
-constexpr int TK_CAND_REGS = 4;  // keys per lane of the one-wave finish
+constexpr int TK_CAND_REGS = 2;  // keys per lane of the one-wave finish
 constexpr int TK_NW = TK_NT / 64;
 
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) {
